@@ -1,0 +1,934 @@
+// The 128-column block loop of BRAGPTQ.fasterquant (bigptq.py:131-264) on
+// gfx950: salient-column search, bell-shaped split, binarization, Err/Loss
+// and the GPTQ trailing update.
+//
+// Search of one block (utils/structure.py:8-20 -> utils/autosearch.py:28-83
+// -> utils/mask.py:7-18), all on the device with no host round trip:
+//   k_colscore   column scores sum_r |T| (fp64 per-workgroup partials)
+//   k_topk       ranks of the columns by score (torch.topk order)
+//   k_phase_a    one lane per (row, salient candidate i): order-2 residual
+//                binarization error of {top i cols} + complement
+//   k_reduce_a   i* = first strict minimum over candidates
+//   k_qpass/k_qscan (x3)
+//                exact np.quantile of |T * ~M3| at the 81 float32
+//                percentiles: 3-level MSD radix select (12/10/10 bits of the
+//                non-negative float's bit pattern) of the 162 order
+//                statistics, then numpy's float32 index/lerp arithmetic
+//   k_phase_c    one lane per (row, split candidate k): order-1 errors of the
+//                two bell groups
+//   k_reduce_c   k* = first strict minimum, split = p[k*]
+//   k_quantize   one wavefront per row: masks, binarization per group,
+//                Q, Err = (w-q)/d, Loss = (w-q)^2/d^2
+// then sgemm_launch for W[:, ed:] -= Err @ U[st:ed, ed:].
+//
+// T = W^2 / diag(U_blk)^2 (hessian metric) or W (magnitude) is recomputed
+// from W on every pass instead of being stored.
+#include "binarize.h"
+#include "gemm_f32.h"
+
+namespace crbq {
+
+constexpr int NQ = 81;       // percentiles linspace(0.10, 0.90, 81)
+constexpr int NT = 2 * NQ;   // order statistics needed (lo, hi per percentile)
+constexpr int NCMAX = 128;   // widest block
+constexpr int UPMAX = 64;    // largest supported up_lim
+constexpr int CS_RPW = 32;   // rows per workgroup in k_colscore
+constexpr int Q_RPW = 16;    // rows per workgroup in the quantile passes
+constexpr int PA_RPW = 13;   // rows per workgroup in phase A (13*49 = 637 items)
+constexpr int PC_RPW = 7;    // rows per workgroup in phase C (7*81 = 567 items)
+constexpr int PX_THREADS = 128;
+constexpr int H1_BITS = 12, H2_BITS = 10, H3_BITS = 10;   // 12 + 10 + 10 = 32
+constexpr int H1 = 1 << H1_BITS, H2 = 1 << H2_BITS, H3 = 1 << H3_BITS;
+constexpr int SH1 = H2_BITS + H3_BITS, SH2 = H3_BITS;     // key = b1<<SH1 | b2<<SH2 | b3
+constexpr int NONE = 0x7fffffff;
+
+// torch.linspace(0.10, 0.90, 81) on the CPU (utils/autosearch.py:65), float32.
+__constant__ float c_q[NQ];
+
+struct Ctrl {        // small per-block control record (device)
+  int istar;
+  int kstar;
+  int ncand_a;
+  int pad;
+  float split;
+};
+
+struct Tgt {         // one order statistic being selected
+  int64_t rank;      // absolute rank in the sorted flattened block
+  int bin1, r1;      // level-1 bin and rank within it
+  int slot1;         // leader target index of bin1
+  int bin2, r2;
+  int bin3;
+};
+
+struct SearchWs {
+  double* colpart;   // [nwg_cs][NCMAX]
+  int* rank;         // [NCMAX]
+  Ctrl* ctrl;
+  double* parta;     // [nwg_a][UPMAX]
+  double* partc;     // [nwg_c][96]
+  uint32_t* hist1;   // [H1]
+  int* slot1map;     // [H1]
+  Tgt* tgt;          // [NT]
+  float* gam;        // [NQ]
+  uint32_t* hist2;   // [NT][H2]
+  int* slot2map;     // [NT][H2]
+  uint32_t* hist3;   // [NT][H3]
+  float* tval;       // [NT]
+  float* pvals;      // [NQ]
+};
+
+static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+static void carve_search(WsCarver& c, int64_t R, SearchWs& s) {
+  s.colpart = c.take<double>((size_t)cdiv(R, CS_RPW) * NCMAX);
+  s.rank = c.take<int>(NCMAX);
+  s.ctrl = c.take<Ctrl>(1);
+  s.parta = c.take<double>((size_t)cdiv(R, PA_RPW) * UPMAX);
+  s.partc = c.take<double>((size_t)cdiv(R, PC_RPW) * 96);
+  s.hist1 = c.take<uint32_t>(H1);
+  s.slot1map = c.take<int>(H1);
+  s.tgt = c.take<Tgt>(NT);
+  s.gam = c.take<float>(NQ);
+  s.hist2 = c.take<uint32_t>((size_t)NT * H2);
+  s.slot2map = c.take<int>((size_t)NT * H2);
+  s.hist3 = c.take<uint32_t>((size_t)NT * H3);
+  s.tval = c.take<float>(NT);
+  s.pvals = c.take<float>(NQ);
+}
+
+// Salient-search target T (utils/structure.py:9-12).
+__device__ __forceinline__ float target_of(float w, float d2, int metric) {
+  if (metric == CRBQ_METRIC_HESSIAN) {
+    const float w2 = w * w;
+    return w2 / d2;
+  }
+  return w;
+}
+
+// ---------------------------------------------------------------------------
+// column scores + zeroing of the selection histograms for this block
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_colscore(
+    const float* __restrict__ W, int64_t ldw, int R, int nc,
+    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
+  __shared__ double part[2][NCMAX];
+  const int tid = threadIdx.x, col = tid & (NCMAX - 1), ph = tid >> 7;
+  const int r0 = blockIdx.x * CS_RPW, r1 = min(R, r0 + CS_RPW);
+  double acc = 0.0;
+  if (col < nc) {
+    const float dg = U[(int64_t)col * ldu + col];
+    const float d2 = dg * dg;
+    for (int r = r0 + ph; r < r1; r += 2)
+      acc += (double)fabsf(target_of(W[(int64_t)r * ldw + col], d2, metric));
+  }
+  part[ph][col] = acc;
+  __syncthreads();
+  if (ph == 0) s.colpart[(size_t)blockIdx.x * NCMAX + col] = part[0][col] + part[1][col];
+  // zero the histograms used later by this block (grid-stride)
+  const size_t gsz = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)NT * H2; i += gsz) {
+    s.hist2[i] = 0u;
+    s.hist3[i] = 0u;
+  }
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)H1; i += gsz) s.hist1[i] = 0u;
+}
+
+// ranks of the columns by descending score (ties: lower column first)
+__global__ __launch_bounds__(NCMAX) void k_topk(int nc, int nwg, SearchWs s) {
+  __shared__ double sc[NCMAX];
+  const int c = threadIdx.x;
+  double v = 0.0;
+  if (c < nc)
+    for (int g = 0; g < nwg; ++g) v += s.colpart[(size_t)g * NCMAX + c];
+  sc[c] = v;
+  __syncthreads();
+  int r = NCMAX;
+  if (c < nc) {
+    r = 0;
+    for (int k = 0; k < nc; ++k) r += (sc[k] > v) || (sc[k] == v && k < c);
+  }
+  s.rank[c] = r;
+}
+
+// ---------------------------------------------------------------------------
+// phase A: error of order-2 residual binarization of {rank < i} and its
+// complement, for candidates i = 1..up_lim-1 (utils/autosearch.py:44-55)
+// ---------------------------------------------------------------------------
+__device__ double phase_a_item(const float* __restrict__ x, const int* __restrict__ rk,
+                               int nc, int i) {
+  const float nS = (float)i, nC = (float)(nc - i);
+  double sS = 0.0, sC = 0.0;
+  for (int c = 0; c < nc; ++c) {
+    const double v = (double)x[c];
+    const bool in = rk[c] < i;
+    sS += in ? v : 0.0;
+    sC += in ? 0.0 : v;
+  }
+  const float m1S = nS > 0.f ? (float)sS / nS : 0.f;
+  const float m1C = nC > 0.f ? (float)sC / nC : 0.f;
+  sS = 0.0; sC = 0.0;
+  for (int c = 0; c < nc; ++c) {
+    const bool in = rk[c] < i;
+    const double a = (double)fabsf(x[c] - (in ? m1S : m1C));
+    sS += in ? a : 0.0;
+    sC += in ? 0.0 : a;
+  }
+  const float a1S = nS > 0.f ? (float)sS / nS : 0.f;
+  const float a1C = nC > 0.f ? (float)sC / nC : 0.f;
+  sS = 0.0; sC = 0.0;
+  for (int c = 0; c < nc; ++c) {
+    const bool in = rk[c] < i;
+    const float m = in ? m1S : m1C, a = in ? a1S : a1C;
+    const float cc = x[c] - m;
+    float s1 = tsign(cc) * a;
+    s1 = s1 + m;
+    const double r = (double)(x[c] - s1);
+    sS += in ? r : 0.0;
+    sC += in ? 0.0 : r;
+  }
+  const float m2S = nS > 0.f ? (float)sS / nS : 0.f;
+  const float m2C = nC > 0.f ? (float)sC / nC : 0.f;
+  sS = 0.0; sC = 0.0;
+  for (int c = 0; c < nc; ++c) {
+    const bool in = rk[c] < i;
+    const float m = in ? m1S : m1C, a = in ? a1S : a1C, m2 = in ? m2S : m2C;
+    const float cc = x[c] - m;
+    float s1 = tsign(cc) * a;
+    s1 = s1 + m;
+    const float r = x[c] - s1;
+    const double a2 = (double)fabsf(r - m2);
+    sS += in ? a2 : 0.0;
+    sC += in ? 0.0 : a2;
+  }
+  const float a2S = nS > 0.f ? (float)sS / nS : 0.f;
+  const float a2C = nC > 0.f ? (float)sC / nC : 0.f;
+  double err = 0.0;
+  for (int c = 0; c < nc; ++c) {
+    const bool in = rk[c] < i;
+    const float m = in ? m1S : m1C, a = in ? a1S : a1C;
+    const float m2 = in ? m2S : m2C, a2 = in ? a2S : a2C;
+    const float cc = x[c] - m;
+    float s1 = tsign(cc) * a;
+    s1 = s1 + m;
+    const float r = x[c] - s1;
+    const float c2 = r - m2;
+    float s2 = tsign(c2) * a2;
+    s2 = s2 + m2;
+    const float tot = s1 + s2;
+    const float df = x[c] - tot;
+    err += (double)(df * df);
+  }
+  return err;
+}
+
+__global__ __launch_bounds__(PX_THREADS) void k_phase_a(
+    const float* __restrict__ W, int64_t ldw, int R, int nc,
+    const float* __restrict__ U, int64_t ldu, int metric, int ncand, SearchWs s) {
+  __shared__ float xs[PA_RPW][NCMAX];
+  __shared__ int rk[NCMAX];
+  __shared__ double errs[PA_RPW][UPMAX];
+  const int tid = threadIdx.x;
+  const int r0 = blockIdx.x * PA_RPW, nr = min(PA_RPW, R - r0);
+  for (int i = tid; i < NCMAX; i += PX_THREADS) rk[i] = s.rank[i];
+  for (int i = tid; i < PA_RPW * NCMAX; i += PX_THREADS) {
+    const int rr = i / NCMAX, c = i % NCMAX;
+    float v = 0.f;
+    if (rr < nr && c < nc) {
+      const float dg = U[(int64_t)c * ldu + c];
+      v = target_of(W[(int64_t)(r0 + rr) * ldw + c], dg * dg, metric);
+    }
+    xs[rr][c] = v;
+  }
+  __syncthreads();
+  const int items = nr * ncand;
+  for (int it = tid; it < items; it += PX_THREADS) {
+    const int rr = it / ncand, ci = it % ncand;
+    errs[rr][ci] = phase_a_item(xs[rr], rk, nc, ci + 1);
+  }
+  __syncthreads();
+  for (int ci = tid; ci < ncand; ci += PX_THREADS) {
+    double e = 0.0;
+    for (int rr = 0; rr < nr; ++rr) e += errs[rr][ci];
+    s.parta[(size_t)blockIdx.x * UPMAX + ci] = e;
+  }
+}
+
+__global__ __launch_bounds__(UPMAX) void k_reduce_a(int nwg, int ncand, int up_lim,
+                                                    SearchWs s, crbq_block_trace* tr) {
+  __shared__ double e[UPMAX];
+  const int c = threadIdx.x;
+  if (c < ncand) {
+    double v = 0.0;
+    for (int g = 0; g < nwg; ++g) v += s.parta[(size_t)g * UPMAX + c];
+    e[c] = v;
+  }
+  __syncthreads();
+  if (c == 0) {
+    double best = INFINITY;
+    int istar = max(1, up_lim / 3);                                  // :43
+    for (int k = 0; k < ncand; ++k)
+      if (e[k] < best) { best = e[k]; istar = k + 1; }
+    s.ctrl->istar = istar;
+    if (tr) tr->i_star = istar;
+  }
+  if (tr) {
+    if (c < ncand) tr->errs_a[c + 1] = e[c];
+    if (c == 0) tr->errs_a[0] = 0.0;
+    if (c > ncand && c < UPMAX) tr->errs_a[c] = 0.0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// exact float32 np.quantile of S = |T * ~M3| (utils/autosearch.py:62-68)
+// ---------------------------------------------------------------------------
+// Level-1: histogram of bits [31:20] of the (non-negative) float pattern.
+__global__ __launch_bounds__(256) void k_qpass1(
+    const float* __restrict__ W, int64_t ldw, int R, int nc,
+    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
+  __shared__ uint32_t lh[H1];
+  __shared__ float d2s[NCMAX];
+  __shared__ int rk[NCMAX];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < H1; i += 256) lh[i] = 0u;
+  const int istar = s.ctrl->istar;
+  for (int c = tid; c < NCMAX; c += 256) {
+    rk[c] = s.rank[c];
+    if (c < nc) { const float dg = U[(int64_t)c * ldu + c]; d2s[c] = dg * dg; }
+  }
+  __syncthreads();
+  const int r0 = blockIdx.x * Q_RPW, r1 = min(R, r0 + Q_RPW);
+  for (int i = tid; i < (r1 - r0) * nc; i += 256) {
+    const int r = r0 + i / nc, c = i % nc;
+    if (rk[c] < istar) continue;           // M3 zeros are counted below
+    const float v = fabsf(target_of(W[(int64_t)r * ldw + c], d2s[c], metric));
+    atomicAdd(&lh[__float_as_uint(v) >> SH1], 1u);
+  }
+  __syncthreads();
+  for (int i = tid; i < H1; i += 256)
+    if (lh[i]) atomicAdd(&s.hist1[i], lh[i]);
+  if (blockIdx.x == 0 && tid == 0) {
+    int nsal = 0;
+    for (int c = 0; c < nc; ++c) nsal += rk[c] < istar;
+    if (nsal) atomicAdd(&s.hist1[0], (uint32_t)R * (uint32_t)nsal);
+  }
+}
+
+// Block-wide exclusive scan of H (multiple of 256) counters in LDS.
+template <int H>
+__device__ void block_scan(const uint32_t* __restrict__ src, uint32_t* cum,
+                           uint32_t* tmp /* 256 */) {
+  constexpr int PER = H / 256;
+  const int tid = threadIdx.x;
+  uint32_t loc[PER];
+  uint32_t sum = 0;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) { loc[k] = src[tid * PER + k]; sum += loc[k]; }
+  tmp[tid] = sum;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {
+    const uint32_t v = tid >= o ? tmp[tid - o] : 0u;
+    __syncthreads();
+    tmp[tid] += v;
+    __syncthreads();
+  }
+  uint32_t run = tmp[tid] - sum;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) { cum[tid * PER + k] = run; run += loc[k]; }
+  __syncthreads();
+}
+
+// Find b with cum[b] <= r < cum[b+1] (cum exclusive, H entries, total n).
+template <int H>
+__device__ __forceinline__ int find_bin(const uint32_t* cum, uint32_t r) {
+  int lo = 0, hi = H - 1;
+  while (lo < hi) {                 // last b with cum[b] <= r
+    const int mid = (lo + hi + 1) >> 1;
+    if (cum[mid] <= r) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(256) void k_qscan1(int64_t n, SearchWs s) {
+  __shared__ uint32_t cum[H1];
+  __shared__ uint32_t tmp[256];
+  __shared__ int lead[H1];
+  const int tid = threadIdx.x;
+  block_scan<H1>(s.hist1, cum, tmp);
+  for (int i = tid; i < H1; i += 256) lead[i] = NONE;
+  __syncthreads();
+  if (tid < NQ) {
+    // numpy 'linear': virtual index (n-1)*q in float32, floor, fractional gamma
+    const float vi = (float)(n - 1) * c_q[tid];
+    int64_t lo, hi;
+    float g;
+    if (vi >= (float)(n - 1)) { lo = hi = n - 1; g = 0.f; }
+    else {
+      const float fl = floorf(vi);
+      lo = (int64_t)fl; hi = lo + 1; g = vi - fl;
+    }
+    s.gam[tid] = g;
+    s.tgt[2 * tid].rank = lo;
+    s.tgt[2 * tid + 1].rank = hi;
+  }
+  __syncthreads();
+  if (tid < NT) {
+    Tgt& t = s.tgt[tid];
+    const uint32_t r = (uint32_t)t.rank;
+    const int b = find_bin<H1>(cum, r);
+    t.bin1 = b;
+    t.r1 = (int)(r - cum[b]);
+    atomicMin(&lead[b], tid);
+  }
+  __syncthreads();
+  for (int i = tid; i < H1; i += 256) s.slot1map[i] = lead[i] == NONE ? -1 : lead[i];
+  if (tid < NT) s.tgt[tid].slot1 = lead[s.tgt[tid].bin1];
+}
+
+// Level-2: bits [19:10] of elements whose level-1 bin holds a target.
+__global__ __launch_bounds__(256) void k_qpass2(
+    const float* __restrict__ W, int64_t ldw, int R, int nc,
+    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
+  __shared__ int sm[H1];
+  __shared__ float d2s[NCMAX];
+  __shared__ int rk[NCMAX];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < H1; i += 256) sm[i] = s.slot1map[i];
+  const int istar = s.ctrl->istar;
+  for (int c = tid; c < NCMAX; c += 256) {
+    rk[c] = s.rank[c];
+    if (c < nc) { const float dg = U[(int64_t)c * ldu + c]; d2s[c] = dg * dg; }
+  }
+  // reset the level-2 leader map (read by k_qscan2 / k_qpass3 only)
+  const size_t gsz = (size_t)gridDim.x * 256;
+  for (size_t i = (size_t)blockIdx.x * 256 + tid; i < (size_t)NT * H2; i += gsz)
+    s.slot2map[i] = NONE;
+  __syncthreads();
+  const int r0 = blockIdx.x * Q_RPW, r1 = min(R, r0 + Q_RPW);
+  for (int i = tid; i < (r1 - r0) * nc; i += 256) {
+    const int r = r0 + i / nc, c = i % nc;
+    if (rk[c] < istar) continue;
+    const float v = fabsf(target_of(W[(int64_t)r * ldw + c], d2s[c], metric));
+    const uint32_t key = __float_as_uint(v);
+    const int sl = sm[key >> SH1];
+    if (sl >= 0) atomicAdd(&s.hist2[(size_t)sl * H2 + ((key >> SH2) & (H2 - 1))], 1u);
+  }
+  if (blockIdx.x == 0 && tid == 0 && sm[0] >= 0) {
+    int nsal = 0;
+    for (int c = 0; c < nc; ++c) nsal += rk[c] < istar;
+    if (nsal) atomicAdd(&s.hist2[(size_t)sm[0] * H2], (uint32_t)R * (uint32_t)nsal);
+  }
+}
+
+// one workgroup per target: resolve its level-2 bin; elect level-2 leaders
+__global__ __launch_bounds__(256) void k_qscan2(SearchWs s) {
+  __shared__ uint32_t cum[H2];
+  __shared__ uint32_t tmp[256];
+  const int t = blockIdx.x;
+  const int sl = s.tgt[t].slot1;
+  block_scan<H2>(s.hist2 + (size_t)sl * H2, cum, tmp);
+  if (threadIdx.x == 0) {
+    Tgt& g = s.tgt[t];
+    const int b = find_bin<H2>(cum, (uint32_t)g.r1);
+    g.bin2 = b;
+    g.r2 = (int)((uint32_t)g.r1 - cum[b]);
+    atomicMin(&s.slot2map[(size_t)sl * H2 + b], t);
+  }
+}
+
+// Level-3: bits [9:0] of elements whose (level-1, level-2) prefix holds a target.
+__global__ __launch_bounds__(256) void k_qpass3(
+    const float* __restrict__ W, int64_t ldw, int R, int nc,
+    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
+  __shared__ int sm[H1];
+  __shared__ float d2s[NCMAX];
+  __shared__ int rk[NCMAX];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < H1; i += 256) sm[i] = s.slot1map[i];
+  const int istar = s.ctrl->istar;
+  for (int c = tid; c < NCMAX; c += 256) {
+    rk[c] = s.rank[c];
+    if (c < nc) { const float dg = U[(int64_t)c * ldu + c]; d2s[c] = dg * dg; }
+  }
+  __syncthreads();
+  const int r0 = blockIdx.x * Q_RPW, r1 = min(R, r0 + Q_RPW);
+  for (int i = tid; i < (r1 - r0) * nc; i += 256) {
+    const int r = r0 + i / nc, c = i % nc;
+    if (rk[c] < istar) continue;
+    const float v = fabsf(target_of(W[(int64_t)r * ldw + c], d2s[c], metric));
+    const uint32_t key = __float_as_uint(v);
+    const int sl = sm[key >> SH1];
+    if (sl < 0) continue;
+    const int l2 = s.slot2map[(size_t)sl * H2 + ((key >> SH2) & (H2 - 1))];
+    if (l2 != NONE) atomicAdd(&s.hist3[(size_t)l2 * H3 + (key & (H3 - 1))], 1u);
+  }
+  if (blockIdx.x == 0 && tid == 0 && sm[0] >= 0) {
+    const int l2 = s.slot2map[(size_t)sm[0] * H2];
+    int nsal = 0;
+    for (int c = 0; c < nc; ++c) nsal += rk[c] < istar;
+    if (l2 != NONE && nsal) atomicAdd(&s.hist3[(size_t)l2 * H3], (uint32_t)R * (uint32_t)nsal);
+  }
+}
+
+__global__ __launch_bounds__(256) void k_qscan3(SearchWs s) {
+  __shared__ uint32_t cum[H3];
+  __shared__ uint32_t tmp[256];
+  const int t = blockIdx.x;
+  const Tgt g = s.tgt[t];
+  const int l2 = s.slot2map[(size_t)g.slot1 * H2 + g.bin2];
+  block_scan<H3>(s.hist3 + (size_t)l2 * H3, cum, tmp);
+  if (threadIdx.x == 0) {
+    const int b = find_bin<H3>(cum, (uint32_t)g.r2);
+    s.tgt[t].bin3 = b;
+    const uint32_t key = ((uint32_t)g.bin1 << SH1) | ((uint32_t)g.bin2 << SH2) | (uint32_t)b;
+    s.tval[t] = __uint_as_float(key);
+  }
+}
+
+// numpy _lerp in float32 (numpy/lib/_function_base_impl.py)
+__device__ __forceinline__ float np_lerp(float a, float b, float t) {
+  const float diff = b - a;
+  float r = diff * t;
+  r = a + r;
+  if (t >= 0.5f) {
+    const float omt = 1.f - t;
+    float q = diff * omt;
+    r = b - q;
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// phase C: order-1 errors of the two bell groups for each of the 81 split
+// candidates (utils/autosearch.py:71-80)
+// ---------------------------------------------------------------------------
+__device__ double phase_c_item(const float* __restrict__ x, const bool* __restrict__ sal,
+                               int nc, float thr) {
+  double s1 = 0.0, s2 = 0.0;
+  float n1 = 0.f, n2 = 0.f;
+  for (int c = 0; c < nc; ++c) {
+    if (sal[c]) continue;
+    const float v = x[c];
+    const bool g2 = fabsf(v) >= thr;
+    s1 += g2 ? 0.0 : (double)v;
+    s2 += g2 ? (double)v : 0.0;
+    n1 += g2 ? 0.f : 1.f;
+    n2 += g2 ? 1.f : 0.f;
+  }
+  const float m1 = n1 > 0.f ? (float)s1 / n1 : 0.f;
+  const float m2 = n2 > 0.f ? (float)s2 / n2 : 0.f;
+  s1 = 0.0; s2 = 0.0;
+  for (int c = 0; c < nc; ++c) {
+    if (sal[c]) continue;
+    const float v = x[c];
+    const bool g2 = fabsf(v) >= thr;
+    const double a = (double)fabsf(v - (g2 ? m2 : m1));
+    s1 += g2 ? 0.0 : a;
+    s2 += g2 ? a : 0.0;
+  }
+  const float a1 = n1 > 0.f ? (float)s1 / n1 : 0.f;
+  const float a2 = n2 > 0.f ? (float)s2 / n2 : 0.f;
+  double err = 0.0;
+  for (int c = 0; c < nc; ++c) {
+    if (sal[c]) continue;
+    const float v = x[c];
+    const bool g2 = fabsf(v) >= thr;
+    const float m = g2 ? m2 : m1, a = g2 ? a2 : a1;
+    const float cc = v - m;
+    float q = tsign(cc) * a;
+    q = q + m;
+    const float df = v - q;
+    err += (double)(df * df);
+  }
+  return err;
+}
+
+__global__ __launch_bounds__(PX_THREADS) void k_phase_c(
+    const float* __restrict__ W, int64_t ldw, int R, int nc,
+    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
+  __shared__ float xs[PC_RPW][NCMAX];
+  __shared__ bool sal[NCMAX];
+  __shared__ float pv[NQ];
+  __shared__ double errs[PC_RPW][NQ];
+  const int tid = threadIdx.x;
+  const int r0 = blockIdx.x * PC_RPW, nr = min(PC_RPW, R - r0);
+  const int istar = s.ctrl->istar;
+  for (int i = tid; i < NCMAX; i += PX_THREADS) sal[i] = s.rank[i] < istar;
+  for (int k = tid; k < NQ; k += PX_THREADS) {
+    pv[k] = np_lerp(s.tval[2 * k], s.tval[2 * k + 1], s.gam[k]);
+    if (blockIdx.x == 0) s.pvals[k] = pv[k];
+  }
+  for (int i = tid; i < PC_RPW * NCMAX; i += PX_THREADS) {
+    const int rr = i / NCMAX, c = i % NCMAX;
+    float v = 0.f;
+    if (rr < nr && c < nc) {
+      const float dg = U[(int64_t)c * ldu + c];
+      v = target_of(W[(int64_t)(r0 + rr) * ldw + c], dg * dg, metric);
+    }
+    xs[rr][c] = v;
+  }
+  __syncthreads();
+  const int items = nr * NQ;
+  for (int it = tid; it < items; it += PX_THREADS) {
+    const int rr = it / NQ, k = it % NQ;
+    errs[rr][k] = phase_c_item(xs[rr], sal, nc, pv[k]);
+  }
+  __syncthreads();
+  for (int k = tid; k < NQ; k += PX_THREADS) {
+    double e = 0.0;
+    for (int rr = 0; rr < nr; ++rr) e += errs[rr][k];
+    s.partc[(size_t)blockIdx.x * 96 + k] = e;
+  }
+}
+
+__global__ __launch_bounds__(128) void k_reduce_c(int nwg, SearchWs s, crbq_block_trace* tr) {
+  __shared__ double e[NQ];
+  const int k = threadIdx.x;
+  if (k < NQ) {
+    double v = 0.0;
+    for (int g = 0; g < nwg; ++g) v += s.partc[(size_t)g * 96 + k];
+    e[k] = v;
+  }
+  __syncthreads();
+  if (k == 0) {
+    double best = INFINITY;
+    int ks = NQ / 2;                                                 // :71 median
+    for (int j = 0; j < NQ; ++j)
+      if (e[j] < best) { best = e[j]; ks = j; }
+    s.ctrl->kstar = ks;
+    s.ctrl->split = s.pvals[ks];
+    if (tr) { tr->k_star = ks; tr->split = s.pvals[ks]; }
+  }
+  if (tr && k < NQ) { tr->errs_c[k] = e[k]; tr->pvals[k] = s.pvals[k]; }
+}
+
+// ---------------------------------------------------------------------------
+// quantize one block: masks -> binarize per group -> Q, Err, Loss
+// (bigptq.py:235-264, utils/mask.py:7-18)
+// ---------------------------------------------------------------------------
+struct QuantArgs {
+  float* W; int64_t ldw; int R; int nc;
+  const float* U; int64_t ldu;      // U[st, st]
+  int metric; int method; int partition; int orders[3];
+  CrbConsts k;
+  int gptq;                          // 0: RTN (no Err/Loss)
+  float* err; int64_t lde;           // R x nc
+  float* losses;
+  uint8_t* masks; int64_t ldm;       // optional
+};
+
+template <int EPL>
+__global__ __launch_bounds__(256) void k_quantize(QuantArgs a, SearchWs s) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.R) return;
+  const int istar = a.partition == 3 ? s.ctrl->istar : 0;
+  const float split = a.partition == 3 ? s.ctrl->split : 0.f;
+  float x[EPL], dd[EPL];
+  int grp[EPL];
+  bool valid[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int c = lane + 64 * e;
+    valid[e] = c < a.nc;
+    x[e] = valid[e] ? a.W[(int64_t)row * a.ldw + c] : 0.f;
+    dd[e] = valid[e] ? a.U[(int64_t)c * a.ldu + c] : 1.f;
+    int g = -1;
+    if (valid[e]) {
+      if (a.partition != 3) g = 0;
+      else if (s.rank[c] < istar) g = 2;
+      else {
+        const float t = fabsf(target_of(x[e], dd[e] * dd[e], a.metric));
+        g = t >= split ? 1 : 0;
+      }
+    }
+    grp[e] = g;
+  }
+  float q[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) q[e] = 0.f;
+  const int ngroups = a.partition == 3 ? 3 : 1;
+  for (int g = 0; g < ngroups; ++g) {
+    bool m[EPL];
+    bool any = false;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) { m[e] = grp[e] == g; any |= m[e]; }
+    (void)any;
+    float out[EPL];
+    binarize_row<EPL>(a.method, x, m, a.orders[g], a.k, out);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) if (m[e]) q[e] = out[e];
+  }
+  double lsum = 0.0;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    if (!valid[e]) continue;
+    const int c = lane + 64 * e;
+    const float w = x[e], d = dd[e];
+    const float df = w - q[e];
+    if (a.gptq) {
+      const float d2 = d * d;
+      const float l = (df * df) / d2;
+      lsum += (double)l;
+      a.err[(int64_t)row * a.lde + c] = df / d;
+    }
+    a.W[(int64_t)row * a.ldw + c] = q[e];
+    if (a.masks) a.masks[(int64_t)row * a.ldm + c] = (uint8_t)(grp[e] + 1);
+  }
+  if (a.gptq) {
+    const float tot = (float)wave_sum(lsum);
+    if (lane == 0) a.losses[row] = a.losses[row] + tot / 2.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host drivers
+// ---------------------------------------------------------------------------
+static int search_block(const float* W, int64_t ldw, int R, int nc, const float* U,
+                        int64_t ldu, int metric, int up_lim, SearchWs& s,
+                        crbq_block_trace* tr, hipStream_t st) {
+  const int ncand = up_lim - 1;
+  const int nwg_cs = (int)cdiv(R, CS_RPW);
+  const int nwg_q = (int)cdiv(R, Q_RPW);
+  const int nwg_a = (int)cdiv(R, PA_RPW);
+  const int nwg_c = (int)cdiv(R, PC_RPW);
+  k_colscore<<<nwg_cs, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
+  k_topk<<<1, NCMAX, 0, st>>>(nc, nwg_cs, s);
+  k_phase_a<<<nwg_a, PX_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, ncand, s);
+  k_reduce_a<<<1, UPMAX, 0, st>>>(nwg_a, ncand, up_lim, s, tr);
+  k_qpass1<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
+  k_qscan1<<<1, 256, 0, st>>>((int64_t)R * nc, s);
+  k_qpass2<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
+  k_qscan2<<<NT, 256, 0, st>>>(s);
+  k_qpass3<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
+  k_qscan3<<<NT, 256, 0, st>>>(s);
+  k_phase_c<<<nwg_c, PX_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
+  k_reduce_c<<<1, 128, 0, st>>>(nwg_c, s, tr);
+  CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}
+
+static bool q_table_ready = false;
+static int ensure_q_table() {
+  if (q_table_ready) return CRBQ_OK;
+  // torch.linspace(0.10, 0.90, 81) (float32, CPU): start + i*step for the
+  // first half, end - (steps-1-i)*step for the second, step in float32.
+  float q[NQ];
+  const float start = 0.10f, end = 0.90f;
+  const float step = (end - start) / (float)(NQ - 1);
+  const int half = NQ / 2;
+  for (int i = 0; i < NQ; ++i)
+    q[i] = i < half ? start + step * (float)i : end - step * (float)(NQ - 1 - i);
+  CRBQ_HIP(hipMemcpyToSymbol(HIP_SYMBOL(c_q), q, sizeof(q)));
+  q_table_ready = true;
+  return CRBQ_OK;
+}
+
+int set_q_table(const float* q) {
+  CRBQ_HIP(hipMemcpyToSymbol(HIP_SYMBOL(c_q), q, NQ * sizeof(float)));
+  q_table_ready = true;
+  return CRBQ_OK;
+}
+
+static size_t search_ws_bytes(int64_t R) {
+  WsCarver c(nullptr, 0);
+  SearchWs s;
+  carve_search(c, R, s);
+  return c.off + 256;
+}
+
+static int check_params(const crbq_params* p) {
+  if (!p) return CRBQ_ERR_ARG;
+  if (p->blocksize < 1 || p->blocksize > NCMAX) return CRBQ_ERR_ARG;
+  if (p->partition != 1 && p->partition != 3) return CRBQ_ERR_ARG;
+  if (p->method < CRBQ_BRAQ || p->method > CRBQ_CRB_SYMDAMP_NOREFINE) return CRBQ_ERR_ARG;
+  if (p->metric != CRBQ_METRIC_HESSIAN && p->metric != CRBQ_METRIC_MAGNITUDE) return CRBQ_ERR_ARG;
+  if (p->partition == 3 && (p->up_lim < 2 || p->up_lim > UPMAX)) return CRBQ_ERR_ARG;
+  for (int g = 0; g < 3; ++g) if (p->orders[g] < 1 || p->orders[g] > 8) return CRBQ_ERR_ARG;
+  if (p->refine_iters < 0 || p->refine_iters > 64) return CRBQ_ERR_ARG;
+  return CRBQ_OK;
+}
+
+}  // namespace crbq
+
+using namespace crbq;
+
+extern "C" size_t crbq_block_search_workspace_size(int64_t R, int32_t up_lim) {
+  (void)up_lim;
+  return search_ws_bytes(R);
+}
+
+namespace crbq {
+__global__ __launch_bounds__(256) void k_emit_masks(const float* __restrict__ W, int64_t ldw,
+                                                    int R, int nc, const float* __restrict__ U,
+                                                    int64_t ldu, int metric, uint8_t* masks,
+                                                    int64_t ldm, SearchWs s) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)R * nc) return;
+  const int r = (int)(i / nc), c = (int)(i % nc);
+  uint8_t code;
+  if (s.rank[c] < s.ctrl->istar) code = 3;
+  else {
+    const float dg = U[(int64_t)c * ldu + c];
+    const float t = fabsf(target_of(W[(int64_t)r * ldw + c], dg * dg, metric));
+    code = t >= s.ctrl->split ? 2 : 1;
+  }
+  masks[(int64_t)r * ldm + c] = code;
+}
+}  // namespace crbq
+
+extern "C" int crbq_block_search(const float* W, int64_t R, int32_t ncols, int64_t ldw,
+                                 const float* Ublk, int64_t ldu, int32_t metric,
+                                 int32_t up_lim, uint8_t* masks, int64_t ldm,
+                                 crbq_block_trace* trace, void* ws, size_t ws_bytes,
+                                 void* stream) {
+  if (!W || !Ublk || R <= 0 || ncols <= 0 || ncols > NCMAX) return CRBQ_ERR_ARG;
+  if (up_lim < 2 || up_lim > UPMAX) return CRBQ_ERR_ARG;
+  if (ncols < up_lim) return CRBQ_ERR_TOPK;
+  if (R * (int64_t)NCMAX >= (1 << 24)) return CRBQ_ERR_ARG;
+  if (metric != CRBQ_METRIC_HESSIAN && metric != CRBQ_METRIC_MAGNITUDE) return CRBQ_ERR_ARG;
+  if (masks && ldm < ncols) return CRBQ_ERR_ARG;
+  WsCarver c(ws, ws_bytes);
+  SearchWs s;
+  carve_search(c, R, s);
+  if (!c.ok()) return CRBQ_ERR_WORKSPACE;
+  int st = ensure_q_table();
+  if (st) return st;
+  hipStream_t hs = (hipStream_t)stream;
+  st = search_block(W, ldw, (int)R, ncols, Ublk, ldu, metric, up_lim, s, trace, hs);
+  if (st) return st;
+  if (masks) {
+    const int64_t n = R * (int64_t)ncols;
+    k_emit_masks<<<(unsigned)cdiv(n, 256), 256, 0, hs>>>(W, ldw, (int)R, ncols, Ublk, ldu,
+                                                         metric, masks, ldm, s);
+    CRBQ_LAUNCH_CHECK();
+  }
+  return CRBQ_OK;
+}
+
+extern "C" int crbq_set_percentiles(const float* q81) {
+  if (!q81) return CRBQ_ERR_ARG;
+  return set_q_table(q81);
+}
+
+extern "C" size_t crbq_fasterquant_workspace_size(int64_t R, int64_t C, const crbq_params* p) {
+  (void)C;
+  const int bs = p ? p->blocksize : NCMAX;
+  return search_ws_bytes(R) + (size_t)R * (size_t)bs * sizeof(float) + 512;
+}
+
+extern "C" int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw, const float* U,
+                                int64_t ldu, const crbq_params* p, float* losses,
+                                uint8_t* masks, int64_t ldm, crbq_block_trace* traces,
+                                void* ws, size_t ws_bytes, void* stream) {
+  int st = check_params(p);
+  if (st) return st;
+  if (!W || !U || !losses || R <= 0 || C <= 0 || ldw < C || ldu < C) return CRBQ_ERR_ARG;
+  if (R * (int64_t)NCMAX >= (1 << 24)) return CRBQ_ERR_ARG;
+  if (masks && ldm < C) return CRBQ_ERR_ARG;
+  const int bs = p->blocksize;
+  WsCarver c(ws, ws_bytes);
+  SearchWs s;
+  carve_search(c, R, s);
+  float* err = c.take<float>((size_t)R * bs);
+  if (!c.ok()) return CRBQ_ERR_WORKSPACE;
+  st = ensure_q_table();
+  if (st) return st;
+  hipStream_t hs = (hipStream_t)stream;
+  if (p->partition == 3) {
+    // every block must be at least up_lim wide (torch.topk k <= n)
+    const int64_t last = C - (C - 1) / bs * bs;
+    if (last < p->up_lim || bs < p->up_lim) return CRBQ_ERR_TOPK;
+  }
+  CrbConsts k;
+  k.lam = p->lam;
+  k.omg = (float)(1.0 - (double)p->corr_damp);
+  k.sym = false;
+  k.skip = false;
+  k.iters = p->refine_iters;
+  int bi = 0;
+  for (int64_t st0 = 0; st0 < C; st0 += bs, ++bi) {
+    const int nc = (int)std::min<int64_t>(bs, C - st0);
+    float* Wb = W + st0;
+    const float* Ub = U + st0 * ldu + st0;
+    crbq_block_trace* tr = traces ? traces + bi : nullptr;
+    if (p->partition == 3) {
+      st = search_block(Wb, ldw, (int)R, nc, Ub, ldu, p->metric, p->up_lim, s, tr, hs);
+      if (st) return st;
+    }
+    QuantArgs a;
+    a.W = Wb; a.ldw = ldw; a.R = (int)R; a.nc = nc;
+    a.U = Ub; a.ldu = ldu;
+    a.metric = p->metric; a.method = p->method; a.partition = p->partition;
+    for (int g = 0; g < 3; ++g) a.orders[g] = p->orders[g];
+    a.k = k;
+    a.gptq = !p->disable_gptq;
+    a.err = err; a.lde = bs;
+    a.losses = losses;
+    a.masks = masks ? masks + st0 : nullptr; a.ldm = ldm;
+    k_quantize<2><<<(unsigned)cdiv(R, 4), 256, 0, hs>>>(a, s);
+    CRBQ_LAUNCH_CHECK();
+    const int64_t ed = st0 + nc;
+    if (a.gptq && ed < C) {
+      st = sgemm_launch(false, false, false, R, C - ed, nc, -1.f, err, bs,
+                        U + st0 * ldu + ed, ldu, 1.f, W + ed, ldw, nullptr, hs);
+      if (st) return st;
+    }
+  }
+  return CRBQ_OK;
+}
+
+// ---------------------------------------------------------------------------
+// standalone Binarization.quantize
+// ---------------------------------------------------------------------------
+namespace crbq {
+template <int EPL>
+__global__ __launch_bounds__(256) void k_binarize(const float* x, int R, int nc, int64_t ldx,
+                                                  const uint8_t* __restrict__ mask, int64_t ldm,
+                                                  int order, int method, CrbConsts k, float* out,
+                                                  int64_t ldo) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= R) return;
+  float v[EPL], o[EPL];
+  bool m[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int c = lane + 64 * e;
+    const bool ok = c < nc;
+    v[e] = ok ? x[(int64_t)row * ldx + c] : 0.f;
+    m[e] = ok && mask[(int64_t)row * ldm + c] != 0;
+  }
+  binarize_row<EPL>(method, v, m, order, k, o);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int c = lane + 64 * e;
+    if (c < nc) out[(int64_t)row * ldo + c] = o[e];
+  }
+}
+}  // namespace crbq
+
+extern "C" int crbq_binarize(const float* x, int64_t R, int32_t ncols, int64_t ldx,
+                             const uint8_t* mask, int64_t ldm, int32_t order, int32_t method,
+                             float lam, float corr_damp, int32_t refine_iters, float* out,
+                             int64_t ldo, void* stream) {
+  if (!x || !mask || !out || R <= 0 || ncols <= 0 || ncols > 1024) return CRBQ_ERR_ARG;
+  if (order < 1 || order > 8 || refine_iters < 0 || refine_iters > 64) return CRBQ_ERR_ARG;
+  if (method < CRBQ_BRAQ || method > CRBQ_CRB_SYMDAMP_NOREFINE) return CRBQ_ERR_ARG;
+  if (R > (int64_t)4 * 65535 * 1024) return CRBQ_ERR_ARG;
+  CrbConsts k;
+  k.lam = lam;
+  k.omg = (float)(1.0 - (double)corr_damp);
+  k.sym = false;
+  k.skip = false;
+  k.iters = refine_iters;
+  hipStream_t hs = (hipStream_t)stream;
+  const unsigned g = (unsigned)cdiv(R, 4);
+  const int r = (int)R;
+  if (ncols <= 128) k_binarize<2><<<g, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, out, ldo);
+  else if (ncols <= 256) k_binarize<4><<<g, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, out, ldo);
+  else if (ncols <= 512) k_binarize<8><<<g, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, out, ldo);
+  else k_binarize<16><<<g, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, out, ldo);
+  CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}

@@ -1,0 +1,169 @@
+"""Torch-tensor wrappers of the crbq C ABI.
+
+Each function takes CUDA (HIP) tensors, allocates what the call needs
+through the PyTorch caching allocator (outputs and the workspace), runs on
+torch's current stream and raises CrbqError on a non-zero status.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import CrbqBlockTrace, check, ptr, stream_of
+
+
+def _dev_check(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise _lib.CrbqError("crbq tensors must live on the GPU")
+
+
+def _ws(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def hessian_accum(X: torch.Tensor, S: torch.Tensor) -> None:
+    """S[i, j] += sum_t X[t, i] X[t, j] (upper triangle i <= j), X [T, C]."""
+    _dev_check(X, S)
+    if X.dim() != 2 or X.stride(1) != 1:
+        X = X.reshape(-1, X.shape[-1]).contiguous()
+    if X.dtype not in _lib.DTYPES:
+        X = X.float()
+    T, C = X.shape
+    lib = _lib.ready(X.device)
+    check(lib.crbq_hessian_accum(X.data_ptr(), _lib.DTYPES[X.dtype], T, X.stride(0), C,
+                                 S.data_ptr(), S.stride(0), stream_of(S)),
+          "crbq_hessian_accum")
+
+
+def hessian_finalize(S: torch.Tensor, scale: float, H: torch.Tensor | None = None) -> torch.Tensor:
+    """H = scale * sym(S) from the upper triangle of S (H may be S)."""
+    _dev_check(S)
+    C = S.shape[0]
+    if H is None:
+        H = torch.empty_like(S)
+    lib = _lib.ready(S.device)
+    check(lib.crbq_hessian_finalize(S.data_ptr(), S.stride(0), C, float(scale), H.data_ptr(),
+                                    H.stride(0), stream_of(S)), "crbq_hessian_finalize")
+    return H
+
+
+def hinv_upper(H: torch.Tensor, W: torch.Tensor | None, percdamp: float = 0.01):
+    """bigptq.py:101-129.  Mutates H (and W's dead columns) like the
+    reference.  Returns (U, retries, fallback)."""
+    _dev_check(H, W)
+    if H.stride(1) != 1 or (W is not None and W.stride(1) != 1):
+        raise _lib.CrbqError("hinv_upper works in place on row-major H and W")
+    C = H.shape[0]
+    lib = _lib.ready(H.device)
+    U = torch.empty((C, C), dtype=torch.float32, device=H.device)
+    ws = _ws(lib.crbq_hinv_workspace_size(C), H.device)
+    retries = ctypes.c_int32(0)
+    fallback = ctypes.c_int32(0)
+    R = W.shape[0] if W is not None else 0
+    ldw = W.stride(0) if W is not None else 0
+    check(lib.crbq_hinv_upper(H.data_ptr(), H.stride(0), C, ptr(W), R, ldw, float(percdamp),
+                              U.data_ptr(), U.stride(0), ws.data_ptr(), ws.numel(),
+                              ctypes.byref(retries), ctypes.byref(fallback), stream_of(H)),
+          "crbq_hinv_upper")
+    return U, int(retries.value), bool(fallback.value)
+
+
+def fasterquant_blocks(W: torch.Tensor, U: torch.Tensor, p: _lib.CrbqParams,
+                       losses: torch.Tensor, want_masks: bool = False,
+                       want_traces: bool = False):
+    """Block loop of bigptq.py:131-264 on W (fp32, in place).
+    Returns (masks uint8 [R, C] or None, traces list or None)."""
+    _dev_check(W, U, losses)
+    if W.dtype != torch.float32 or W.stride(1) != 1:
+        raise _lib.CrbqError("fasterquant_blocks works in place on a row-major fp32 W")
+    if U.stride(1) != 1:
+        U = U.contiguous()
+    R, C = W.shape
+    lib = _lib.ready(W.device)
+    ws = _ws(lib.crbq_fasterquant_workspace_size(R, C, ctypes.byref(p)), W.device)
+    masks = torch.zeros((R, C), dtype=torch.uint8, device=W.device) if want_masks else None
+    nblk = (C + p.blocksize - 1) // p.blocksize
+    tr = torch.zeros(nblk * _lib.TRACE_BYTES, dtype=torch.uint8,
+                     device=W.device) if want_traces else None
+    check(lib.crbq_fasterquant(W.data_ptr(), R, C, W.stride(0), U.data_ptr(), U.stride(0),
+                               ctypes.byref(p), losses.data_ptr(), ptr(masks),
+                               masks.stride(0) if masks is not None else 0, ptr(tr),
+                               ws.data_ptr(), ws.numel(), stream_of(W)),
+          "crbq_fasterquant")
+    traces = decode_traces(tr, nblk) if tr is not None else None
+    return masks, traces
+
+
+def decode_traces(buf: torch.Tensor, n: int):
+    raw = bytes(buf.cpu().numpy().tobytes())
+    out = []
+    for i in range(n):
+        t = CrbqBlockTrace.from_buffer_copy(raw, i * _lib.TRACE_BYTES)
+        out.append({
+            "i_star": t.i_star, "k_star": t.k_star, "split": t.split,
+            "pvals": list(t.pvals), "errs_a": list(t.errs_a), "errs_c": list(t.errs_c),
+        })
+    return out
+
+
+def block_search(Wblk: torch.Tensor, Ublk: torch.Tensor, metric: str = "hessian",
+                 up_lim: int = 50):
+    """One block of utils/structure.py:8-20.  Wblk [R, ncols] (may be a
+    column slice of W), Ublk [ncols, ncols] slice of U.
+    Returns (mask codes uint8 [R, ncols]: 1/2/3, trace dict)."""
+    _dev_check(Wblk, Ublk)
+    if Wblk.stride(1) != 1:
+        Wblk = Wblk.contiguous()
+    if Ublk.stride(1) != 1:
+        Ublk = Ublk.contiguous()
+    R, nc = Wblk.shape
+    lib = _lib.ready(Wblk.device)
+    ws = _ws(lib.crbq_block_search_workspace_size(R, up_lim), Wblk.device)
+    masks = torch.zeros((R, nc), dtype=torch.uint8, device=Wblk.device)
+    tr = torch.zeros(_lib.TRACE_BYTES, dtype=torch.uint8, device=Wblk.device)
+    check(lib.crbq_block_search(Wblk.data_ptr(), R, nc, Wblk.stride(0), Ublk.data_ptr(),
+                                Ublk.stride(0), _lib.METRICS[metric], up_lim, masks.data_ptr(),
+                                masks.stride(0), tr.data_ptr(), ws.data_ptr(), ws.numel(),
+                                stream_of(Wblk)), "crbq_block_search")
+    return masks, decode_traces(tr, 1)[0]
+
+
+def binarize(x: torch.Tensor, mask: torch.Tensor, order: int, method: str, lam: float = 1e-5,
+             corr_damp: float = 0.1, refine_iters: int = 1, out: torch.Tensor | None = None):
+    """Binarization.quantize (binary.py:2874-2890) for the crbq methods."""
+    _dev_check(x, mask)
+    if method not in _lib.METHODS:
+        raise NotImplementedError(method)
+    xf = x if (x.dtype == torch.float32 and x.stride(-1) == 1) else x.float().contiguous()
+    m = mask.to(torch.uint8).contiguous()
+    R, nc = xf.shape
+    if out is None:
+        out = torch.empty((R, nc), dtype=torch.float32, device=x.device)
+    lib = _lib.ready(x.device)
+    check(lib.crbq_binarize(xf.data_ptr(), R, nc, xf.stride(0), m.data_ptr(), m.stride(0),
+                            int(order), _lib.METHODS[method], float(lam), float(corr_damp),
+                            int(refine_iters), out.data_ptr(), out.stride(0), stream_of(xf)),
+          "crbq_binarize")
+    return out
+
+
+def sgemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, alpha: float = 1.0,
+          beta: float = 0.0, transa: bool = False, transb: bool = False) -> torch.Tensor:
+    """C = beta*C + alpha*op(A) op(B) on fp32 MFMA (row-major operands)."""
+    _dev_check(A, B, C)
+    if C.stride(1) != 1:
+        raise _lib.CrbqError("sgemm writes a row-major C")
+    if A.stride(1) != 1:
+        A = A.contiguous()
+    if B.stride(1) != 1:
+        B = B.contiguous()
+    M, N = C.shape
+    K = A.shape[0] if transa else A.shape[1]
+    lib = _lib.ready(C.device)
+    check(lib.crbq_sgemm(int(transa), int(transb), M, N, K, float(alpha), A.data_ptr(),
+                         A.stride(0), B.data_ptr(), B.stride(0), float(beta), C.data_ptr(),
+                         C.stride(0), stream_of(C)), "crbq_sgemm")
+    return C

@@ -1,0 +1,163 @@
+/* crbq.h - C ABI of the MI355X-native CRB layer-wise binarization quantizer.
+ *
+ * Every pointer argument named as "device" is a device pointer owned by the
+ * caller (for the Python host: the PyTorch caching allocator).  The library
+ * never allocates device memory: scratch space comes in through `ws`
+ * (size from the matching *_workspace_size query).  `stream` is a
+ * hipStream_t passed as void*; NULL means the default stream.  Every entry
+ * point returns a status: 0 = ok, < 0 = error (see crbq_status_string), and
+ * never throws across the ABI.  Entry points that must read a device result
+ * to continue (the Cholesky retry loop) synchronise `stream`.
+ *
+ * Reference interface replaced (paths relative to the SDMuhsin/CRB root):
+ *   BRAGPTQ.add_batch            bigptq.py:37-53
+ *   BRAGPTQ.fasterquant          bigptq.py:56-291
+ *   structural_guassian_distribution / structural_searching /
+ *   generate_structural_mask     utils/structure.py:8-20,
+ *                                utils/autosearch.py:28-83, utils/mask.py:7-18
+ *   Binarization.quantize        binary.py:2850-2890 ->
+ *                                high_order_residual binary.py:18-39,
+ *                                coupled_residual_binarization binary.py:577-687,
+ *                                coupled_residual_binarization_stable_v7
+ *                                binary.py:1544-1638
+ */
+#ifndef CRBQ_H
+#define CRBQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define CRBQ_OK              0
+#define CRBQ_ERR_ARG        -1   /* bad size, stride, enum or alignment */
+#define CRBQ_ERR_HIP        -2   /* a HIP runtime call failed */
+#define CRBQ_ERR_WORKSPACE  -3   /* workspace pointer NULL or too small */
+#define CRBQ_ERR_TOPK       -4   /* block narrower than the salient search limit
+                                    (torch.topk k out of range, utils/autosearch.py:42) */
+
+/* ---- enums -------------------------------------------------------------- */
+enum crbq_dtype  { CRBQ_F32 = 0, CRBQ_F16 = 1, CRBQ_BF16 = 2 };
+/* Binarization methods in scope (binary.py:2875-2890). */
+enum crbq_method {
+  CRBQ_BRAQ = 0,                 /* high_order_residual                     */
+  CRBQ_CRB = 1,                  /* ..._stable_v7                            */
+  CRBQ_CRBOG = 2,                /* coupled_residual_binarization            */
+  CRBQ_CRB_NOREFINE = 3,         /* v7, skip_refinement=True                 */
+  CRBQ_CRB_SYMDAMP = 4,          /* v7, symmetric_damp=True                  */
+  CRBQ_CRB_SYMDAMP_NOREFINE = 5  /* v7, both                                 */
+};
+enum crbq_metric { CRBQ_METRIC_MAGNITUDE = 0, CRBQ_METRIC_HESSIAN = 1 };
+
+/* Quantizer hyper-parameters of one fasterquant call
+ * (bigptq.py:56-62, binary.py:2851-2866, run.py:868-873). */
+typedef struct crbq_params {
+  int32_t method;        /* enum crbq_method                                 */
+  int32_t metric;        /* enum crbq_metric (salient_metric)                */
+  int32_t blocksize;     /* column block, 1..128 (reference default 128)     */
+  int32_t partition;     /* 3 = salient/bell split; 1 = one all-ones mask    */
+  int32_t orders[3];     /* binarization order per mask (default 1,1,2)      */
+  int32_t up_lim;        /* salient-column search limit (50, bigptq.py:142)  */
+  int32_t refine_iters;  /* CRB sign-refinement rounds (reference: 1)        */
+  int32_t disable_gptq;  /* 1 = RTN: no error feedback (bigptq.py:149-162)   */
+  float   lam;           /* CRB Tikhonov term (1e-5)                          */
+  float   corr_damp;     /* CRB correlation damping (0.1)                     */
+} crbq_params;
+
+/* Per-block search record (filled when a trace buffer is given).
+ * errs_a[i] = summed squared error of salient candidate i (index 0 unused),
+ * errs_c[k] = summed squared error of split candidate k, without the
+ * constant salient-group term. */
+typedef struct crbq_block_trace {
+  int32_t i_star;        /* number of salient columns chosen                 */
+  int32_t k_star;        /* index of the chosen percentile split             */
+  float   split;         /* chosen split value                                */
+  float   pvals[81];     /* the 81 float32 percentiles (np.quantile)         */
+  double  errs_a[64];
+  double  errs_c[81];
+} crbq_block_trace;
+
+/* ---- library ------------------------------------------------------------ */
+int         crbq_version(void);
+const char* crbq_status_string(int status);
+/* 0 when the current HIP device is a gfx950 (MI355X), else < 0. */
+int         crbq_device_ok(void);
+/* The 81 float32 split percentiles, torch.linspace(0.10, 0.90, 81) as the
+ * host's torch computes it on the CPU (utils/autosearch.py:65; its last bits
+ * depend on the CPU's vector width).  q81: host pointer.  Without this call
+ * the library uses torch's scalar formula. */
+int         crbq_set_percentiles(const float* q81);
+
+/* ---- Hessian accumulation (BRAGPTQ.add_batch, bigptq.py:37-53) ---------
+ * S[i,j] += sum_t X[t,i] * X[t,j] over ntok token rows of X (row stride ldx
+ * elements, dtype enum crbq_dtype), for the upper triangle i <= j of the
+ * fp32 C x C matrix S (row stride lds).  f16/bf16 products are exact and
+ * accumulate in fp32 on MFMA; fp32 inputs use the fp32 MFMA.
+ * The reference's running rescale H *= n/(n+b); H += (2/n) X^T X is applied
+ * once, in crbq_hessian_finalize, which gives the same H up to rounding. */
+int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_t ldx,
+                       int64_t C, float* S, int64_t lds, void* stream);
+/* H[i,j] = scale * S[min(i,j), max(i,j)] for all i, j (H may alias S). */
+int crbq_hessian_finalize(const float* S, int64_t lds, int64_t C, float scale,
+                          float* H, int64_t ldh, void* stream);
+
+/* ---- inverse-Hessian factor (fasterquant prologue, bigptq.py:101-129) ----
+ * Dead columns (diag(H) == 0 -> H_ii = 1, W[:, i] = 0), damping
+ * H_ii += percdamp * mean(diag H), Cholesky with up to 10 retries adding
+ * 1e-3 * mean(diag H) (1e-6 if that is 0), diagonal fallback, and
+ * U = upper Cholesky factor of H^-1, written to U (C x C, row stride ldu,
+ * zero below the diagonal).  H is modified like the reference's.  U is
+ * computed as J L'^-1 J with L' = chol(J H J) (J = index reversal), which is
+ * the same matrix in 2C^3/3 flops instead of 4C^3/3.
+ * W may be NULL (then dead columns are not cleared).  retries/fallback: host
+ * pointers (may be NULL).  Synchronises `stream`. */
+size_t crbq_hinv_workspace_size(int64_t C);
+int crbq_hinv_upper(float* H, int64_t ldh, int64_t C, float* W, int64_t R,
+                    int64_t ldw, float percdamp, float* U, int64_t ldu,
+                    void* ws, size_t ws_bytes, int* retries, int* fallback,
+                    void* stream);
+
+/* ---- block loop (BRAGPTQ.fasterquant, bigptq.py:131-264) -----------------
+ * Quantizes W (R x C fp32, row stride ldw) in place, column block by column
+ * block: salient/bell mask search, binarization, Err/Loss, and the GPTQ
+ * trailing update W[:, ed:] -= Err @ U[st:ed, ed:].  losses (R floats) is
+ * accumulated (+= per-row loss sum / 2), like Losses in the reference.
+ * masks (optional, R x C uint8, row stride ldm): 1/2/3 = mask1/2/3 member.
+ * traces (optional, device array of ceil(C/blocksize) crbq_block_trace). */
+size_t crbq_fasterquant_workspace_size(int64_t R, int64_t C,
+                                       const crbq_params* p);
+int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw,
+                     const float* U, int64_t ldu, const crbq_params* p,
+                     float* losses, uint8_t* masks, int64_t ldm,
+                     crbq_block_trace* traces, void* ws, size_t ws_bytes,
+                     void* stream);
+
+/* ---- one-block pieces (for tests and the Binarization API) --------------
+ * Search of one column block (utils/structure.py:8-20): writes the
+ * R x ncols mask codes 1/2/3 (row stride ldm) and, optionally, a trace. */
+size_t crbq_block_search_workspace_size(int64_t R, int32_t up_lim);
+int crbq_block_search(const float* W, int64_t R, int32_t ncols, int64_t ldw,
+                      const float* Ublk, int64_t ldu, int32_t metric,
+                      int32_t up_lim, uint8_t* masks, int64_t ldm,
+                      crbq_block_trace* trace, void* ws, size_t ws_bytes,
+                      void* stream);
+/* Binarization.quantize(x, mask, order) (binary.py:2874-2890) on an
+ * R x ncols fp32 matrix with a 0/1 uint8 mask; out may alias x.
+ * ncols <= 1024. */
+int crbq_binarize(const float* x, int64_t R, int32_t ncols, int64_t ldx,
+                  const uint8_t* mask, int64_t ldm, int32_t order,
+                  int32_t method, float lam, float corr_damp,
+                  int32_t refine_iters, float* out, int64_t ldo, void* stream);
+/* C = beta*C + alpha*op(A)*op(B), fp32 on MFMA (the trailing update uses
+ * alpha = -1, beta = 1, bigptq.py:264).  transa/transb: op(X) = X^T. */
+int crbq_sgemm(int transa, int transb, int64_t M, int64_t N, int64_t K,
+               float alpha, const float* A, int64_t lda, const float* B,
+               int64_t ldb, float beta, float* C, int64_t ldc, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CRBQ_H */

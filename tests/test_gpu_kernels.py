@@ -1,0 +1,253 @@
+"""GPU parity of the individual crbq kernels against the CPU oracle, the
+reference-written golden vectors and float64 closed forms.
+
+Tolerances (fp32 kernels vs. fp32 torch-CPU reductions, which differ only in
+summation order):
+  * GEMM / Hessian / U: relative Frobenius error <= 1e-5 (GEMM, Hessian),
+    <= 1e-4 (U, through a factorization);
+  * binarizers: per-element |diff| <= 1e-5 * max|x| on >= 99.9% of elements
+    (ulp-level differences of a row mean can flip sign(x - mean) for an
+    element sitting on the mean), and all per-row values match to 1e-4 rel;
+  * search: split and salient count identical to the reference's, unless the
+    reference's own candidate errors tie within 1e-6 relative.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import crb_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _k():
+    from crb_amd import kernels
+    return kernels
+
+
+def rel(a, b):
+    a = a.double().cpu()
+    b = b.double().cpu()
+    return float((a - b).norm() / max(b.norm(), 1e-300))
+
+
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (130, 70, 37), (256, 384, 128), (300, 129, 200)])
+def test_sgemm(ta, tb, M, N, K):
+    print(f"sgemm ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + N * 3 + K)
+    A = torch.randn((K, M) if ta else (M, K), generator=g)
+    B = torch.randn((N, K) if tb else (K, N), generator=g)
+    C = torch.randn(M, N, generator=g)
+    want = 0.5 * C.double() + (-1.25) * ((A.double().t() if ta else A.double())
+                                         @ (B.double().t() if tb else B.double()))
+    Cd = C.to(DEV)
+    _k().sgemm(A.to(DEV), B.to(DEV), Cd, alpha=-1.25, beta=0.5, transa=ta, transb=tb)
+    torch.cuda.synchronize()
+    assert rel(Cd, want) < 1e-5
+
+
+def test_sgemm_trailing_update_shape():
+    """W[:, ed:] -= Err @ U[st:ed, ed:] on strided views (bigptq.py:264)."""
+    print("sgemm trailing", flush=True)
+    g = torch.Generator().manual_seed(5)
+    R, C, st, ed = 200, 520, 128, 256
+    W = torch.randn(R, C, generator=g)
+    U = torch.triu(torch.randn(C, C, generator=g))
+    E = torch.randn(R, ed - st, generator=g)
+    want = W.double().clone()
+    want[:, ed:] -= E.double() @ U[st:ed, ed:].double()
+    Wd, Ud, Ed = W.to(DEV), U.to(DEV), E.to(DEV)
+    _k().sgemm(Ed, Ud[st:ed, ed:], Wd[:, ed:], alpha=-1.0, beta=1.0)
+    torch.cuda.synchronize()
+    assert rel(Wd, want) < 1e-6
+    assert torch.equal(Wd[:, :ed].cpu(), W[:, :ed])
+
+
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,C", [(300, 200), (64, 128), (1000, 384), (5, 8)])
+def test_hessian_accum(dtype, T, C):
+    print(f"hessian {dtype} T={T} C={C}", flush=True)
+    g = torch.Generator().manual_seed(T + C)
+    X = (torch.randn(T, C, generator=g) * torch.exp(torch.randn(C, generator=g))).to(dtype)
+    S = torch.zeros(C, C, device=DEV)
+    _k().hessian_accum(X.to(DEV), S)
+    _k().hessian_accum(X[: T // 2].to(DEV), S)      # accumulates
+    torch.cuda.synchronize()
+    Xd = X.double()
+    want = Xd.t() @ Xd + Xd[: T // 2].t() @ Xd[: T // 2]
+    got = S.cpu().double()
+    iu = torch.triu_indices(C, C)
+    assert rel(got[iu[0], iu[1]], want[iu[0], iu[1]]) < 1e-5
+    H = _k().hessian_finalize(S, 0.5)
+    torch.cuda.synchronize()
+    assert rel(H, 0.5 * want) < 1e-5
+    assert torch.equal(H.cpu(), H.cpu().t())
+
+
+def test_hessian_matches_reference_add_batch():
+    """Incremental rescale of bigptq.py:50-53 vs. one 2/n scaling."""
+    print("hessian add_batch", flush=True)
+    g = torch.Generator().manual_seed(3)
+    X = torch.randn(6, 50, 96, generator=g).half()
+    H = torch.zeros(96, 96)
+    n = 0
+    for s in range(6):
+        H, n = O.hessian_add_batch(H, n, X[s:s + 1].float())
+    S = torch.zeros(96, 96, device=DEV)
+    for s in range(6):
+        _k().hessian_accum(X[s].to(DEV), S)
+    Hg = _k().hessian_finalize(S, 2.0 / 6)
+    torch.cuda.synchronize()
+    assert rel(Hg, H) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+def _spd(C, seed, cond=1e3):
+    g = torch.Generator().manual_seed(seed)
+    Q, _ = torch.linalg.qr(torch.randn(C, C, generator=g, dtype=torch.float64))
+    ev = torch.logspace(0, np.log10(cond), C, dtype=torch.float64)
+    return (Q * ev) @ Q.t()
+
+
+@pytest.mark.parametrize("C", [7, 128, 300, 512])
+def test_hinv_upper_matches_oracle(C):
+    print(f"hinv C={C}", flush=True)
+    H = _spd(C, C).float()
+    W = torch.randn(16, C)
+    Uo, info = O.hinv_upper(H.clone(), W.clone(), 0.01)
+    Hd, Wd = H.to(DEV), W.to(DEV)
+    U, retries, fb = _k().hinv_upper(Hd, Wd, 0.01)
+    torch.cuda.synchronize()
+    assert retries == info.retries == 0 and not fb
+    assert rel(U, Uo) < 1e-4
+    assert torch.equal(torch.tril(U.cpu(), -1), torch.zeros(C, C))
+    # invariant: U^T U (H + damp I) = I
+    Hdamp = H.double() + 0.01 * torch.diag(H.double()).mean() * torch.eye(C, dtype=torch.float64)
+    Ud = U.cpu().double()
+    assert float((Ud.t() @ Ud @ Hdamp - torch.eye(C, dtype=torch.float64)).abs().max()) < 1e-3
+
+
+def test_hinv_dead_columns():
+    print("hinv dead", flush=True)
+    C = 160
+    H = _spd(C, 4).float()
+    H[:, 5] = 0
+    H[5, :] = 0                                   # dead column (bigptq.py:103-105)
+    W = torch.randn(8, C)
+    Ho = H.clone()
+    Uo, info = O.hinv_upper(Ho, W.clone(), 0.01)
+    Hd, Wd = H.to(DEV), W.to(DEV)
+    U, retries, fb = _k().hinv_upper(Hd, Wd, 0.01)
+    torch.cuda.synchronize()
+    assert retries == info.retries == 0 and not fb
+    assert torch.all(Wd[:, 5].cpu() == 0) and torch.equal(Wd[:, 6:].cpu(), W[:, 6:])
+    # dead diagonal set to 1, then damped like every other diagonal entry
+    assert rel(torch.diag(Hd), torch.diag(Ho)) < 1e-6
+    assert rel(U, Uo) < 1e-4
+
+
+@pytest.mark.parametrize("need", [1, 3])
+def test_hinv_retries(need):
+    """An indefinite H whose smallest eigenvalue needs `need` extra damping
+    rounds of 1e-3 * mean(diag) (bigptq.py:114-123) after the 1% damping."""
+    print(f"hinv retries need={need}", flush=True)
+    C = 160
+    g = torch.Generator().manual_seed(11)
+    Q, _ = torch.linalg.qr(torch.randn(C, C, generator=g, dtype=torch.float64))
+    ev = torch.ones(C, dtype=torch.float64)
+    ev[0] = -(0.01 + (need - 0.5) * 1e-3) * 0.994
+    H = ((Q * ev) @ Q.t()).float()
+    Uo, info = O.hinv_upper(H.clone(), torch.zeros(2, C), 0.01)
+    U, retries, fb = _k().hinv_upper(H.to(DEV), None, 0.01)
+    torch.cuda.synchronize()
+    print("  retries gpu", retries, "oracle", info.retries)
+    assert info.retries == need
+    assert retries == info.retries and fb == info.fallback
+    assert rel(U, Uo) < 1e-3
+
+
+def test_hinv_fallback():
+    print("hinv fallback", flush=True)
+    C = 64
+    H = torch.eye(C) * 2.0
+    H[3, 3] = -1e9                                # no amount of damping rescues it
+    Uo, info = O.hinv_upper(H.clone(), torch.zeros(2, C), 0.01)
+    U, retries, fb = _k().hinv_upper(H.to(DEV), None, 0.01)
+    torch.cuda.synchronize()
+    assert info.fallback and fb and retries == 10
+    assert rel(U, Uo) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+BIN_METHODS = ["braq", "crb", "crb_norefine", "crb_symdamp", "crbog"]
+
+
+@pytest.mark.parametrize("method", BIN_METHODS)
+@pytest.mark.parametrize("order", [1, 2])
+def test_binarize_matches_reference_golden(golden, method, order):
+    print(f"binarize {method} order {order}", flush=True)
+    summary, A = golden
+    for c in summary["binarize"]:
+        i = c["case"]
+        x = torch.from_numpy(A[f"bin{i}_x"])
+        m = torch.from_numpy(A[f"bin{i}_m"])
+        want = torch.from_numpy(A[f"bin{i}_o{order}_{method}"])
+        got = _k().binarize(x.to(DEV), m.to(DEV), order, method).cpu()
+        tol = 1e-5 * float(x.abs().max())
+        bad = ((got - want).abs() > tol)
+        frac = float(bad.float().mean())
+        print(f"  case {i}: max|d|={float((got - want).abs().max()):.3g} bad={frac:.4%}")
+        assert frac <= 1e-3 or int(bad.sum()) <= 1
+
+
+@pytest.mark.parametrize("method", BIN_METHODS)
+def test_binarize_random_vs_oracle(method):
+    print(f"binarize random {method}", flush=True)
+    g = torch.Generator().manual_seed(17)
+    for R, nc in [(64, 128), (40, 300), (9, 1024), (3, 1)]:
+        x = torch.randn(R, nc, generator=g) * 0.02
+        m = torch.rand(R, nc, generator=g) < 0.7
+        for order in (1, 2):
+            want = O.binarize(method, x, m, order)
+            got = _k().binarize(x.to(DEV), m.to(DEV), order, method).cpu()
+            tol = 1e-5 * float(x.abs().max())
+            bad = (got - want).abs() > tol
+            assert float(bad.float().mean()) <= 2e-3, (R, nc, order)
+
+
+# ---------------------------------------------------------------------------
+def test_block_search_matches_reference_golden(golden):
+    """structural_searching on the reference-written blocks: T is passed as W
+    with the magnitude metric (T = W), which is exactly the reference's
+    searching input (utils/autosearch.py:28)."""
+    summary, A = golden
+    for c in summary["search"]:
+        i = c["case"]
+        print(f"search case {i} R={c['R']}", flush=True)
+        T = torch.from_numpy(A[f"search{i}_T"])
+        tr = O.SearchTrace()
+        split_o, m3_o = O.structural_searching(T, 50, trace=tr)
+        Td = T.to(DEV)
+        U = torch.eye(128, device=DEV)
+        masks, gt = _k().block_search(Td, U, metric="magnitude", up_lim=50)
+        torch.cuda.synchronize()
+        # percentiles are exact (same T, same float32 index arithmetic)
+        pv = np.asarray(gt["pvals"], dtype=np.float32)
+        qo = np.quantile(np.abs((T * (~m3_o)).numpy()).ravel(),
+                         O.PERCENTILES.numpy()).astype(np.float32)
+        if gt["i_star"] == c["n_salient_cols"]:
+            np.testing.assert_array_equal(pv, qo)
+        ea = np.asarray(gt["errs_a"][1:50]) / T.numel()
+        eo = np.asarray(tr.errs_a)
+        print("  istar gpu", gt["i_star"], "ref", c["n_salient_cols"],
+              "max rel errA diff", float(np.max(np.abs(ea - eo) / np.abs(eo))))
+        assert np.max(np.abs(ea - eo) / np.abs(eo)) < 1e-4
+        assert gt["i_star"] == c["n_salient_cols"]
+        assert float(gt["split"]).hex() == c["split_hex"] or \
+            abs(gt["split"] - c["split"]) <= 1e-6 * abs(c["split"])
+        np.testing.assert_array_equal((masks.cpu() == 3).numpy(), A[f"search{i}_m3"])
