@@ -58,7 +58,9 @@ _SIGS = {
     "crbq_status_string": (ctypes.c_char_p, [c_i32]),
     "crbq_device_ok": (c_i32, []),
     "crbq_set_percentiles": (c_i32, [c_vp]),
-    "crbq_hessian_accum": (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp]),
+    "crbq_hessian_workspace_size": (c_size, [c_i64, c_i64]),
+    "crbq_hessian_accum": (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_size,
+                                   c_vp]),
     "crbq_hessian_finalize": (c_i32, [c_vp, c_i64, c_i64, ctypes.c_float, c_vp, c_i64, c_vp]),
     "crbq_hinv_workspace_size": (c_size, [c_i64]),
     "crbq_hinv_upper": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, ctypes.c_float, c_vp,

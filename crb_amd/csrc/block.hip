@@ -37,6 +37,8 @@ constexpr int Q_RPW = 16;    // rows per workgroup in the quantile passes
 constexpr int PA_RPW = 13;   // rows per workgroup in phase A (13*49 = 637 items)
 constexpr int PC_RPW = 7;    // rows per workgroup in phase C (7*81 = 567 items)
 constexpr int PX_THREADS = 128;
+constexpr int CS_MAXWG = 256;  // colscore partials (grid-stride over row groups)
+constexpr int PX_MAXWG = 1024; // phase A / C partials
 constexpr int H1_BITS = 12, H2_BITS = 10, H3_BITS = 10;   // 12 + 10 + 10 = 32
 constexpr int H1 = 1 << H1_BITS, H2 = 1 << H2_BITS, H3 = 1 << H3_BITS;
 constexpr int SH1 = H2_BITS + H3_BITS, SH2 = H3_BITS;     // key = b1<<SH1 | b2<<SH2 | b3
@@ -81,11 +83,11 @@ struct SearchWs {
 static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 static void carve_search(WsCarver& c, int64_t R, SearchWs& s) {
-  s.colpart = c.take<double>((size_t)cdiv(R, CS_RPW) * NCMAX);
+  s.colpart = c.take<double>((size_t)CS_MAXWG * NCMAX);
   s.rank = c.take<int>(NCMAX);
   s.ctrl = c.take<Ctrl>(1);
-  s.parta = c.take<double>((size_t)cdiv(R, PA_RPW) * UPMAX);
-  s.partc = c.take<double>((size_t)cdiv(R, PC_RPW) * 96);
+  s.parta = c.take<double>((size_t)PX_MAXWG * UPMAX);
+  s.partc = c.take<double>((size_t)PX_MAXWG * 96);
   s.hist1 = c.take<uint32_t>(H1);
   s.slot1map = c.take<int>(H1);
   s.tgt = c.take<Tgt>(NT);
@@ -114,13 +116,15 @@ __global__ __launch_bounds__(256) void k_colscore(
     const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
   __shared__ double part[2][NCMAX];
   const int tid = threadIdx.x, col = tid & (NCMAX - 1), ph = tid >> 7;
-  const int r0 = blockIdx.x * CS_RPW, r1 = min(R, r0 + CS_RPW);
   double acc = 0.0;
   if (col < nc) {
     const float dg = U[(int64_t)col * ldu + col];
     const float d2 = dg * dg;
-    for (int r = r0 + ph; r < r1; r += 2)
-      acc += (double)fabsf(target_of(W[(int64_t)r * ldw + col], d2, metric));
+    for (int r0 = blockIdx.x * CS_RPW; r0 < R; r0 += gridDim.x * CS_RPW) {
+      const int r1 = min(R, r0 + CS_RPW);
+      for (int r = r0 + ph; r < r1; r += 2)
+        acc += (double)fabsf(target_of(W[(int64_t)r * ldw + col], d2, metric));
+    }
   }
   part[ph][col] = acc;
   __syncthreads();
@@ -134,21 +138,41 @@ __global__ __launch_bounds__(256) void k_colscore(
   for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)H1; i += gsz) s.hist1[i] = 0u;
 }
 
-// ranks of the columns by descending score (ties: lower column first)
-__global__ __launch_bounds__(NCMAX) void k_topk(int nc, int nwg, SearchWs s) {
-  __shared__ double sc[NCMAX];
-  const int c = threadIdx.x;
+// Fixed-order sum of nwg partials (row stride `stride` doubles) for `ncand`
+// candidates with 1024 threads: PARTS threads per candidate, then the PARTS
+// subtotals in order.  Result in out[0..ncand).
+template <int NK, int PARTS>
+__device__ void reduce_partials(const double* __restrict__ part, int stride, int nwg, int ncand,
+                                double (*red)[NK], double* out) {
+  const int t = threadIdx.x, k = t % NK, pp = t / NK;
   double v = 0.0;
-  if (c < nc)
-    for (int g = 0; g < nwg; ++g) v += s.colpart[(size_t)g * NCMAX + c];
-  sc[c] = v;
+  if (k < ncand && pp < PARTS)
+    for (int g = pp; g < nwg; g += PARTS) v += part[(size_t)g * stride + k];
+  if (pp < PARTS) red[pp][k] = v;
   __syncthreads();
-  int r = NCMAX;
-  if (c < nc) {
-    r = 0;
-    for (int k = 0; k < nc; ++k) r += (sc[k] > v) || (sc[k] == v && k < c);
+  if (t < ncand) {
+    double a = 0.0;
+    for (int q = 0; q < PARTS; ++q) a += red[q][t];
+    out[t] = a;
   }
-  s.rank[c] = r;
+  __syncthreads();
+}
+
+// ranks of the columns by descending score (ties: lower column first)
+__global__ __launch_bounds__(1024) void k_topk(int nc, int nwg, SearchWs s) {
+  __shared__ double red[8][NCMAX];
+  __shared__ double sc[NCMAX];
+  reduce_partials<NCMAX, 8>(s.colpart, NCMAX, nwg, NCMAX, red, sc);
+  const int c = threadIdx.x;
+  if (c < NCMAX) {
+    const double v = sc[c];
+    int r = NCMAX;
+    if (c < nc) {
+      r = 0;
+      for (int k = 0; k < nc; ++k) r += (sc[k] > v) || (sc[k] == v && k < c);
+    }
+    s.rank[c] = r;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -227,43 +251,47 @@ __global__ __launch_bounds__(PX_THREADS) void k_phase_a(
     const float* __restrict__ U, int64_t ldu, int metric, int ncand, SearchWs s) {
   __shared__ float xs[PA_RPW][NCMAX];
   __shared__ int rk[NCMAX];
+  __shared__ float d2s[NCMAX];
   __shared__ double errs[PA_RPW][UPMAX];
+  __shared__ double acc[UPMAX];
   const int tid = threadIdx.x;
-  const int r0 = blockIdx.x * PA_RPW, nr = min(PA_RPW, R - r0);
-  for (int i = tid; i < NCMAX; i += PX_THREADS) rk[i] = s.rank[i];
-  for (int i = tid; i < PA_RPW * NCMAX; i += PX_THREADS) {
-    const int rr = i / NCMAX, c = i % NCMAX;
-    float v = 0.f;
-    if (rr < nr && c < nc) {
-      const float dg = U[(int64_t)c * ldu + c];
-      v = target_of(W[(int64_t)(r0 + rr) * ldw + c], dg * dg, metric);
+  for (int i = tid; i < NCMAX; i += PX_THREADS) {
+    rk[i] = s.rank[i];
+    if (i < nc) { const float dg = U[(int64_t)i * ldu + i]; d2s[i] = dg * dg; }
+  }
+  for (int i = tid; i < UPMAX; i += PX_THREADS) acc[i] = 0.0;
+  for (int r0 = blockIdx.x * PA_RPW; r0 < R; r0 += gridDim.x * PA_RPW) {
+    const int nr = min(PA_RPW, R - r0);
+    __syncthreads();
+    for (int i = tid; i < PA_RPW * NCMAX; i += PX_THREADS) {
+      const int rr = i / NCMAX, c = i % NCMAX;
+      xs[rr][c] = (rr < nr && c < nc) ? target_of(W[(int64_t)(r0 + rr) * ldw + c], d2s[c], metric)
+                                      : 0.f;
     }
-    xs[rr][c] = v;
+    __syncthreads();
+    const int items = nr * ncand;
+    for (int it = tid; it < items; it += PX_THREADS) {
+      const int rr = it / ncand, ci = it % ncand;
+      errs[rr][ci] = phase_a_item(xs[rr], rk, nc, ci + 1);
+    }
+    __syncthreads();
+    for (int ci = tid; ci < ncand; ci += PX_THREADS) {
+      double e = acc[ci];
+      for (int rr = 0; rr < nr; ++rr) e += errs[rr][ci];
+      acc[ci] = e;
+    }
   }
   __syncthreads();
-  const int items = nr * ncand;
-  for (int it = tid; it < items; it += PX_THREADS) {
-    const int rr = it / ncand, ci = it % ncand;
-    errs[rr][ci] = phase_a_item(xs[rr], rk, nc, ci + 1);
-  }
-  __syncthreads();
-  for (int ci = tid; ci < ncand; ci += PX_THREADS) {
-    double e = 0.0;
-    for (int rr = 0; rr < nr; ++rr) e += errs[rr][ci];
-    s.parta[(size_t)blockIdx.x * UPMAX + ci] = e;
-  }
+  for (int ci = tid; ci < ncand; ci += PX_THREADS)
+    s.parta[(size_t)blockIdx.x * UPMAX + ci] = acc[ci];
 }
 
-__global__ __launch_bounds__(UPMAX) void k_reduce_a(int nwg, int ncand, int up_lim,
-                                                    SearchWs s, crbq_block_trace* tr) {
+__global__ __launch_bounds__(1024) void k_reduce_a(int nwg, int ncand, int up_lim,
+                                                   SearchWs s, crbq_block_trace* tr) {
+  __shared__ double red[16][UPMAX];
   __shared__ double e[UPMAX];
+  reduce_partials<UPMAX, 16>(s.parta, UPMAX, nwg, ncand, red, e);
   const int c = threadIdx.x;
-  if (c < ncand) {
-    double v = 0.0;
-    for (int g = 0; g < nwg; ++g) v += s.parta[(size_t)g * UPMAX + c];
-    e[c] = v;
-  }
-  __syncthreads();
   if (c == 0) {
     double best = INFINITY;
     int istar = max(1, up_lim / 3);                                  // :43
@@ -272,11 +300,7 @@ __global__ __launch_bounds__(UPMAX) void k_reduce_a(int nwg, int ncand, int up_l
     s.ctrl->istar = istar;
     if (tr) tr->i_star = istar;
   }
-  if (tr) {
-    if (c < ncand) tr->errs_a[c + 1] = e[c];
-    if (c == 0) tr->errs_a[0] = 0.0;
-    if (c > ncand && c < UPMAX) tr->errs_a[c] = 0.0;
-  }
+  if (tr && c < UPMAX) tr->errs_a[c] = (c >= 1 && c <= ncand) ? e[c - 1] : 0.0;
 }
 
 // ---------------------------------------------------------------------------
@@ -548,48 +572,51 @@ __global__ __launch_bounds__(PX_THREADS) void k_phase_c(
     const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
   __shared__ float xs[PC_RPW][NCMAX];
   __shared__ bool sal[NCMAX];
+  __shared__ float d2s[NCMAX];
   __shared__ float pv[NQ];
   __shared__ double errs[PC_RPW][NQ];
+  __shared__ double acc[NQ];
   const int tid = threadIdx.x;
-  const int r0 = blockIdx.x * PC_RPW, nr = min(PC_RPW, R - r0);
   const int istar = s.ctrl->istar;
-  for (int i = tid; i < NCMAX; i += PX_THREADS) sal[i] = s.rank[i] < istar;
+  for (int i = tid; i < NCMAX; i += PX_THREADS) {
+    sal[i] = s.rank[i] < istar;
+    if (i < nc) { const float dg = U[(int64_t)i * ldu + i]; d2s[i] = dg * dg; }
+  }
   for (int k = tid; k < NQ; k += PX_THREADS) {
     pv[k] = np_lerp(s.tval[2 * k], s.tval[2 * k + 1], s.gam[k]);
     if (blockIdx.x == 0) s.pvals[k] = pv[k];
+    acc[k] = 0.0;
   }
-  for (int i = tid; i < PC_RPW * NCMAX; i += PX_THREADS) {
-    const int rr = i / NCMAX, c = i % NCMAX;
-    float v = 0.f;
-    if (rr < nr && c < nc) {
-      const float dg = U[(int64_t)c * ldu + c];
-      v = target_of(W[(int64_t)(r0 + rr) * ldw + c], dg * dg, metric);
+  for (int r0 = blockIdx.x * PC_RPW; r0 < R; r0 += gridDim.x * PC_RPW) {
+    const int nr = min(PC_RPW, R - r0);
+    __syncthreads();
+    for (int i = tid; i < PC_RPW * NCMAX; i += PX_THREADS) {
+      const int rr = i / NCMAX, c = i % NCMAX;
+      xs[rr][c] = (rr < nr && c < nc) ? target_of(W[(int64_t)(r0 + rr) * ldw + c], d2s[c], metric)
+                                      : 0.f;
     }
-    xs[rr][c] = v;
+    __syncthreads();
+    const int items = nr * NQ;
+    for (int it = tid; it < items; it += PX_THREADS) {
+      const int rr = it / NQ, k = it % NQ;
+      errs[rr][k] = phase_c_item(xs[rr], sal, nc, pv[k]);
+    }
+    __syncthreads();
+    for (int k = tid; k < NQ; k += PX_THREADS) {
+      double e = acc[k];
+      for (int rr = 0; rr < nr; ++rr) e += errs[rr][k];
+      acc[k] = e;
+    }
   }
   __syncthreads();
-  const int items = nr * NQ;
-  for (int it = tid; it < items; it += PX_THREADS) {
-    const int rr = it / NQ, k = it % NQ;
-    errs[rr][k] = phase_c_item(xs[rr], sal, nc, pv[k]);
-  }
-  __syncthreads();
-  for (int k = tid; k < NQ; k += PX_THREADS) {
-    double e = 0.0;
-    for (int rr = 0; rr < nr; ++rr) e += errs[rr][k];
-    s.partc[(size_t)blockIdx.x * 96 + k] = e;
-  }
+  for (int k = tid; k < NQ; k += PX_THREADS) s.partc[(size_t)blockIdx.x * 96 + k] = acc[k];
 }
 
-__global__ __launch_bounds__(128) void k_reduce_c(int nwg, SearchWs s, crbq_block_trace* tr) {
-  __shared__ double e[NQ];
+__global__ __launch_bounds__(1024) void k_reduce_c(int nwg, SearchWs s, crbq_block_trace* tr) {
+  __shared__ double red[8][128];
+  __shared__ double e[128];
+  reduce_partials<128, 8>(s.partc, 96, nwg, NQ, red, e);
   const int k = threadIdx.x;
-  if (k < NQ) {
-    double v = 0.0;
-    for (int g = 0; g < nwg; ++g) v += s.partc[(size_t)g * 96 + k];
-    e[k] = v;
-  }
-  __syncthreads();
   if (k == 0) {
     double best = INFINITY;
     int ks = NQ / 2;                                                 // :71 median
@@ -688,14 +715,14 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
                         int64_t ldu, int metric, int up_lim, SearchWs& s,
                         crbq_block_trace* tr, hipStream_t st) {
   const int ncand = up_lim - 1;
-  const int nwg_cs = (int)cdiv(R, CS_RPW);
+  const int nwg_cs = (int)std::min<int64_t>(cdiv(R, CS_RPW), CS_MAXWG);
   const int nwg_q = (int)cdiv(R, Q_RPW);
-  const int nwg_a = (int)cdiv(R, PA_RPW);
-  const int nwg_c = (int)cdiv(R, PC_RPW);
+  const int nwg_a = (int)std::min<int64_t>(cdiv(R, PA_RPW), PX_MAXWG);
+  const int nwg_c = (int)std::min<int64_t>(cdiv(R, PC_RPW), PX_MAXWG);
   k_colscore<<<nwg_cs, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  k_topk<<<1, NCMAX, 0, st>>>(nc, nwg_cs, s);
+  k_topk<<<1, 1024, 0, st>>>(nc, nwg_cs, s);
   k_phase_a<<<nwg_a, PX_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, ncand, s);
-  k_reduce_a<<<1, UPMAX, 0, st>>>(nwg_a, ncand, up_lim, s, tr);
+  k_reduce_a<<<1, 1024, 0, st>>>(nwg_a, ncand, up_lim, s, tr);
   k_qpass1<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_qscan1<<<1, 256, 0, st>>>((int64_t)R * nc, s);
   k_qpass2<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
@@ -703,7 +730,7 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
   k_qpass3<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_qscan3<<<NT, 256, 0, st>>>(s);
   k_phase_c<<<nwg_c, PX_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  k_reduce_c<<<1, 128, 0, st>>>(nwg_c, s, tr);
+  k_reduce_c<<<1, 1024, 0, st>>>(nwg_c, s, tr);
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }

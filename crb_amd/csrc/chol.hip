@@ -102,63 +102,136 @@ __global__ __launch_bounds__(256) void k_fallback_u(const float* __restrict__ H,
   U[(int64_t)i * ldu + j] = v;
 }
 
-// Diagonal block: Cholesky and triangular inverse in LDS.
+// Diagonal block: Cholesky and triangular inverse of one NB x NB block.
+// 256 threads as a 16 x 16 grid; thread (ty, tx) keeps the 8 x 8 sub-block
+// rows ty*8.., cols tx*8.. in registers.  Right-looking: step k takes the
+// pivot from its owner, scales column k, publishes it through LDS and every
+// thread applies the rank-1 update to its own lower-triangle entries.  The
+// inverse is the same sweep on the identity (X = L^-1, forward substitution).
 __global__ __launch_bounds__(256) void k_potrf_diag(float* A, int64_t lda, int off, int bj,
                                                     float* D, int* info) {
   if (*info) return;
-  __shared__ float L[NB][NB + 1];
-  __shared__ float X[NB][NB + 1];
+  __shared__ float col[NB];
+  __shared__ float row[NB];
+  __shared__ float dg[NB];
   __shared__ int fail;
-  const int tid = threadIdx.x;
-  for (int idx = tid; idx < NB * NB; idx += 256) {
-    const int i = idx / NB, k = idx % NB;
-    L[i][k] = (i < bj && k <= i) ? A[(int64_t)(off + i) * lda + off + k] : 0.f;
-    X[i][k] = (i == k) ? 1.f : 0.f;
-  }
+  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
+  const int i0 = ty * 8, j0 = tx * 8;
+  float a[8][8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int i = i0 + r, j = j0 + c;
+      a[r][c] = (i < bj && j <= i) ? A[(int64_t)(off + i) * lda + off + j] : 0.f;
+    }
   if (tid == 0) fail = 0;
   __syncthreads();
   for (int k = 0; k < bj; ++k) {
-    if (tid == 0) {
-      const float p = L[k][k];
+    const int kb = k >> 3, kr = k & 7;
+    if (ty == kb && tx == kb) {          // pivot owner
+      float p = 0.f;
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        if (r == kr) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c)
+            if (c == kr) p = a[r][c];
+        }
       if (!(p > 0.f)) {
         fail = 1;
         atomicCAS(info, 0, off + k + 1);
       }
-      L[k][k] = sqrtf(p);
+      dg[k] = sqrtf(p);
     }
     __syncthreads();
     if (fail) return;
-    const float d = L[k][k];
-    for (int i = k + 1 + tid; i < bj; i += 256) L[i][k] = L[i][k] / d;
+    const float d = dg[k];
+    if (tx == kb) {                      // owners of column k
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        if (c == kr) {
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            const int i = i0 + r;
+            if (i > k) a[r][c] = a[r][c] / d;
+            else if (i == k) a[r][c] = d;
+            col[i] = i > k ? a[r][c] : 0.f;
+          }
+        }
+    }
     __syncthreads();
-    const int m = bj - k - 1;
-    for (int idx = tid; idx < m * m; idx += 256) {
-      const int ii = idx / m, cc = idx % m;
-      if (cc <= ii) {
-        const int i = k + 1 + ii, c = k + 1 + cc;
-        L[i][c] = L[i][c] - L[i][k] * L[c][k];
+    if (j0 + 7 > k && i0 + 7 > k) {      // trailing rank-1 update
+      float ci[8], cj[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) ci[r] = col[i0 + r];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) cj[c] = col[j0 + c];
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const int i = i0 + r, j = j0 + c;
+          if (j > k && j <= i) a[r][c] = a[r][c] - ci[r] * cj[c];
+        }
+    }
+  }
+  // a now holds L (lower).  X = L^-1: right-looking forward substitution.
+  float x[8][8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) x[r][c] = (i0 + r == j0 + c) ? 1.f : 0.f;
+  for (int k = 0; k < bj; ++k) {
+    const int kb = k >> 3, kr = k & 7;
+    __syncthreads();                     // previous step's readers are done
+    if (ty == kb) {                      // owners of row k of X: scale, publish
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        if (r == kr) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const int j = j0 + c;
+            if (j <= k) x[r][c] = x[r][c] / dg[k];
+            row[j] = j <= k ? x[r][c] : 0.f;
+          }
+        }
+    }
+    if (tx == kb) {                      // owners of column k of L: publish
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        if (c == kr) {
+#pragma unroll
+          for (int r = 0; r < 8; ++r) col[i0 + r] = (i0 + r > k) ? a[r][c] : 0.f;
+        }
+    }
+    __syncthreads();
+    if (i0 + 7 > k && j0 <= k) {
+      float ci[8], rj[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) ci[r] = col[i0 + r];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) rj[c] = row[j0 + c];
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const int i = i0 + r, j = j0 + c;
+          if (i > k && j <= k) x[r][c] = x[r][c] - ci[r] * rj[c];
+        }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int i = i0 + r, j = j0 + c;
+      if (i < bj && j < bj) {
+        const float v = j <= i ? x[r][c] : 0.f;
+        D[i * NB + j] = v;
+        A[(int64_t)(off + i) * lda + off + j] = v;
       }
     }
-    __syncthreads();
-  }
-  // X = L^-1 by right-looking forward substitution on the identity
-  for (int k = 0; k < bj; ++k) {
-    const float d = L[k][k];
-    for (int c = tid; c <= k; c += 256) X[k][c] = X[k][c] / d;
-    __syncthreads();
-    const int m = bj - k - 1, w = k + 1;
-    for (int idx = tid; idx < m * w; idx += 256) {
-      const int i = k + 1 + idx / w, c = idx % w;
-      X[i][c] = X[i][c] - L[i][k] * X[k][c];
-    }
-    __syncthreads();
-  }
-  for (int idx = tid; idx < bj * bj; idx += 256) {
-    const int i = idx / bj, c = idx % bj;
-    const float v = c <= i ? X[i][c] : 0.f;
-    D[i * NB + c] = v;
-    A[(int64_t)(off + i) * lda + off + c] = v;
-  }
 }
 
 static inline unsigned nblocks(int64_t n) { return (unsigned)((n + 255) / 256); }

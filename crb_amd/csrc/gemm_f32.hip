@@ -7,75 +7,135 @@
 // fp32 MFMA with fp32 accumulation.
 //
 // Tiling: 128x128 output tile per 256-thread workgroup (4 wavefronts in a
-// 2x2 arrangement, 64x64 each = 4x4 MFMA 16x16 tiles), K staged through LDS
-// 16 at a time in k-major layout so every MFMA operand read is one
-// conflict-free ds_read_b32 per lane.
+// 2x2 arrangement, 64x64 each = 4x4 MFMA 16x16 tiles).  K is staged through
+// double-buffered LDS 32 at a time; every operand keeps its global layout in
+// LDS so a tile moves as float4 copies, and the next K chunk's global loads
+// are in flight while the current chunk's 128 MFMAs per wavefront run.
 #include "gemm_f32.h"
 
 namespace crbq {
 
-constexpr int GB_M = 128, GB_N = 128, GB_K = 16, G_PAD = 4;
+constexpr int GB_M = 128, GB_N = 128, GB_K = 32;
+constexpr int P_MK = GB_K + 4;    // pitch of a row-of-K layout (m- or n-major)
+constexpr int P_KM = GB_M + 4;    // pitch of a K-major layout
+constexpr int T_ELEMS = GB_M * P_MK > GB_K * P_KM ? GB_M * P_MK : GB_K * P_KM;
+
+// Load the float4 at (row, col..col+3) of a row-major matrix, zero-filling
+// anything outside rows x cols.
+__device__ __forceinline__ float4 ld4(const float* p, int64_t ld, int row, int col, int rows,
+                                      int cols, bool vec) {
+  if (row >= rows) return make_float4(0.f, 0.f, 0.f, 0.f);
+  const float* q = p + (int64_t)row * ld + col;
+  if (vec && col + 3 < cols) return *(const float4*)q;
+  float4 v;
+  v.x = col + 0 < cols ? q[0] : 0.f;
+  v.y = col + 1 < cols ? q[1] : 0.f;
+  v.z = col + 2 < cols ? q[2] : 0.f;
+  v.w = col + 3 < cols ? q[3] : 0.f;
+  return v;
+}
+
+// Tile of op(X) for K chunk k0.  KMAJ: X is stored [k][mn] (row = k);
+// otherwise X is stored [mn][k].  Thread f-th float4 -> (row, col).
+template <bool KMAJ>
+__device__ __forceinline__ void load_tile(const float* X, int64_t ld, int mn0, int k0, int MN,
+                                          int K, bool vec, float4 (&r)[4]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int f = tid + 256 * e;
+    if (KMAJ) {
+      const int k = f >> 5, c = (f & 31) * 4;
+      r[e] = ld4(X, ld, k0 + k, mn0 + c, K, MN, vec);
+    } else {
+      const int m = f >> 3, c = (f & 7) * 4;
+      r[e] = ld4(X, ld, mn0 + m, k0 + c, MN, K, vec);
+    }
+  }
+}
+
+template <bool KMAJ>
+__device__ __forceinline__ void store_tile(float* S, const float4 (&r)[4]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int f = tid + 256 * e;
+    if (KMAJ) {
+      const int k = f >> 5, c = (f & 31) * 4;
+      *(float4*)&S[k * P_KM + c] = r[e];
+    } else {
+      const int m = f >> 3, c = (f & 7) * 4;
+      *(float4*)&S[m * P_MK + c] = r[e];
+    }
+  }
+}
 
 template <bool TA, bool TB, bool LOWER>
 __global__ __launch_bounds__(256) void k_sgemm(
     int M, int N, int K, float alpha, const float* A, int64_t lda,
     const float* B, int64_t ldb, float beta, float* C,
-    int64_t ldc, const int* __restrict__ stop) {
+    int64_t ldc, const int* __restrict__ stop, int va, int vb) {
   if (stop && *stop) return;
   const int m0 = blockIdx.y * GB_M, n0 = blockIdx.x * GB_N;
   if (LOWER && n0 > m0 + GB_M - 1) return;  // tile entirely above diagonal
-  __shared__ float As[GB_K][GB_M + G_PAD];
-  __shared__ float Bs[GB_K][GB_N + G_PAD];
+  __shared__ __attribute__((aligned(16))) float As[2][T_ELEMS];
+  __shared__ __attribute__((aligned(16))) float Bs[2][T_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int c16 = lane & 15, kq = lane >> 4;
+  // A is K-major in memory iff TA; B is K-major iff !TB
+  constexpr bool AK = TA, BK = !TB;
   f4_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = 0; k0 < K; k0 += GB_K) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int idx = tid + 256 * e;
-      int m, k;
-      if (TA) { k = idx >> 7; m = idx & 127; }
-      else    { m = idx >> 4; k = idx & 15; }
-      const int gm = m0 + m, gk = k0 + k;
-      float v = 0.f;
-      if (gm < M && gk < K) v = TA ? A[(int64_t)gk * lda + gm] : A[(int64_t)gm * lda + gk];
-      As[k][m] = v;
+  const int nch = (K + GB_K - 1) / GB_K;
+  float4 ra[4], rb[4];
+  if (nch > 0) {
+    load_tile<AK>(A, lda, m0, 0, M, K, va, ra);
+    load_tile<BK>(B, ldb, n0, 0, N, K, vb, rb);
+    store_tile<AK>(As[0], ra);
+    store_tile<BK>(Bs[0], rb);
+  }
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < nch) {
+      load_tile<AK>(A, lda, m0, (c + 1) * GB_K, M, K, va, ra);
+      load_tile<BK>(B, ldb, n0, (c + 1) * GB_K, N, K, vb, rb);
     }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int idx = tid + 256 * e;
-      int n, k;
-      if (TB) { n = idx >> 4; k = idx & 15; }
-      else    { k = idx >> 7; n = idx & 127; }
-      const int gn = n0 + n, gk = k0 + k;
-      float v = 0.f;
-      if (gn < N && gk < K) v = TB ? B[(int64_t)gn * ldb + gk] : B[(int64_t)gk * ldb + gn];
-      Bs[k][n] = v;
-    }
-    __syncthreads();
+    const float* as = As[buf];
+    const float* bs = Bs[buf];
 #pragma unroll
     for (int kk = 0; kk < GB_K; kk += 4) {
-      const int kr = kk + (lane >> 4), c16 = lane & 15;
+      const int k = kk + kq;
       float a[4], b[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = As[kr][wm + i * 16 + c16];
+      for (int i = 0; i < 4; ++i) {
+        const int m = wm + i * 16 + c16;
+        a[i] = AK ? as[k * P_KM + m] : as[m * P_MK + k];
+      }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = Bs[kr][wn + j * 16 + c16];
+      for (int j = 0; j < 4; ++j) {
+        const int n = wn + j * 16 + c16;
+        b[j] = BK ? bs[k * P_KM + n] : bs[n * P_MK + k];
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
     }
+    if (c + 1 < nch) {
+      store_tile<AK>(As[buf ^ 1], ra);
+      store_tile<BK>(Bs[buf ^ 1], rb);
+    }
     __syncthreads();
   }
   // D[row][col]: col = lane%16, row = 4*(lane/16) + r.
-  const int c16 = lane & 15, r4 = (lane >> 4) * 4;
+  const int r4 = kq * 4;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -92,6 +152,10 @@ __global__ __launch_bounds__(256) void k_sgemm(
       }
 }
 
+static inline bool vec_ok(const float* p, int64_t ld) {
+  return ((((uintptr_t)p) & 15) == 0) && ((ld & 3) == 0);
+}
+
 int sgemm_launch(bool ta, bool tb, bool lower, int64_t M, int64_t N, int64_t K,
                  float alpha, const float* A, int64_t lda, const float* B,
                  int64_t ldb, float beta, float* C, int64_t ldc,
@@ -101,10 +165,11 @@ int sgemm_launch(bool ta, bool tb, bool lower, int64_t M, int64_t N, int64_t K,
   dim3 grid((unsigned)((N + GB_N - 1) / GB_N), (unsigned)((M + GB_M - 1) / GB_M));
   if (grid.y > 65535) return CRBQ_ERR_ARG;
   const int m = (int)M, n = (int)N, k = (int)K;
+  const int va = vec_ok(A, lda), vb = vec_ok(B, ldb);
 #define CRBQ_GEMM_CASE(TA_, TB_, LO_)                                              \
   if (ta == TA_ && tb == TB_ && lower == LO_) {                                    \
     k_sgemm<TA_, TB_, LO_><<<grid, 256, 0, s>>>(m, n, k, alpha, A, lda, B, ldb,    \
-                                                beta, C, ldc, stop);               \
+                                                beta, C, ldc, stop, va, vb);       \
     CRBQ_LAUNCH_CHECK();                                                           \
     return CRBQ_OK;                                                                \
   }

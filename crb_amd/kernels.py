@@ -33,8 +33,10 @@ def hessian_accum(X: torch.Tensor, S: torch.Tensor) -> None:
         X = X.float()
     T, C = X.shape
     lib = _lib.ready(X.device)
+    nb = lib.crbq_hessian_workspace_size(T, C) if S.stride(0) == C else 0
+    ws = _ws(nb, X.device) if nb else None
     check(lib.crbq_hessian_accum(X.data_ptr(), _lib.DTYPES[X.dtype], T, X.stride(0), C,
-                                 S.data_ptr(), S.stride(0), stream_of(S)),
+                                 S.data_ptr(), S.stride(0), ptr(ws), nb, stream_of(S)),
           "crbq_hessian_accum")
 
 

@@ -97,9 +97,14 @@ int         crbq_set_percentiles(const float* q81);
  * fp32 C x C matrix S (row stride lds).  f16/bf16 products are exact and
  * accumulate in fp32 on MFMA; fp32 inputs use the fp32 MFMA.
  * The reference's running rescale H *= n/(n+b); H += (2/n) X^T X is applied
- * once, in crbq_hessian_finalize, which gives the same H up to rounding. */
+ * once, in crbq_hessian_finalize, which gives the same H up to rounding.
+ * ws (optional, crbq_hessian_workspace_size bytes; may be NULL) holds
+ * per-split partial sums when the token range is split across workgroups
+ * to fill the GPU (small C); they are added to S in a fixed order. */
+size_t crbq_hessian_workspace_size(int64_t ntok, int64_t C);
 int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_t ldx,
-                       int64_t C, float* S, int64_t lds, void* stream);
+                       int64_t C, float* S, int64_t lds, void* ws, size_t ws_bytes,
+                       void* stream);
 /* H[i,j] = scale * S[min(i,j), max(i,j)] for all i, j (H may alias S). */
 int crbq_hessian_finalize(const float* S, int64_t lds, int64_t C, float scale,
                           float* H, int64_t ldh, void* stream);
