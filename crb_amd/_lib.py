@@ -66,6 +66,10 @@ _SIGS = {
     "crbq_hinv_upper": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, ctypes.c_float, c_vp,
                                 c_i64, c_vp, c_size, ctypes.POINTER(c_i32),
                                 ctypes.POINTER(c_i32), c_vp]),
+    "crbq_hinv_upper_async": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, ctypes.c_float,
+                                      c_vp, c_i64, c_vp, c_size, c_vp]),
+    "crbq_hinv_upper_finish": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_size,
+                                       ctypes.POINTER(c_i32), ctypes.POINTER(c_i32), c_vp]),
     "crbq_fasterquant_workspace_size": (c_size, [c_i64, c_i64, ctypes.POINTER(CrbqParams)]),
     "crbq_fasterquant": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64,
                                  ctypes.POINTER(CrbqParams), c_vp, c_vp, c_i64, c_vp, c_vp,

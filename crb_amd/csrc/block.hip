@@ -35,7 +35,6 @@ constexpr int UPMAX = 64;    // largest supported up_lim
 constexpr int CS_RPW = 32;   // rows per workgroup in k_colscore
 constexpr int Q_RPW = 16;    // rows per workgroup in the quantile passes
 constexpr int PA_RPW = 13;   // rows per workgroup in phase A (13*49 = 637 items)
-constexpr int PC_RPW = 7;    // rows per workgroup in phase C (7*81 = 567 items)
 constexpr int PX_THREADS = 128;
 constexpr int CS_MAXWG = 256;  // colscore partials (grid-stride over row groups)
 constexpr int PX_MAXWG = 1024; // phase A / C partials
@@ -524,92 +523,178 @@ __device__ __forceinline__ float np_lerp(float a, float b, float t) {
 
 // ---------------------------------------------------------------------------
 // phase C: order-1 errors of the two bell groups for each of the 81 split
-// candidates (utils/autosearch.py:71-80)
+// candidates (utils/autosearch.py:71-80), in closed form.
+//
+// One wavefront per row: the row's non-salient targets are bitonic-sorted
+// (2 per lane) and fp64 prefix sums of v and v^2 are formed.  A group
+// {|v| < p} or {|v| >= p} is then one or two ranges of the sorted row, and
+// order-1 residual binarization of a group is
+//   mu = sum v / n,  alpha = sum |v - mu| / n,
+//   q(v) = mu + alpha*sign(v - mu),  err = sum (v - q(v))^2,
+// where the ranges v < mu, v == mu, v > mu come from binary searches with
+// the same fp32 comparisons the elementwise code makes, and every sum is a
+// difference of prefix sums: sum (v - t)^2 = Q - 2 t S + n t^2.
 // ---------------------------------------------------------------------------
-__device__ double phase_c_item(const float* __restrict__ x, const bool* __restrict__ sal,
-                               int nc, float thr) {
-  double s1 = 0.0, s2 = 0.0;
-  float n1 = 0.f, n2 = 0.f;
-  for (int c = 0; c < nc; ++c) {
-    if (sal[c]) continue;
-    const float v = x[c];
-    const bool g2 = fabsf(v) >= thr;
-    s1 += g2 ? 0.0 : (double)v;
-    s2 += g2 ? (double)v : 0.0;
-    n1 += g2 ? 0.f : 1.f;
-    n2 += g2 ? 1.f : 0.f;
+constexpr int PC_WAVES = 4;
+
+struct SortedRow {
+  float v[NCMAX];        // ascending; first n valid
+  double S[NCMAX + 1];   // exclusive prefix sums of v
+  double Q[NCMAX + 1];   // exclusive prefix sums of v^2
+  int n;
+};
+
+// first index in [0, n) with v[i] >= x (lower bound) / v[i] > x (upper bound)
+__device__ __forceinline__ int lbound(const float* v, int n, float x) {
+  int lo = 0, hi = n;
+  while (lo < hi) { const int m = (lo + hi) >> 1; if (v[m] < x) lo = m + 1; else hi = m; }
+  return lo;
+}
+__device__ __forceinline__ int ubound(const float* v, int n, float x) {
+  int lo = 0, hi = n;
+  while (lo < hi) { const int m = (lo + hi) >> 1; if (v[m] <= x) lo = m + 1; else hi = m; }
+  return lo;
+}
+
+struct Stat { double n, s, q; };
+__device__ __forceinline__ Stat rstat(const SortedRow& r, int l, int h) {
+  if (h <= l) return Stat{0.0, 0.0, 0.0};
+  return Stat{(double)(h - l), r.S[h] - r.S[l], r.Q[h] - r.Q[l]};
+}
+__device__ __forceinline__ double sqdev(const Stat& a, double t) {   // sum (v - t)^2
+  return a.q - 2.0 * t * a.s + a.n * t * t;
+}
+
+// order-1 error of the group made of sorted ranges [l1,h1) and [l2,h2)
+__device__ double group_err1(const SortedRow& r, int l1, int h1, int l2, int h2) {
+  const int n = max(h1 - l1, 0) + max(h2 - l2, 0);
+  if (n == 0) return 0.0;
+  const Stat a1 = rstat(r, l1, h1), a2 = rstat(r, l2, h2);
+  const float nf = (float)n;
+  const float mu = (float)(a1.s + a2.s) / nf;
+  const int lb = lbound(r.v, r.n, mu), ub = ubound(r.v, r.n, mu);
+  double sabs = 0.0, err = 0.0;
+  Stat parts[2][3];
+  const int L[2] = {l1, l2}, Hh[2] = {h1, h2};
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int l = L[g], h = Hh[g];
+    const int b1 = min(max(lb, l), max(h, l)), b2 = min(max(ub, l), max(h, l));
+    parts[g][0] = rstat(r, l, b1);      // v < mu
+    parts[g][1] = rstat(r, b1, b2);     // v == mu
+    parts[g][2] = rstat(r, b2, h);      // v > mu
+    sabs += (parts[g][2].s - parts[g][2].n * (double)mu) + (parts[g][0].n * (double)mu - parts[g][0].s);
   }
-  const float m1 = n1 > 0.f ? (float)s1 / n1 : 0.f;
-  const float m2 = n2 > 0.f ? (float)s2 / n2 : 0.f;
-  s1 = 0.0; s2 = 0.0;
-  for (int c = 0; c < nc; ++c) {
-    if (sal[c]) continue;
-    const float v = x[c];
-    const bool g2 = fabsf(v) >= thr;
-    const double a = (double)fabsf(v - (g2 ? m2 : m1));
-    s1 += g2 ? 0.0 : a;
-    s2 += g2 ? a : 0.0;
-  }
-  const float a1 = n1 > 0.f ? (float)s1 / n1 : 0.f;
-  const float a2 = n2 > 0.f ? (float)s2 / n2 : 0.f;
-  double err = 0.0;
-  for (int c = 0; c < nc; ++c) {
-    if (sal[c]) continue;
-    const float v = x[c];
-    const bool g2 = fabsf(v) >= thr;
-    const float m = g2 ? m2 : m1, a = g2 ? a2 : a1;
-    const float cc = v - m;
-    float q = tsign(cc) * a;
-    q = q + m;
-    const float df = v - q;
-    err += (double)(df * df);
-  }
+  const float alpha = (float)sabs / nf;
+  const float hi = alpha + mu, lo = -alpha + mu;
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+    err += sqdev(parts[g][0], (double)lo) + sqdev(parts[g][1], (double)mu) +
+           sqdev(parts[g][2], (double)hi);
   return err;
 }
 
-__global__ __launch_bounds__(PX_THREADS) void k_phase_c(
+// bitonic sort of 128 values held 2 per lane (position lane + 64*slot)
+__device__ __forceinline__ void wave_sort128(float& x0, float& x1) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 2; k <= 128; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j == 64) {                       // partner is the other slot of this lane
+        const bool up = ((lane & k) == 0);  // k == 128: always ascending
+        const float a = fminf(x0, x1), b = fmaxf(x0, x1);
+        x0 = up ? a : b;
+        x1 = up ? b : a;
+      } else {
+#pragma unroll
+        for (int slot = 0; slot < 2; ++slot) {
+          float& x = slot ? x1 : x0;
+          const int pos = lane + 64 * slot;
+          const float y = __shfl_xor(x, j, CRBQ_WAVE);
+          const bool up = ((pos & k) == 0);
+          const bool lower = (pos & j) == 0;
+          x = (lower == up) ? fminf(x, y) : fmaxf(x, y);
+        }
+      }
+    }
+  }
+}
+
+// exclusive fp64 prefix sums of the sorted row into r.S / r.Q
+__device__ __forceinline__ void wave_prefix(SortedRow& r, float x0, float x1, int n) {
+  const int lane = threadIdx.x & 63;
+  double s0 = lane < n ? (double)x0 : 0.0, s1 = lane + 64 < n ? (double)x1 : 0.0;
+  double q0 = s0 * s0, q1 = s1 * s1;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {       // inclusive scans within each slot
+    const double a = __shfl_up(s0, o, CRBQ_WAVE), b = __shfl_up(s1, o, CRBQ_WAVE);
+    const double c = __shfl_up(q0, o, CRBQ_WAVE), d = __shfl_up(q1, o, CRBQ_WAVE);
+    if (lane >= o) { s0 += a; s1 += b; q0 += c; q1 += d; }
+  }
+  const double tS = __shfl(s0, 63, CRBQ_WAVE), tQ = __shfl(q0, 63, CRBQ_WAVE);
+  s1 += tS;
+  q1 += tQ;
+  r.S[lane + 1] = s0;
+  r.S[lane + 65] = s1;
+  r.Q[lane + 1] = q0;
+  r.Q[lane + 65] = q1;
+  if (lane == 0) { r.S[0] = 0.0; r.Q[0] = 0.0; }
+  r.v[lane] = x0;
+  r.v[lane + 64] = x1;
+}
+
+__global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
     const float* __restrict__ W, int64_t ldw, int R, int nc,
     const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
-  __shared__ float xs[PC_RPW][NCMAX];
-  __shared__ bool sal[NCMAX];
-  __shared__ float d2s[NCMAX];
+  __shared__ SortedRow rows[PC_WAVES];
   __shared__ float pv[NQ];
-  __shared__ double errs[PC_RPW][NQ];
+  __shared__ double errs[PC_WAVES][NQ];
   __shared__ double acc[NQ];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int istar = s.ctrl->istar;
-  for (int i = tid; i < NCMAX; i += PX_THREADS) {
-    sal[i] = s.rank[i] < istar;
-    if (i < nc) { const float dg = U[(int64_t)i * ldu + i]; d2s[i] = dg * dg; }
-  }
-  for (int k = tid; k < NQ; k += PX_THREADS) {
+  for (int k = tid; k < NQ; k += 64 * PC_WAVES) {
     pv[k] = np_lerp(s.tval[2 * k], s.tval[2 * k + 1], s.gam[k]);
     if (blockIdx.x == 0) s.pvals[k] = pv[k];
     acc[k] = 0.0;
   }
-  for (int r0 = blockIdx.x * PC_RPW; r0 < R; r0 += gridDim.x * PC_RPW) {
-    const int nr = min(PC_RPW, R - r0);
-    __syncthreads();
-    for (int i = tid; i < PC_RPW * NCMAX; i += PX_THREADS) {
-      const int rr = i / NCMAX, c = i % NCMAX;
-      xs[rr][c] = (rr < nr && c < nc) ? target_of(W[(int64_t)(r0 + rr) * ldw + c], d2s[c], metric)
-                                      : 0.f;
+  const int c0 = lane, c1 = lane + 64;
+  const bool in0 = c0 < nc && s.rank[c0] >= istar, in1 = c1 < nc && s.rank[c1] >= istar;
+  float d20 = 1.f, d21 = 1.f;
+  if (c0 < nc) { const float dg = U[(int64_t)c0 * ldu + c0]; d20 = dg * dg; }
+  if (c1 < nc) { const float dg = U[(int64_t)c1 * ldu + c1]; d21 = dg * dg; }
+  const int n = (int)wave_sum_f((in0 ? 1.f : 0.f) + (in1 ? 1.f : 0.f));
+  SortedRow& sr = rows[wv];
+  for (int r0 = blockIdx.x * PC_WAVES; r0 < R; r0 += gridDim.x * PC_WAVES) {
+    const int row = r0 + wv;
+    __syncthreads();                       // previous rows' errs consumed
+    if (row < R) {
+      float x0 = in0 ? target_of(W[(int64_t)row * ldw + c0], d20, metric) : INFINITY;
+      float x1 = in1 ? target_of(W[(int64_t)row * ldw + c1], d21, metric) : INFINITY;
+      wave_sort128(x0, x1);
+      wave_prefix(sr, x0, x1, n);
+      if (lane == 0) sr.n = n;
     }
     __syncthreads();
-    const int items = nr * NQ;
-    for (int it = tid; it < items; it += PX_THREADS) {
-      const int rr = it / NQ, k = it % NQ;
-      errs[rr][k] = phase_c_item(xs[rr], sal, nc, pv[k]);
+    if (row < R) {
+      for (int k = lane; k < NQ; k += 64) {
+        const float thr = pv[k];
+        // M1 = {-thr < v < thr} = [a, b), M2 = [0, a) + [b, n)
+        const int a = ubound(sr.v, n, -thr);
+        const int b = max(lbound(sr.v, n, thr), a);
+        errs[wv][k] = group_err1(sr, a, b, 0, 0) + group_err1(sr, 0, a, b, n);
+      }
     }
     __syncthreads();
-    for (int k = tid; k < NQ; k += PX_THREADS) {
+    const int nr = min(PC_WAVES, R - r0);
+    for (int k = tid; k < NQ; k += 64 * PC_WAVES) {
       double e = acc[k];
-      for (int rr = 0; rr < nr; ++rr) e += errs[rr][k];
+      for (int w = 0; w < nr; ++w) e += errs[w][k];
       acc[k] = e;
     }
   }
   __syncthreads();
-  for (int k = tid; k < NQ; k += PX_THREADS) s.partc[(size_t)blockIdx.x * 96 + k] = acc[k];
+  for (int k = tid; k < NQ; k += 64 * PC_WAVES) s.partc[(size_t)blockIdx.x * 96 + k] = acc[k];
 }
 
 __global__ __launch_bounds__(1024) void k_reduce_c(int nwg, SearchWs s, crbq_block_trace* tr) {
@@ -718,7 +803,7 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
   const int nwg_cs = (int)std::min<int64_t>(cdiv(R, CS_RPW), CS_MAXWG);
   const int nwg_q = (int)cdiv(R, Q_RPW);
   const int nwg_a = (int)std::min<int64_t>(cdiv(R, PA_RPW), PX_MAXWG);
-  const int nwg_c = (int)std::min<int64_t>(cdiv(R, PC_RPW), PX_MAXWG);
+  const int nwg_c = (int)std::min<int64_t>(cdiv(R, PC_WAVES), PX_MAXWG);
   k_colscore<<<nwg_cs, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_topk<<<1, 1024, 0, st>>>(nc, nwg_cs, s);
   k_phase_a<<<nwg_a, PX_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, ncand, s);
@@ -729,7 +814,7 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
   k_qscan2<<<NT, 256, 0, st>>>(s);
   k_qpass3<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_qscan3<<<NT, 256, 0, st>>>(s);
-  k_phase_c<<<nwg_c, PX_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
+  k_phase_c<<<nwg_c, 64 * PC_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_reduce_c<<<1, 1024, 0, st>>>(nwg_c, s, tr);
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
@@ -838,10 +923,17 @@ extern "C" int crbq_set_percentiles(const float* q81) {
   return set_q_table(q81);
 }
 
+// Column blocks per super-block of the two-level GPTQ update: inside a
+// super-block each block's error updates only the rest of the super-block
+// (K = blocksize); at its end one GEMM with K = SB_BLOCKS * blocksize updates
+// every later column.  Same sums as the reference's per-block
+// W[:, ed:] -= Err @ U[st:ed, ed:] (bigptq.py:264), regrouped.
+constexpr int SB_BLOCKS = 8;
+
 extern "C" size_t crbq_fasterquant_workspace_size(int64_t R, int64_t C, const crbq_params* p) {
-  (void)C;
   const int bs = p ? p->blocksize : NCMAX;
-  return search_ws_bytes(R) + (size_t)R * (size_t)bs * sizeof(float) + 512;
+  const int64_t sb = std::min<int64_t>((int64_t)SB_BLOCKS * bs, C);
+  return search_ws_bytes(R) + (size_t)R * (size_t)sb * sizeof(float) + 512;
 }
 
 extern "C" int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw, const float* U,
@@ -854,10 +946,11 @@ extern "C" int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw, con
   if (R * (int64_t)NCMAX >= (1 << 24)) return CRBQ_ERR_ARG;
   if (masks && ldm < C) return CRBQ_ERR_ARG;
   const int bs = p->blocksize;
+  const int64_t SB = std::min<int64_t>((int64_t)SB_BLOCKS * bs, C);
   WsCarver c(ws, ws_bytes);
   SearchWs s;
   carve_search(c, R, s);
-  float* err = c.take<float>((size_t)R * bs);
+  float* err = c.take<float>((size_t)R * SB);
   if (!c.ok()) return CRBQ_ERR_WORKSPACE;
   st = ensure_q_table();
   if (st) return st;
@@ -873,32 +966,41 @@ extern "C" int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw, con
   k.sym = false;
   k.skip = false;
   k.iters = p->refine_iters;
+  const bool gptq = !p->disable_gptq;
   int bi = 0;
-  for (int64_t st0 = 0; st0 < C; st0 += bs, ++bi) {
-    const int nc = (int)std::min<int64_t>(bs, C - st0);
-    float* Wb = W + st0;
-    const float* Ub = U + st0 * ldu + st0;
-    crbq_block_trace* tr = traces ? traces + bi : nullptr;
-    if (p->partition == 3) {
-      st = search_block(Wb, ldw, (int)R, nc, Ub, ldu, p->metric, p->up_lim, s, tr, hs);
-      if (st) return st;
+  for (int64_t sb0 = 0; sb0 < C; sb0 += SB) {
+    const int64_t sb1 = std::min<int64_t>(sb0 + SB, C);
+    for (int64_t st0 = sb0; st0 < sb1; st0 += bs, ++bi) {
+      const int nc = (int)std::min<int64_t>(bs, sb1 - st0);
+      float* Wb = W + st0;
+      const float* Ub = U + st0 * ldu + st0;
+      crbq_block_trace* tr = traces ? traces + bi : nullptr;
+      if (p->partition == 3) {
+        st = search_block(Wb, ldw, (int)R, nc, Ub, ldu, p->metric, p->up_lim, s, tr, hs);
+        if (st) return st;
+      }
+      QuantArgs a;
+      a.W = Wb; a.ldw = ldw; a.R = (int)R; a.nc = nc;
+      a.U = Ub; a.ldu = ldu;
+      a.metric = p->metric; a.method = p->method; a.partition = p->partition;
+      for (int g = 0; g < 3; ++g) a.orders[g] = p->orders[g];
+      a.k = k;
+      a.gptq = gptq;
+      a.err = err + (st0 - sb0); a.lde = SB;
+      a.losses = losses;
+      a.masks = masks ? masks + st0 : nullptr; a.ldm = ldm;
+      k_quantize<2><<<(unsigned)cdiv(R, 4), 256, 0, hs>>>(a, s);
+      CRBQ_LAUNCH_CHECK();
+      const int64_t ed = st0 + nc;
+      if (gptq && ed < sb1) {            // rest of this super-block
+        st = sgemm_launch(false, false, false, R, sb1 - ed, nc, -1.f, a.err, SB,
+                          U + st0 * ldu + ed, ldu, 1.f, W + ed, ldw, nullptr, hs);
+        if (st) return st;
+      }
     }
-    QuantArgs a;
-    a.W = Wb; a.ldw = ldw; a.R = (int)R; a.nc = nc;
-    a.U = Ub; a.ldu = ldu;
-    a.metric = p->metric; a.method = p->method; a.partition = p->partition;
-    for (int g = 0; g < 3; ++g) a.orders[g] = p->orders[g];
-    a.k = k;
-    a.gptq = !p->disable_gptq;
-    a.err = err; a.lde = bs;
-    a.losses = losses;
-    a.masks = masks ? masks + st0 : nullptr; a.ldm = ldm;
-    k_quantize<2><<<(unsigned)cdiv(R, 4), 256, 0, hs>>>(a, s);
-    CRBQ_LAUNCH_CHECK();
-    const int64_t ed = st0 + nc;
-    if (a.gptq && ed < C) {
-      st = sgemm_launch(false, false, false, R, C - ed, nc, -1.f, err, bs,
-                        U + st0 * ldu + ed, ldu, 1.f, W + ed, ldw, nullptr, hs);
+    if (gptq && sb1 < C) {               // every later column, K = sb1 - sb0
+      st = sgemm_launch(false, false, false, R, C - sb1, sb1 - sb0, -1.f, err, SB,
+                        U + sb0 * ldu + sb1, ldu, 1.f, W + sb1, ldw, nullptr, hs);
       if (st) return st;
     }
   }

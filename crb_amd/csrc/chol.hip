@@ -102,123 +102,175 @@ __global__ __launch_bounds__(256) void k_fallback_u(const float* __restrict__ H,
   U[(int64_t)i * ldu + j] = v;
 }
 
-// Diagonal block: Cholesky and triangular inverse of one NB x NB block.
-// 256 threads as a 16 x 16 grid; thread (ty, tx) keeps the 8 x 8 sub-block
-// rows ty*8.., cols tx*8.. in registers.  Right-looking: step k takes the
-// pivot from its owner, scales column k, publishes it through LDS and every
-// thread applies the rank-1 update to its own lower-triangle entries.  The
-// inverse is the same sweep on the identity (X = L^-1, forward substitution).
+// Diagonal block: Cholesky and triangular inverse of one NB x NB block,
+// blocked by 8.  256 threads as a 16 x 16 grid; thread (ty, tx) keeps the
+// 8 x 8 sub-block rows ty*8.., cols tx*8.. in registers.  Step kb of the
+// factorization: the owner of diagonal block (kb, kb) factors and inverts
+// it in registers; the owners of column kb form the panel
+// P_I = A_I,kb D_kb^T; every lower block right of column kb takes the
+// rank-8 update A_IJ -= P_I P_J^T.  The inverse X = L^-1 is the same
+// right-looking sweep on the identity: X_kb,J = D_kb B_kb,J, then
+// B_I,J -= L_I,kb X_kb,J.  Rows past bj are padded with the identity.
+__device__ __forceinline__ void chol8(float (&a)[8][8], float (&x)[8][8], int& bad) {
+  bad = -1;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float p = a[k][k];
+    if (!(p > 0.f) && bad < 0) bad = k;
+    const float d = sqrtf(p), di = 1.f / d;
+    a[k][k] = d;
+#pragma unroll
+    for (int r = k + 1; r < 8; ++r) a[r][k] = a[r][k] * di;
+#pragma unroll
+    for (int c = k + 1; c < 8; ++c)
+#pragma unroll
+      for (int r = c; r < 8; ++r) a[r][c] = a[r][c] - a[r][k] * a[c][k];
+  }
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) x[r][c] = r == c ? 1.f : 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float di = 1.f / a[k][k];
+#pragma unroll
+    for (int c = 0; c <= k; ++c) x[k][c] = x[k][c] * di;
+#pragma unroll
+    for (int r = k + 1; r < 8; ++r)
+#pragma unroll
+      for (int c = 0; c <= k; ++c) x[r][c] = x[r][c] - a[r][k] * x[k][c];
+  }
+}
+
 __global__ __launch_bounds__(256) void k_potrf_diag(float* A, int64_t lda, int off, int bj,
                                                     float* D, int* info) {
   if (*info) return;
-  __shared__ float col[NB];
-  __shared__ float row[NB];
-  __shared__ float dg[NB];
+  __shared__ __attribute__((aligned(16))) float pan[NB][8];     // column panel of L
+  __shared__ __attribute__((aligned(16))) float Dk[NB / 8][8][8];  // inverses of diag blocks
+  __shared__ __attribute__((aligned(16))) float xr[8][NB];      // row panel of X
   __shared__ int fail;
   const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
   const int i0 = ty * 8, j0 = tx * 8;
-  float a[8][8];
+  const int nkb = (bj + 7) / 8;
+  float a[8][8], x[8][8];
 #pragma unroll
   for (int r = 0; r < 8; ++r)
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const int i = i0 + r, j = j0 + c;
-      a[r][c] = (i < bj && j <= i) ? A[(int64_t)(off + i) * lda + off + j] : 0.f;
+      a[r][c] = (i < bj && j <= i) ? A[(int64_t)(off + i) * lda + off + j]
+                                   : (i == j ? 1.f : 0.f);
     }
   if (tid == 0) fail = 0;
   __syncthreads();
-  for (int k = 0; k < bj; ++k) {
-    const int kb = k >> 3, kr = k & 7;
-    if (ty == kb && tx == kb) {          // pivot owner
-      float p = 0.f;
+  for (int kb = 0; kb < nkb; ++kb) {
+    if (ty == kb && tx == kb) {                       // factor + invert the diagonal block
+      int bad;
+      chol8(a, x, bad);
+      if (bad >= 0 && i0 + bad < bj) {
+        fail = 1;
+        atomicCAS(info, 0, off + i0 + bad + 1);
+      }
 #pragma unroll
       for (int r = 0; r < 8; ++r)
-        if (r == kr) {
 #pragma unroll
-          for (int c = 0; c < 8; ++c)
-            if (c == kr) p = a[r][c];
-        }
-      if (!(p > 0.f)) {
-        fail = 1;
-        atomicCAS(info, 0, off + k + 1);
-      }
-      dg[k] = sqrtf(p);
+        for (int c = 0; c < 8; ++c) Dk[kb][r][c] = c <= r ? x[r][c] : 0.f;
     }
     __syncthreads();
     if (fail) return;
-    const float d = dg[k];
-    if (tx == kb) {                      // owners of column k
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-        if (c == kr) {
-#pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            const int i = i0 + r;
-            if (i > k) a[r][c] = a[r][c] / d;
-            else if (i == k) a[r][c] = d;
-            col[i] = i > k ? a[r][c] : 0.f;
-          }
-        }
-    }
-    __syncthreads();
-    if (j0 + 7 > k && i0 + 7 > k) {      // trailing rank-1 update
-      float ci[8], cj[8];
-#pragma unroll
-      for (int r = 0; r < 8; ++r) ci[r] = col[i0 + r];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) cj[c] = col[j0 + c];
+    if (tx == kb && ty > kb) {                        // panel P_I = A_I,kb D_kb^T
+      float p[8][8];
 #pragma unroll
       for (int r = 0; r < 8; ++r)
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-          const int i = i0 + r, j = j0 + c;
-          if (j > k && j <= i) a[r][c] = a[r][c] - ci[r] * cj[c];
+          float v = 0.f;
+#pragma unroll
+          for (int m = 0; m <= c; ++m) v = v + a[r][m] * Dk[kb][c][m];
+          p[r][c] = v;
+        }
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          a[r][c] = p[r][c];
+          pan[i0 + r][c] = p[r][c];
         }
     }
+    __syncthreads();
+    if (ty >= tx && tx > kb) {                        // A_IJ -= P_I P_J^T
+      float pi[8][8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int m = 0; m < 8; ++m) pi[r][m] = pan[i0 + r][m];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float pj[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) pj[m] = pan[j0 + c][m];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          float v = a[r][c];
+#pragma unroll
+          for (int m = 0; m < 8; ++m) v = v - pi[r][m] * pj[m];
+          a[r][c] = v;
+        }
+      }
+    }
   }
-  // a now holds L (lower).  X = L^-1: right-looking forward substitution.
-  float x[8][8];
+  // a: L blocks (I >= J).  X = L^-1, right-looking on the identity.
 #pragma unroll
   for (int r = 0; r < 8; ++r)
 #pragma unroll
     for (int c = 0; c < 8; ++c) x[r][c] = (i0 + r == j0 + c) ? 1.f : 0.f;
-  for (int k = 0; k < bj; ++k) {
-    const int kb = k >> 3, kr = k & 7;
-    __syncthreads();                     // previous step's readers are done
-    if (ty == kb) {                      // owners of row k of X: scale, publish
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-        if (r == kr) {
-#pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            const int j = j0 + c;
-            if (j <= k) x[r][c] = x[r][c] / dg[k];
-            row[j] = j <= k ? x[r][c] : 0.f;
-          }
-        }
-    }
-    if (tx == kb) {                      // owners of column k of L: publish
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-        if (c == kr) {
-#pragma unroll
-          for (int r = 0; r < 8; ++r) col[i0 + r] = (i0 + r > k) ? a[r][c] : 0.f;
-        }
-    }
-    __syncthreads();
-    if (i0 + 7 > k && j0 <= k) {
-      float ci[8], rj[8];
-#pragma unroll
-      for (int r = 0; r < 8; ++r) ci[r] = col[i0 + r];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) rj[c] = row[j0 + c];
+  for (int kb = 0; kb < nkb; ++kb) {
+    __syncthreads();                                  // previous step's readers are done
+    if (ty == kb && tx <= kb) {                       // X_kb,J = D_kb B_kb,J
+      float y[8][8];
 #pragma unroll
       for (int r = 0; r < 8; ++r)
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-          const int i = i0 + r, j = j0 + c;
-          if (i > k && j <= k) x[r][c] = x[r][c] - ci[r] * rj[c];
+          float v = 0.f;
+#pragma unroll
+          for (int m = 0; m <= r; ++m) v = v + Dk[kb][r][m] * x[m][c];
+          y[r][c] = v;
         }
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          x[r][c] = y[r][c];
+          xr[r][j0 + c] = y[r][c];
+        }
+    }
+    if (tx == kb && ty > kb) {                        // publish L_I,kb
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int m = 0; m < 8; ++m) pan[i0 + r][m] = a[r][m];
+    }
+    __syncthreads();
+    if (ty > kb && tx <= kb) {                        // B_I,J -= L_I,kb X_kb,J
+      float li[8][8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int m = 0; m < 8; ++m) li[r][m] = pan[i0 + r][m];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float xc[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) xc[m] = xr[m][j0 + c];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          float v = x[r][c];
+#pragma unroll
+          for (int m = 0; m < 8; ++m) v = v - li[r][m] * xc[m];
+          x[r][c] = v;
+        }
+      }
     }
   }
 #pragma unroll
@@ -304,12 +356,21 @@ extern "C" size_t crbq_hinv_workspace_size(int64_t C) {
   return c.off + 256;
 }
 
-extern "C" int crbq_hinv_upper(float* H, int64_t ldh, int64_t C, float* W, int64_t R,
-                               int64_t ldw, float percdamp, float* U, int64_t ldu, void* ws,
-                               size_t ws_bytes, int* retries, int* fallback, void* stream) {
+static int hinv_check(float* H, int64_t ldh, int64_t C, float* W, int64_t R, int64_t ldw,
+                      float* U, int64_t ldu) {
   if (!H || !U || C <= 0 || ldh < C || ldu < C) return CRBQ_ERR_ARG;
   if (W && (R <= 0 || ldw < C)) return CRBQ_ERR_ARG;
   if (C > (1 << 20)) return CRBQ_ERR_ARG;
+  return CRBQ_OK;
+}
+
+// dead columns, damping and one factorization attempt; U written assuming
+// success (the finish step checks *info and redoes it on failure)
+extern "C" int crbq_hinv_upper_async(float* H, int64_t ldh, int64_t C, float* W, int64_t R,
+                                     int64_t ldw, float percdamp, float* U, int64_t ldu,
+                                     void* ws, size_t ws_bytes, void* stream) {
+  int st = hinv_check(H, ldh, C, W, R, ldw, U, ldu);
+  if (st) return st;
   WsCarver c(ws, ws_bytes);
   HinvWs w;
   carve_hinv(c, C, w);
@@ -324,26 +385,66 @@ extern "C" int crbq_hinv_upper(float* H, int64_t ldh, int64_t C, float* W, int64
   }
   k_damp<<<1, 1024, 0, s>>>(H, ldh, Ci, percdamp, 0, w.scal);      // bigptq.py:109-111
   CRBQ_LAUNCH_CHECK();
+  k_set_int<<<1, 1, 0, s>>>(w.info, 0);
+  k_reverse_lower<<<nblocks(C * C), 256, 0, s>>>(H, ldh, Ci, w.A, C);
+  CRBQ_LAUNCH_CHECK();
+  st = chol_inv_sweep(w.A, C, Ci, w, s);
+  if (st) return st;
+  k_reverse_to_u<<<nblocks(C * C), 256, 0, s>>>(w.A, C, Ci, U, ldu);
+  CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}
+
+// Synchronises `stream`, reads the first attempt's outcome and, if the
+// Cholesky failed, runs the reference's retries and fallback
+// (bigptq.py:114-126) synchronously.
+extern "C" int crbq_hinv_upper_finish(float* H, int64_t ldh, int64_t C, float* U, int64_t ldu,
+                                      void* ws, size_t ws_bytes, int* retries, int* fallback,
+                                      void* stream) {
+  int st = hinv_check(H, ldh, C, nullptr, 0, 0, U, ldu);
+  if (st) return st;
+  WsCarver c(ws, ws_bytes);
+  HinvWs w;
+  carve_hinv(c, C, w);
+  if (!c.ok()) return CRBQ_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  const int Ci = (int)C;
+  int hinfo = 0;
+  CRBQ_HIP(hipMemcpyAsync(&hinfo, w.info, sizeof(int), hipMemcpyDeviceToHost, s));
+  CRBQ_HIP(hipStreamSynchronize(s));
   int nretry = 0;
-  bool ok = false;
-  for (int attempt = 0; attempt < 10; ++attempt) {                // bigptq.py:115-123
-    k_set_int<<<1, 1, 0, s>>>(w.info, 0);
-    k_reverse_lower<<<nblocks(C * C), 256, 0, s>>>(H, ldh, Ci, w.A, C);
-    CRBQ_LAUNCH_CHECK();
-    int st = chol_inv_sweep(w.A, C, Ci, w, s);
-    if (st) return st;
-    int hinfo = 0;
-    CRBQ_HIP(hipMemcpyAsync(&hinfo, w.info, sizeof(int), hipMemcpyDeviceToHost, s));
-    CRBQ_HIP(hipStreamSynchronize(s));
-    if (hinfo == 0) { ok = true; break; }
+  bool ok = hinfo == 0;
+  for (int attempt = 1; !ok && attempt <= 10; ++attempt) {        // bigptq.py:115-123
     ++nretry;
     k_damp<<<1, 1024, 0, s>>>(H, ldh, Ci, 1e-3f, 1, w.scal);
     CRBQ_LAUNCH_CHECK();
+    if (attempt == 10) break;                                       // 10 attempts in all
+    k_set_int<<<1, 1, 0, s>>>(w.info, 0);
+    k_reverse_lower<<<nblocks(C * C), 256, 0, s>>>(H, ldh, Ci, w.A, C);
+    CRBQ_LAUNCH_CHECK();
+    st = chol_inv_sweep(w.A, C, Ci, w, s);
+    if (st) return st;
+    CRBQ_HIP(hipMemcpyAsync(&hinfo, w.info, sizeof(int), hipMemcpyDeviceToHost, s));
+    CRBQ_HIP(hipStreamSynchronize(s));
+    ok = hinfo == 0;
+    if (ok) {
+      k_reverse_to_u<<<nblocks(C * C), 256, 0, s>>>(w.A, C, Ci, U, ldu);
+      CRBQ_LAUNCH_CHECK();
+    }
   }
-  if (ok) k_reverse_to_u<<<nblocks(C * C), 256, 0, s>>>(w.A, C, Ci, U, ldu);
-  else k_fallback_u<<<nblocks(C * C), 256, 0, s>>>(H, ldh, Ci, U, ldu);
-  CRBQ_LAUNCH_CHECK();
+  if (!ok) {
+    k_fallback_u<<<nblocks(C * C), 256, 0, s>>>(H, ldh, Ci, U, ldu);
+    CRBQ_LAUNCH_CHECK();
+  }
   if (retries) *retries = nretry;
   if (fallback) *fallback = ok ? 0 : 1;
   return CRBQ_OK;
+}
+
+extern "C" int crbq_hinv_upper(float* H, int64_t ldh, int64_t C, float* W, int64_t R,
+                               int64_t ldw, float percdamp, float* U, int64_t ldu, void* ws,
+                               size_t ws_bytes, int* retries, int* fallback, void* stream) {
+  int st = crbq_hinv_upper_async(H, ldh, C, W, R, ldw, percdamp, U, ldu, ws, ws_bytes, stream);
+  if (st) return st;
+  return crbq_hinv_upper_finish(H, ldh, C, U, ldu, ws, ws_bytes, retries, fallback, stream);
 }

@@ -73,6 +73,45 @@ def hinv_upper(H: torch.Tensor, W: torch.Tensor | None, percdamp: float = 0.01):
     return U, int(retries.value), bool(fallback.value)
 
 
+class HinvJob:
+    """An inverse-factor computation enqueued with hinv_upper_async."""
+
+    def __init__(self, H, U, ws, stream):
+        self.H, self.U, self.ws, self.stream = H, U, ws, stream
+
+
+def hinv_upper_async(H: torch.Tensor, W: torch.Tensor | None, percdamp: float = 0.01) -> HinvJob:
+    """Enqueue bigptq.py:101-129 on the current stream without waiting."""
+    _dev_check(H, W)
+    if H.stride(1) != 1 or (W is not None and W.stride(1) != 1):
+        raise _lib.CrbqError("hinv_upper works in place on row-major H and W")
+    C = H.shape[0]
+    lib = _lib.ready(H.device)
+    U = torch.empty((C, C), dtype=torch.float32, device=H.device)
+    ws = _ws(lib.crbq_hinv_workspace_size(C), H.device)
+    R = W.shape[0] if W is not None else 0
+    ldw = W.stride(0) if W is not None else 0
+    st = stream_of(H)
+    check(lib.crbq_hinv_upper_async(H.data_ptr(), H.stride(0), C, ptr(W), R, ldw,
+                                    float(percdamp), U.data_ptr(), U.stride(0), ws.data_ptr(),
+                                    ws.numel(), st), "crbq_hinv_upper_async")
+    return HinvJob(H, U, ws, torch.cuda.current_stream(H.device))
+
+
+def hinv_upper_finish(job: HinvJob):
+    """Wait for the job's stream, retry/fallback if needed.  Returns
+    (U, retries, fallback)."""
+    lib = _lib.ready(job.H.device)
+    retries = ctypes.c_int32(0)
+    fallback = ctypes.c_int32(0)
+    C = job.H.shape[0]
+    check(lib.crbq_hinv_upper_finish(job.H.data_ptr(), job.H.stride(0), C, job.U.data_ptr(),
+                                     job.U.stride(0), job.ws.data_ptr(), job.ws.numel(),
+                                     ctypes.byref(retries), ctypes.byref(fallback),
+                                     job.stream.cuda_stream), "crbq_hinv_upper_finish")
+    return job.U, int(retries.value), bool(fallback.value)
+
+
 def fasterquant_blocks(W: torch.Tensor, U: torch.Tensor, p: _lib.CrbqParams,
                        losses: torch.Tensor, want_masks: bool = False,
                        want_traces: bool = False):

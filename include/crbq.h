@@ -124,6 +124,17 @@ int crbq_hinv_upper(float* H, int64_t ldh, int64_t C, float* W, int64_t R,
                     int64_t ldw, float percdamp, float* U, int64_t ldu,
                     void* ws, size_t ws_bytes, int* retries, int* fallback,
                     void* stream);
+/* The same in two steps, so several factorizations can run concurrently on
+ * different streams: _async enqueues dead-column handling, damping and the
+ * first attempt (no synchronisation); _finish synchronises `stream`, checks
+ * the outcome and runs any retries / the fallback.  Both calls take the
+ * same H, U and workspace. */
+int crbq_hinv_upper_async(float* H, int64_t ldh, int64_t C, float* W, int64_t R,
+                          int64_t ldw, float percdamp, float* U, int64_t ldu,
+                          void* ws, size_t ws_bytes, void* stream);
+int crbq_hinv_upper_finish(float* H, int64_t ldh, int64_t C, float* U, int64_t ldu,
+                           void* ws, size_t ws_bytes, int* retries, int* fallback,
+                           void* stream);
 
 /* ---- block loop (BRAGPTQ.fasterquant, bigptq.py:131-264) -----------------
  * Quantizes W (R x C fp32, row stride ldw) in place, column block by column
