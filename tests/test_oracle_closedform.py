@@ -1,0 +1,198 @@
+"""Pins of the CPU oracle that do not come from the reference's own outputs:
+float64 closed forms, library identities and invariants, chosen so that a
+dropped term, a wrong sign or a transposed operand fails one of them.
+(The golden-vector tests pin the same functions against the reference.)"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import crb_oracle as O
+
+
+def test_hessian_closed_form():
+    """bigptq.py:37-53: after n sequences H = (2/n) sum_t x_t x_t^T."""
+    g = torch.Generator().manual_seed(1)
+    X = torch.randn(5, 40, 24, generator=g)
+    H = torch.zeros(24, 24)
+    n = 0
+    for s in range(5):
+        H, n = O.hessian_add_batch(H, n, X[s:s + 1])
+    Xd = X.reshape(-1, 24).double()
+    want = 2.0 / 5 * Xd.t() @ Xd
+    assert n == 5
+    assert float((H.double() - want).abs().max() / want.abs().max()) < 1e-6
+    # a batch of 2 counts as 2 samples
+    H2, n2 = O.hessian_add_batch(torch.zeros(24, 24), 0, X[:2])
+    assert n2 == 2
+    want2 = 2.0 / 2 * X[:2].reshape(-1, 24).double().t() @ X[:2].reshape(-1, 24).double()
+    assert float((H2.double() - want2).abs().max() / want2.abs().max()) < 1e-6
+
+
+def test_hinv_upper_identity_and_structure():
+    g = torch.Generator().manual_seed(2)
+    A = torch.randn(64, 30, generator=g, dtype=torch.float64)
+    H = (A.t() @ A).float()
+    W = torch.randn(4, 30)
+    Hm = H.clone()
+    U, info = O.hinv_upper(Hm, W, 0.01)
+    Hd = H.double() + 0.01 * H.double().diag().mean() * torch.eye(30, dtype=torch.float64)
+    Ud = U.double()
+    assert torch.equal(torch.triu(U), U) and bool((torch.diag(U) > 0).all())
+    assert float((Ud.t() @ Ud @ Hd - torch.eye(30, dtype=torch.float64)).abs().max()) < 1e-4
+    assert info.retries == 0 and not info.fallback
+
+
+def test_hinv_dead_columns():
+    H = torch.eye(6) * 4.0
+    H[2, :] = 0
+    H[:, 2] = 0
+    W = torch.ones(3, 6)
+    U, info = O.hinv_upper(H, W, 0.0)
+    assert bool(info.dead[2]) and int(info.dead.sum()) == 1
+    assert torch.all(W[:, 2] == 0) and torch.all(W[:, [0, 1, 3, 4, 5]] == 1)
+    assert float(U[2, 2]) == 1.0 and abs(float(U[0, 0]) - 0.5) < 1e-7
+
+
+def _hor_f64(x, m, order):
+    """binary.py:18-39 in float64 per row."""
+    out = np.zeros_like(x, dtype=np.float64)
+    for r in range(x.shape[0]):
+        idx = np.nonzero(m[r])[0]
+        acc = np.zeros(len(idx))
+        v = x[r, idx].astype(np.float64)
+        for _ in range(order):
+            res = v - acc
+            if len(idx) == 0:
+                break
+            mu = res.mean()
+            c = res - mu
+            a = np.abs(c).mean()
+            acc = acc + np.sign(c) * a + mu
+        out[r, idx] = acc
+    return out
+
+
+@pytest.mark.parametrize("order", [1, 2, 3])
+def test_hor_matches_float64_closed_form(order):
+    g = torch.Generator().manual_seed(3 + order)
+    x = torch.randn(20, 64, generator=g) * 0.05
+    m = torch.rand(20, 64, generator=g) < 0.5
+    m[0] = False
+    got = O.hor(x, m, order).double().numpy()
+    want = _hor_f64(x.numpy(), m.numpy(), order)
+    assert np.abs(got - want).max() < 1e-6
+    assert np.all(got[~m.numpy()] == 0)
+
+
+def test_hor_order1_brute_force_tiny():
+    """Order 1 on 3 values: q = mu + alpha*sign(x - mu), alpha = mean|x - mu|."""
+    x = torch.tensor([[1.0, 2.0, 6.0]])
+    m = torch.ones(1, 3, dtype=torch.bool)
+    mu, alpha = 3.0, (2 + 1 + 3) / 3
+    want = torch.tensor([[mu - alpha, mu - alpha, mu + alpha]])
+    assert torch.allclose(O.hor(x, m, 1), want)
+
+
+def test_crb_solve_is_the_ridge_normal_equations():
+    """Without damping/Tikhonov and refinement, CRB's (a1, a2) minimise
+    ||cen - a1 B1 - a2 B2|| (binary.py:1582-1596) when both are positive."""
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(16, 128, generator=g) * 0.02
+    m = torch.ones(16, 128, dtype=torch.bool)
+    out, sc = O.crb_v7(x, m, 2, lam=0.0, corr_damp=0.0, skip_refinement=True, return_scales=True)
+    for r in range(16):
+        cen = (x[r] - sc.mean[r]).double().numpy()
+        B = np.stack([sc.b1[r].double().numpy(), sc.b2[r].double().numpy()], 1)
+        a, *_ = np.linalg.lstsq(B, cen, rcond=None)
+        if a.min() > 0:
+            assert abs(a[0] - float(sc.a1[r])) < 1e-5 * abs(a[0]) + 1e-9
+            assert abs(a[1] - float(sc.a2[r])) < 1e-5 * abs(a[1]) + 1e-9
+    assert bool((sc.a1 >= 0).all() and (sc.a2 >= 0).all())
+
+
+def test_crb_mu_correction_zeroes_the_mean_residual():
+    """Step 7 adds the mean of the residual, so the per-row mean of
+    x - out over the mask is ~0 (binary.py:1633-1636)."""
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(8, 128, generator=g) * 0.03
+    m = torch.rand(8, 128, generator=g) < 0.8
+    out = O.crb_v7(x, m, 2)
+    res = ((x - out) * m).sum(1) / m.sum(1)
+    assert float(res.abs().max()) < 1e-8
+
+
+def test_crb_order2_fits_at_least_as_well_as_order1():
+    """Without damping, Tikhonov term or refinement, (a1, a2) are the least
+    squares scales for (B1, B2) when both are positive, and a1_0 = mean|cen|
+    is the least squares scale of B1 alone, so the order-2 error (before
+    and after the mean correction) is at most the order-1 error.  (Sign
+    refinement re-centres residuals, binary.py:1617-1630, and carries no
+    such guarantee.)"""
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(64, 128, generator=g) * 0.02
+    m = torch.ones(64, 128, dtype=torch.bool)
+    q2, sc = O.crb_v7(x, m, 2, lam=0.0, corr_damp=0.0, skip_refinement=True,
+                      return_scales=True)
+    q1 = O.crb_v7(x, m, 1)
+    e1 = ((x - q1).double() ** 2).sum(1)
+    e2 = ((x - q2).double() ** 2).sum(1)
+    ok = (sc.a1 > 0) & (sc.a2 > 0)
+    assert int(ok.sum()) > 32
+    assert float((e2 - e1)[ok].max()) <= 1e-9
+
+
+def test_crbog_float64_least_squares():
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(6, 40, generator=g)
+    m = torch.ones(6, 40, dtype=torch.bool)
+    out = O.crbog(x, m, 2)
+    for r in range(6):
+        v = x[r].double().numpy()
+        mean = np.float32(x[r].mean())
+        cen = v - mean
+        b1 = np.sign(cen)
+        a1 = np.abs(cen).mean()
+        b2 = np.sign(cen - a1 * b1)
+        B = np.stack([b1, b2], 1)
+        a, *_ = np.linalg.lstsq(B, cen, rcond=None)
+        a = np.maximum(a, 0)
+        want = mean + a[0] * b1 + a[1] * b2
+        assert np.abs(out[r].double().numpy() - want).max() < 1e-5
+
+
+def test_search_picks_the_true_argmin_on_separated_input():
+    """Two columns 1000x larger than the rest: the order-2 salient group
+    must take exactly those two (utils/autosearch.py:44-55)."""
+    g = torch.Generator().manual_seed(11)
+    T = torch.rand(32, 128, generator=g) * 0.01
+    T[:, 5] = 10 + torch.rand(32, generator=g)
+    T[:, 77] = 20 + torch.rand(32, generator=g)
+    tr = O.SearchTrace()
+    split, m3 = O.structural_searching(T, 50, trace=tr)
+    assert tr.i_star == 2
+    assert bool(m3[:, 5].all() and m3[:, 77].all()) and int(m3[0].sum()) == 2
+
+
+def test_quantile_float32_semantics():
+    """The oracle uses np.quantile on float32 data with float32 q: results
+    are float32 and equal a float32 restatement of numpy's linear method."""
+    g = np.random.default_rng(0)
+    a = np.abs(g.standard_normal(4096).astype(np.float32))
+    q = O.PERCENTILES.numpy()
+    got = np.quantile(a, q)
+    s = np.sort(a)
+    n = np.float32(len(a) - 1)
+    for k, qk in enumerate(q):
+        vi = np.float32(n * qk)
+        lo = int(np.floor(vi))
+        gam = np.float32(vi - np.float32(lo))
+        x0, x1 = s[lo], s[min(lo + 1, len(a) - 1)]
+        d = np.float32(x1 - x0)
+        r = np.float32(x0 + np.float32(d * gam))
+        if gam >= 0.5:
+            r = np.float32(x1 - np.float32(d * np.float32(1 - gam)))
+        assert got[k] == r, k
+    assert got.dtype == np.float32
+    assert math.isclose(float(q[0]), 0.1, rel_tol=1e-6) and len(q) == 81
