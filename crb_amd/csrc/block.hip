@@ -4,11 +4,12 @@
 //
 // Search of one block (utils/structure.py:8-20 -> utils/autosearch.py:28-83
 // -> utils/mask.py:7-18), all on the device with no host round trip:
-//   k_colscore   column scores sum_r |T| (fp64 per-workgroup partials)
-//   k_topk       ranks of the columns by score (torch.topk order)
-//   k_phase_a    one lane per (row, salient candidate i): order-2 residual
-//                binarization error of {top i cols} + complement
-//   k_reduce_a   i* = first strict minimum over candidates
+//   k_colscore   column scores sum_r |T| (fp64 per-workgroup partials);
+//                the last workgroup ranks the columns (torch.topk order)
+//   k_phase_a    one wavefront per row, one lane per salient candidate i:
+//                order-2 residual binarization error of {top i cols} +
+//                complement (prefix scan + two passes, closed-form error)
+//                the last workgroup takes i* = first strict minimum
 //   k_qpass/k_qscan (x3)
 //                exact np.quantile of |T * ~M3| at the 81 float32
 //                percentiles: 3-level MSD radix select (12/10/10 bits of the
@@ -16,7 +17,8 @@
 //                statistics, then numpy's float32 index/lerp arithmetic
 //   k_phase_c    one lane per (row, split candidate k): order-1 errors of the
 //                two bell groups
-//   k_reduce_c   k* = first strict minimum, split = p[k*]
+//                the last workgroup takes k* = first strict minimum,
+//                split = p[k*]
 //   k_quantize   one wavefront per row: masks, binarization per group,
 //                Q, Err = (w-q)/d, Loss = (w-q)^2/d^2
 // then sgemm_launch for W[:, ed:] -= Err @ U[st:ed, ed:].
@@ -32,12 +34,15 @@ constexpr int NQ = 81;       // percentiles linspace(0.10, 0.90, 81)
 constexpr int NT = 2 * NQ;   // order statistics needed (lo, hi per percentile)
 constexpr int NCMAX = 128;   // widest block
 constexpr int UPMAX = 64;    // largest supported up_lim
-constexpr int CS_RPW = 32;   // rows per workgroup in k_colscore
 constexpr int Q_RPW = 16;    // rows per workgroup in the quantile passes
-constexpr int PA_RPW = 13;   // rows per workgroup in phase A (13*49 = 637 items)
-constexpr int PX_THREADS = 128;
-constexpr int CS_MAXWG = 256;  // colscore partials (grid-stride over row groups)
-constexpr int PX_MAXWG = 1024; // phase A / C partials
+#ifndef CRBQ_CS_MAXWG
+#define CRBQ_CS_MAXWG 128
+#endif
+constexpr int CS_MAXWG = CRBQ_CS_MAXWG;   // colscore partials
+#ifndef CRBQ_PX_MAXWG
+#define CRBQ_PX_MAXWG 256
+#endif
+constexpr int PX_MAXWG = CRBQ_PX_MAXWG;  // phase A / C partials
 constexpr int H1_BITS = 12, H2_BITS = 10, H3_BITS = 10;   // 12 + 10 + 10 = 32
 constexpr int H1 = 1 << H1_BITS, H2 = 1 << H2_BITS, H3 = 1 << H3_BITS;
 constexpr int SH1 = H2_BITS + H3_BITS, SH2 = H3_BITS;     // key = b1<<SH1 | b2<<SH2 | b3
@@ -52,7 +57,9 @@ struct Ctrl {        // small per-block control record (device)
   int ncand_a;
   int pad;
   float split;
+  uint32_t cnt[4];   // arrival counters of the last-workgroup reductions
 };
+enum { CNT_CS = 0, CNT_A = 1, CNT_C = 2 };
 
 struct Tgt {         // one order statistic being selected
   int64_t rank;      // absolute rank in the sorted flattened block
@@ -108,45 +115,47 @@ __device__ __forceinline__ float target_of(float w, float d2, int metric) {
 }
 
 // ---------------------------------------------------------------------------
-// column scores + zeroing of the selection histograms for this block
+// last-workgroup reductions
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_colscore(
-    const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
-  __shared__ double part[2][NCMAX];
-  const int tid = threadIdx.x, col = tid & (NCMAX - 1), ph = tid >> 7;
-  double acc = 0.0;
-  if (col < nc) {
-    const float dg = U[(int64_t)col * ldu + col];
-    const float d2 = dg * dg;
-    for (int r0 = blockIdx.x * CS_RPW; r0 < R; r0 += gridDim.x * CS_RPW) {
-      const int r1 = min(R, r0 + CS_RPW);
-      for (int r = r0 + ph; r < r1; r += 2)
-        acc += (double)fabsf(target_of(W[(int64_t)r * ldw + col], d2, metric));
+// Every workgroup calls this after writing its partial results.  It returns
+// true in exactly one workgroup, the last to arrive, which then sees every
+// other workgroup's writes (release/acquire fences at device scope around
+// the arrival counter) and resets the counter for the next launch.
+#ifndef CRBQ_FENCE_ALL
+#define CRBQ_FENCE_ALL 0
+#endif
+__device__ __forceinline__ bool last_block(uint32_t* cnt) {
+  __shared__ bool last;
+#if CRBQ_FENCE_ALL
+  __threadfence();
+#endif
+  __syncthreads();   // every wave's partial stores have completed
+  if (threadIdx.x == 0) {
+    __threadfence();   // release (device scope) before arriving
+    const uint32_t prev = atomicAdd(cnt, 1u);
+    last = prev == gridDim.x - 1;
+    if (last) {
+      atomicExch(cnt, 0u);
+      __threadfence();   // acquire: drop stale cached partials
     }
   }
-  part[ph][col] = acc;
   __syncthreads();
-  if (ph == 0) s.colpart[(size_t)blockIdx.x * NCMAX + col] = part[0][col] + part[1][col];
-  // zero the histograms used later by this block (grid-stride)
-  const size_t gsz = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)NT * H2; i += gsz) {
-    s.hist2[i] = 0u;
-    s.hist3[i] = 0u;
-  }
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)H1; i += gsz) s.hist1[i] = 0u;
+  return last;
 }
 
 // Fixed-order sum of nwg partials (row stride `stride` doubles) for `ncand`
-// candidates with 1024 threads: PARTS threads per candidate, then the PARTS
-// subtotals in order.  Result in out[0..ncand).
+// candidates with NK * PARTS threads: PARTS threads per candidate, each
+// summing every PARTS-th partial, then the PARTS subtotals in order.
+// Result in out[0..ncand).
 template <int NK, int PARTS>
-__device__ void reduce_partials(const double* __restrict__ part, int stride, int nwg, int ncand,
+__device__ void reduce_partials(const double* part, int stride, int nwg, int ncand,
                                 double (*red)[NK], double* out) {
   const int t = threadIdx.x, k = t % NK, pp = t / NK;
   double v = 0.0;
-  if (k < ncand && pp < PARTS)
+  if (k < ncand && pp < PARTS) {
+#pragma unroll 8
     for (int g = pp; g < nwg; g += PARTS) v += part[(size_t)g * stride + k];
+  }
   if (pp < PARTS) red[pp][k] = v;
   __syncthreads();
   if (t < ncand) {
@@ -157,13 +166,49 @@ __device__ void reduce_partials(const double* __restrict__ part, int stride, int
   __syncthreads();
 }
 
-// ranks of the columns by descending score (ties: lower column first)
-__global__ __launch_bounds__(1024) void k_topk(int nc, int nwg, SearchWs s) {
-  __shared__ double red[8][NCMAX];
+// ---------------------------------------------------------------------------
+// column scores -> ranks (torch.topk order); zeroing of this block's
+// selection histograms
+// ---------------------------------------------------------------------------
+#ifndef CRBQ_CS_PH
+#define CRBQ_CS_PH 8
+#endif
+constexpr int CS_PH = CRBQ_CS_PH;            // row phases per workgroup
+constexpr int CS_THREADS = NCMAX * CS_PH;
+__global__ __launch_bounds__(CS_THREADS) void k_colscore(
+    const float* __restrict__ W, int64_t ldw, int R, int nc,
+    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
+  __shared__ double part[CS_PH][NCMAX];
+  __shared__ double red[CS_PH][NCMAX];
   __shared__ double sc[NCMAX];
-  reduce_partials<NCMAX, 8>(s.colpart, NCMAX, nwg, NCMAX, red, sc);
-  const int c = threadIdx.x;
-  if (c < NCMAX) {
+  const int tid = threadIdx.x, col = tid & (NCMAX - 1), ph = tid / NCMAX;
+  double acc = 0.0;
+  if (col < nc) {
+    const float dg = U[(int64_t)col * ldu + col];
+    const float d2 = dg * dg;
+    for (int r = CS_PH * blockIdx.x + ph; r < R; r += CS_PH * gridDim.x)
+      acc += (double)fabsf(target_of(W[(int64_t)r * ldw + col], d2, metric));
+  }
+  part[ph][col] = acc;
+  // zero the histograms used later by this block (grid-stride)
+  const size_t gsz = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)NT * H2; i += gsz) {
+    s.hist2[i] = 0u;
+    s.hist3[i] = 0u;
+  }
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)H1; i += gsz) s.hist1[i] = 0u;
+  __syncthreads();
+  if (ph == 0) {
+    double v = 0.0;
+#pragma unroll
+    for (int q = 0; q < CS_PH; ++q) v += part[q][col];
+    s.colpart[(size_t)blockIdx.x * NCMAX + col] = v;
+  }
+  if (!last_block(&s.ctrl->cnt[CNT_CS])) return;
+  reduce_partials<NCMAX, CS_PH>(s.colpart, NCMAX, gridDim.x, NCMAX, red, sc);
+  // rank of column c by descending score, ties to the lower column
+  if (tid < NCMAX) {
+    const int c = tid;
     const double v = sc[c];
     int r = NCMAX;
     if (c < nc) {
@@ -176,122 +221,155 @@ __global__ __launch_bounds__(1024) void k_topk(int nc, int nwg, SearchWs s) {
 
 // ---------------------------------------------------------------------------
 // phase A: error of order-2 residual binarization of {rank < i} and its
-// complement, for candidates i = 1..up_lim-1 (utils/autosearch.py:44-55)
+// complement, for candidates i = 1..up_lim-1 (utils/autosearch.py:44-55);
+// the last workgroup picks i* = first strict minimum (default
+// max(1, up_lim // 3), :43)
 // ---------------------------------------------------------------------------
-__device__ double phase_a_item(const float* __restrict__ x, const int* __restrict__ rk,
-                               int nc, int i) {
-  const float nS = (float)i, nC = (float)(nc - i);
-  double sS = 0.0, sC = 0.0;
-  for (int c = 0; c < nc; ++c) {
-    const double v = (double)x[c];
-    const bool in = rk[c] < i;
-    sS += in ? v : 0.0;
-    sC += in ? 0.0 : v;
+// One wavefront per row, one lane per candidate i = lane + 1.  The row's
+// targets are placed in LDS in column-rank order, so the salient group of
+// candidate i is ranks [0, i) and its complement ranks [i, nc).  Order-2
+// residual binarization of a group with mean m1, scale a1, residual
+// r = x - (a1*sign(x - m1) + m1), residual mean m2 and scale a2 has error
+//   sum (e - a2*sign(e))^2 = E2 - 2*a2*E1 + a2^2 * nz,
+// e = r - m2, E1 = sum |e|, E2 = sum e^2, nz = #(e != 0).  Group sums of x
+// come from a wave prefix scan; sum |x - m1| and the sign counts (which give
+// sum r in closed form, s1 taking the three fp32 values m1 +- a1 and m1)
+// from one pass; E1, E2, nz from a second pass in which r and e are formed
+// with the reference's fp32 operations, so every sign decision is the
+// reference's.  All sums are fp64.
+#ifndef CRBQ_PA_WAVES
+#define CRBQ_PA_WAVES 16
+#endif
+constexpr int PA_WAVES = CRBQ_PA_WAVES;
+
+struct GroupA {         // per-lane accumulators of one group
+  double ad, e1, e2;
+  float npos, nneg, nz;
+};
+
+template <bool MIXED>
+__device__ __forceinline__ void pass_abs(const float* xs, int c0, int c1, int i, float m1S,
+                                         float m1C, GroupA& S, GroupA& Cg) {
+  for (int c = c0; c < c1; ++c) {
+    const float x = xs[c];
+    const bool inS = MIXED && c < i;
+    const float d = x - (inS ? m1S : m1C);
+    const double ad = (double)fabsf(d);
+    const float pos = d > 0.f ? 1.f : 0.f, neg = d < 0.f ? 1.f : 0.f;
+    if (MIXED) {
+      S.ad += inS ? ad : 0.0;
+      S.npos += inS ? pos : 0.f;
+      S.nneg += inS ? neg : 0.f;
+    }
+    Cg.ad += inS ? 0.0 : ad;
+    Cg.npos += inS ? 0.f : pos;
+    Cg.nneg += inS ? 0.f : neg;
   }
-  const float m1S = nS > 0.f ? (float)sS / nS : 0.f;
-  const float m1C = nC > 0.f ? (float)sC / nC : 0.f;
-  sS = 0.0; sC = 0.0;
-  for (int c = 0; c < nc; ++c) {
-    const bool in = rk[c] < i;
-    const double a = (double)fabsf(x[c] - (in ? m1S : m1C));
-    sS += in ? a : 0.0;
-    sC += in ? 0.0 : a;
-  }
-  const float a1S = nS > 0.f ? (float)sS / nS : 0.f;
-  const float a1C = nC > 0.f ? (float)sC / nC : 0.f;
-  sS = 0.0; sC = 0.0;
-  for (int c = 0; c < nc; ++c) {
-    const bool in = rk[c] < i;
-    const float m = in ? m1S : m1C, a = in ? a1S : a1C;
-    const float cc = x[c] - m;
-    float s1 = tsign(cc) * a;
-    s1 = s1 + m;
-    const double r = (double)(x[c] - s1);
-    sS += in ? r : 0.0;
-    sC += in ? 0.0 : r;
-  }
-  const float m2S = nS > 0.f ? (float)sS / nS : 0.f;
-  const float m2C = nC > 0.f ? (float)sC / nC : 0.f;
-  sS = 0.0; sC = 0.0;
-  for (int c = 0; c < nc; ++c) {
-    const bool in = rk[c] < i;
-    const float m = in ? m1S : m1C, a = in ? a1S : a1C, m2 = in ? m2S : m2C;
-    const float cc = x[c] - m;
-    float s1 = tsign(cc) * a;
-    s1 = s1 + m;
-    const float r = x[c] - s1;
-    const double a2 = (double)fabsf(r - m2);
-    sS += in ? a2 : 0.0;
-    sC += in ? 0.0 : a2;
-  }
-  const float a2S = nS > 0.f ? (float)sS / nS : 0.f;
-  const float a2C = nC > 0.f ? (float)sC / nC : 0.f;
-  double err = 0.0;
-  for (int c = 0; c < nc; ++c) {
-    const bool in = rk[c] < i;
-    const float m = in ? m1S : m1C, a = in ? a1S : a1C;
-    const float m2 = in ? m2S : m2C, a2 = in ? a2S : a2C;
-    const float cc = x[c] - m;
-    float s1 = tsign(cc) * a;
-    s1 = s1 + m;
-    const float r = x[c] - s1;
-    const float c2 = r - m2;
-    float s2 = tsign(c2) * a2;
-    s2 = s2 + m2;
-    const float tot = s1 + s2;
-    const float df = x[c] - tot;
-    err += (double)(df * df);
-  }
-  return err;
 }
 
-__global__ __launch_bounds__(PX_THREADS) void k_phase_a(
+template <bool MIXED>
+__device__ __forceinline__ void pass_res(const float* xs, int c0, int c1, int i,
+                                         const float (&m1)[2], const float (&a1)[2],
+                                         const float (&m2)[2], GroupA& S, GroupA& Cg) {
+  for (int c = c0; c < c1; ++c) {
+    const float x = xs[c];
+    const bool inS = MIXED && c < i;
+    const int g = inS ? 0 : 1;
+    const float m = MIXED ? (inS ? m1[0] : m1[1]) : m1[1];
+    const float a = MIXED ? (inS ? a1[0] : a1[1]) : a1[1];
+    const float mm = MIXED ? (inS ? m2[0] : m2[1]) : m2[1];
+    (void)g;
+    float s1 = tsign(x - m) * a;                 // binary.py:32-34
+    s1 = s1 + m;
+    const float r = x - s1;                      // binary.py:26 (order 2)
+    const float e = r - mm;
+    const double ae = (double)fabsf(e), e2 = (double)e * (double)e;
+    const float nz = e != 0.f ? 1.f : 0.f;
+    if (MIXED) {
+      S.e1 += inS ? ae : 0.0;
+      S.e2 += inS ? e2 : 0.0;
+      S.nz += inS ? nz : 0.f;
+    }
+    Cg.e1 += inS ? 0.0 : ae;
+    Cg.e2 += inS ? 0.0 : e2;
+    Cg.nz += inS ? 0.f : nz;
+  }
+}
+
+__global__ __launch_bounds__(64 * PA_WAVES) void k_phase_a(
     const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, int ncand, SearchWs s) {
-  __shared__ float xs[PA_RPW][NCMAX];
-  __shared__ int rk[NCMAX];
-  __shared__ float d2s[NCMAX];
-  __shared__ double errs[PA_RPW][UPMAX];
-  __shared__ double acc[UPMAX];
-  const int tid = threadIdx.x;
-  for (int i = tid; i < NCMAX; i += PX_THREADS) {
-    rk[i] = s.rank[i];
-    if (i < nc) { const float dg = U[(int64_t)i * ldu + i]; d2s[i] = dg * dg; }
-  }
-  for (int i = tid; i < UPMAX; i += PX_THREADS) acc[i] = 0.0;
-  for (int r0 = blockIdx.x * PA_RPW; r0 < R; r0 += gridDim.x * PA_RPW) {
-    const int nr = min(PA_RPW, R - r0);
-    __syncthreads();
-    for (int i = tid; i < PA_RPW * NCMAX; i += PX_THREADS) {
-      const int rr = i / NCMAX, c = i % NCMAX;
-      xs[rr][c] = (rr < nr && c < nc) ? target_of(W[(int64_t)(r0 + rr) * ldw + c], d2s[c], metric)
-                                      : 0.f;
-    }
-    __syncthreads();
-    const int items = nr * ncand;
-    for (int it = tid; it < items; it += PX_THREADS) {
-      const int rr = it / ncand, ci = it % ncand;
-      errs[rr][ci] = phase_a_item(xs[rr], rk, nc, ci + 1);
-    }
-    __syncthreads();
-    for (int ci = tid; ci < ncand; ci += PX_THREADS) {
-      double e = acc[ci];
-      for (int rr = 0; rr < nr; ++rr) e += errs[rr][ci];
-      acc[ci] = e;
-    }
-  }
-  __syncthreads();
-  for (int ci = tid; ci < ncand; ci += PX_THREADS)
-    s.parta[(size_t)blockIdx.x * UPMAX + ci] = acc[ci];
-}
-
-__global__ __launch_bounds__(1024) void k_reduce_a(int nwg, int ncand, int up_lim,
-                                                   SearchWs s, crbq_block_trace* tr) {
-  __shared__ double red[16][UPMAX];
+    const float* __restrict__ U, int64_t ldu, int metric, int ncand, int up_lim, SearchWs s,
+    crbq_block_trace* tr) {
+  __shared__ float xs[PA_WAVES][NCMAX];
+  __shared__ double errs[PA_WAVES][64];
+  __shared__ double red[PA_WAVES][UPMAX];
   __shared__ double e[UPMAX];
-  reduce_partials<UPMAX, 16>(s.parta, UPMAX, nwg, ncand, red, e);
-  const int c = threadIdx.x;
-  if (c == 0) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int c0 = lane, c1 = lane + 64;
+  const int rk0 = c0 < nc ? s.rank[c0] : -1, rk1 = c1 < nc ? s.rank[c1] : -1;
+  float d20 = 1.f, d21 = 1.f;
+  if (c0 < nc) { const float dg = U[(int64_t)c0 * ldu + c0]; d20 = dg * dg; }
+  if (c1 < nc) { const float dg = U[(int64_t)c1 * ldu + c1]; d21 = dg * dg; }
+  const int i = lane + 1;                        // candidate (salient columns)
+  const float nS = (float)i, nC = (float)(nc - i);
+  const int mix_end = min(nc, 64);               // ranks >= 64 are never salient
+  double acc = 0.0;
+  for (int r0 = blockIdx.x * PA_WAVES; r0 < R; r0 += gridDim.x * PA_WAVES) {
+    const int row = r0 + wv;
+    float* x = xs[wv];
+    __syncthreads();                             // previous row's readers are done
+    if (row < R) {
+      if (rk0 >= 0) x[rk0] = target_of(W[(int64_t)row * ldw + c0], d20, metric);
+      if (rk1 >= 0) x[rk1] = target_of(W[(int64_t)row * ldw + c1], d21, metric);
+    }
+    __syncthreads();
+    if (row < R) {
+      // prefix sums in rank order: candidate i's salient group is ranks [0, i)
+      const double y0 = lane < nc ? (double)x[lane] : 0.0;
+      const double y1 = lane + 64 < nc ? (double)x[lane + 64] : 0.0;
+      double ps = y0;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const double t = __shfl_up(ps, o, CRBQ_WAVE);
+        if (lane >= o) ps += t;
+      }
+      const double tot = wave_sum(y0 + y1);
+      const float m1S = (float)ps / nS;
+      const float m1C = nC > 0.f ? (float)(tot - ps) / nC : 0.f;
+      GroupA S = {0.0, 0.0, 0.0, 0.f, 0.f, 0.f}, Cg = {0.0, 0.0, 0.0, 0.f, 0.f, 0.f};
+      pass_abs<true>(x, 0, mix_end, i, m1S, m1C, S, Cg);
+      pass_abs<false>(x, mix_end, nc, i, m1S, m1C, S, Cg);
+      const float a1S = (float)S.ad / nS;
+      const float a1C = nC > 0.f ? (float)Cg.ad / nC : 0.f;
+      // sum r = sum x - sum s1, s1 in {fl(a1 + m1), fl(-a1 + m1), m1}
+      float hiS = a1S + m1S, loS = -a1S + m1S, hiC = a1C + m1C, loC = -a1C + m1C;
+      const double s1S = S.npos * (double)hiS + S.nneg * (double)loS +
+                         ((double)nS - S.npos - S.nneg) * (double)m1S;
+      const double s1C = Cg.npos * (double)hiC + Cg.nneg * (double)loC +
+                         ((double)nC - Cg.npos - Cg.nneg) * (double)m1C;
+      const float m2S = (float)(ps - s1S) / nS;
+      const float m2C = nC > 0.f ? (float)((tot - ps) - s1C) / nC : 0.f;
+      const float m1v[2] = {m1S, m1C}, a1v[2] = {a1S, a1C}, m2v[2] = {m2S, m2C};
+      pass_res<true>(x, 0, mix_end, i, m1v, a1v, m2v, S, Cg);
+      pass_res<false>(x, mix_end, nc, i, m1v, a1v, m2v, S, Cg);
+      const double a2S = (double)((float)S.e1 / nS);
+      const double a2C = nC > 0.f ? (double)((float)Cg.e1 / nC) : 0.0;
+      const double eS = S.e2 - 2.0 * a2S * S.e1 + a2S * a2S * (double)S.nz;
+      const double eC = Cg.e2 - 2.0 * a2C * Cg.e1 + a2C * a2C * (double)Cg.nz;
+      acc += eS + eC;
+    }
+  }
+  errs[wv][lane] = acc;
+  __syncthreads();
+  if (tid < ncand) {
+    double v = 0.0;
+#pragma unroll
+    for (int w = 0; w < PA_WAVES; ++w) v += errs[w][tid];
+    s.parta[(size_t)blockIdx.x * UPMAX + tid] = v;
+  }
+  if (!last_block(&s.ctrl->cnt[CNT_A])) return;
+  reduce_partials<UPMAX, PA_WAVES>(s.parta, UPMAX, gridDim.x, ncand, red, e);
+  if (tid == 0) {
     double best = INFINITY;
     int istar = max(1, up_lim / 3);                                  // :43
     for (int k = 0; k < ncand; ++k)
@@ -299,8 +377,9 @@ __global__ __launch_bounds__(1024) void k_reduce_a(int nwg, int ncand, int up_li
     s.ctrl->istar = istar;
     if (tr) tr->i_star = istar;
   }
-  if (tr && c < UPMAX) tr->errs_a[c] = (c >= 1 && c <= ncand) ? e[c - 1] : 0.0;
+  if (tr && tid < UPMAX) tr->errs_a[tid] = (tid >= 1 && tid <= ncand) ? e[tid - 1] : 0.0;
 }
+
 
 // ---------------------------------------------------------------------------
 // exact float32 np.quantile of S = |T * ~M3| (utils/autosearch.py:62-68)
@@ -535,7 +614,10 @@ __device__ __forceinline__ float np_lerp(float a, float b, float t) {
 // the same fp32 comparisons the elementwise code makes, and every sum is a
 // difference of prefix sums: sum (v - t)^2 = Q - 2 t S + n t^2.
 // ---------------------------------------------------------------------------
-constexpr int PC_WAVES = 4;
+#ifndef CRBQ_PC_WAVES
+#define CRBQ_PC_WAVES 16
+#endif
+constexpr int PC_WAVES = CRBQ_PC_WAVES;
 
 struct SortedRow {
   float v[NCMAX];        // ascending; first n valid
@@ -646,8 +728,10 @@ __device__ __forceinline__ void wave_prefix(SortedRow& r, float x0, float x1, in
 
 __global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
     const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
+    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s, crbq_block_trace* tr) {
   __shared__ SortedRow rows[PC_WAVES];
+  __shared__ double red[PC_WAVES / 2][128];
+  __shared__ double e[128];
   __shared__ float pv[NQ];
   __shared__ double errs[PC_WAVES][NQ];
   __shared__ double acc[NQ];
@@ -688,21 +772,16 @@ __global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
     __syncthreads();
     const int nr = min(PC_WAVES, R - r0);
     for (int k = tid; k < NQ; k += 64 * PC_WAVES) {
-      double e = acc[k];
-      for (int w = 0; w < nr; ++w) e += errs[w][k];
-      acc[k] = e;
+      double v = acc[k];
+      for (int w = 0; w < nr; ++w) v += errs[w][k];
+      acc[k] = v;
     }
   }
   __syncthreads();
   for (int k = tid; k < NQ; k += 64 * PC_WAVES) s.partc[(size_t)blockIdx.x * 96 + k] = acc[k];
-}
-
-__global__ __launch_bounds__(1024) void k_reduce_c(int nwg, SearchWs s, crbq_block_trace* tr) {
-  __shared__ double red[8][128];
-  __shared__ double e[128];
-  reduce_partials<128, 8>(s.partc, 96, nwg, NQ, red, e);
-  const int k = threadIdx.x;
-  if (k == 0) {
+  if (!last_block(&s.ctrl->cnt[CNT_C])) return;
+  reduce_partials<128, PC_WAVES / 2>(s.partc, 96, gridDim.x, NQ, red, e);
+  if (tid == 0) {
     double best = INFINITY;
     int ks = NQ / 2;                                                 // :71 median
     for (int j = 0; j < NQ; ++j)
@@ -711,7 +790,7 @@ __global__ __launch_bounds__(1024) void k_reduce_c(int nwg, SearchWs s, crbq_blo
     s.ctrl->split = s.pvals[ks];
     if (tr) { tr->k_star = ks; tr->split = s.pvals[ks]; }
   }
-  if (tr && k < NQ) { tr->errs_c[k] = e[k]; tr->pvals[k] = s.pvals[k]; }
+  if (tr && tid < NQ) { tr->errs_c[tid] = e[tid]; tr->pvals[tid] = s.pvals[tid]; }
 }
 
 // ---------------------------------------------------------------------------
@@ -793,6 +872,11 @@ __global__ __launch_bounds__(256) void k_quantize(QuantArgs a, SearchWs s) {
   }
 }
 
+// clears the arrival counters of the last-workgroup reductions
+__global__ void k_init_ctrl(SearchWs s) {
+  if (threadIdx.x < 4) s.ctrl->cnt[threadIdx.x] = 0u;
+}
+
 // ---------------------------------------------------------------------------
 // host drivers
 // ---------------------------------------------------------------------------
@@ -800,22 +884,20 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
                         int64_t ldu, int metric, int up_lim, SearchWs& s,
                         crbq_block_trace* tr, hipStream_t st) {
   const int ncand = up_lim - 1;
-  const int nwg_cs = (int)std::min<int64_t>(cdiv(R, CS_RPW), CS_MAXWG);
+  const int nwg_cs = (int)std::min<int64_t>(cdiv(R, CS_PH), CS_MAXWG);
   const int nwg_q = (int)cdiv(R, Q_RPW);
-  const int nwg_a = (int)std::min<int64_t>(cdiv(R, PA_RPW), PX_MAXWG);
+  const int nwg_a = (int)std::min<int64_t>(cdiv(R, PA_WAVES), PX_MAXWG);
   const int nwg_c = (int)std::min<int64_t>(cdiv(R, PC_WAVES), PX_MAXWG);
-  k_colscore<<<nwg_cs, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  k_topk<<<1, 1024, 0, st>>>(nc, nwg_cs, s);
-  k_phase_a<<<nwg_a, PX_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, ncand, s);
-  k_reduce_a<<<1, 1024, 0, st>>>(nwg_a, ncand, up_lim, s, tr);
+  k_colscore<<<nwg_cs, CS_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
+  k_phase_a<<<nwg_a, 64 * PA_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric, ncand, up_lim, s,
+                                              tr);
   k_qpass1<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_qscan1<<<1, 256, 0, st>>>((int64_t)R * nc, s);
   k_qpass2<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_qscan2<<<NT, 256, 0, st>>>(s);
   k_qpass3<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_qscan3<<<NT, 256, 0, st>>>(s);
-  k_phase_c<<<nwg_c, 64 * PC_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  k_reduce_c<<<1, 1024, 0, st>>>(nwg_c, s, tr);
+  k_phase_c<<<nwg_c, 64 * PC_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s, tr);
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }
@@ -907,6 +989,7 @@ extern "C" int crbq_block_search(const float* W, int64_t R, int32_t ncols, int64
   int st = ensure_q_table();
   if (st) return st;
   hipStream_t hs = (hipStream_t)stream;
+  k_init_ctrl<<<1, 64, 0, hs>>>(s);
   st = search_block(W, ldw, (int)R, ncols, Ublk, ldu, metric, up_lim, s, trace, hs);
   if (st) return st;
   if (masks) {
@@ -955,6 +1038,7 @@ extern "C" int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw, con
   st = ensure_q_table();
   if (st) return st;
   hipStream_t hs = (hipStream_t)stream;
+  k_init_ctrl<<<1, 64, 0, hs>>>(s);
   if (p->partition == 3) {
     // every block must be at least up_lim wide (torch.topk k <= n)
     const int64_t last = C - (C - 1) / bs * bs;
