@@ -7,16 +7,20 @@
 // and J L'^-1 J is upper triangular with a positive diagonal, so it is U
 // (the Cholesky factor is unique).  2C^3/3 flops.
 //
-// L'^-1 is formed in the same right-looking blocked sweep as L' (nb = 128):
-// step j factors the diagonal block (one workgroup, in LDS, also inverting
-// it: D_j = L'_jj^-1), then on fp32 MFMA
-//   X[j, 0:j]        = D_j X[j, 0:j]                    (row block of L'^-1)
-//   P                = A[j+1:, j] D_j^T                 (panel of L')
-//   A[j+1:, j+1:]   -= P P^T          (lower tiles)     (SYRK)
-//   X[j+1:, 0:j]    -= P X[j, 0:j]                      (inverse update)
-//   X[j+1:, j]       = -P D_j
-// where X shares A's storage: column block j of L' is consumed at step j,
-// and the same storage then holds column block j of L'^-1.
+// L'^-1 is formed recursively together with L' (block boundaries at
+// multiples of NB = 128).  For A = [A11 0; A21 A22] split near the middle:
+//   X11 = chol_inv(A11)                     (L11^-1, recursively)
+//   T   = A21 X11^T                         (= L21, the panel of L')
+//   A22 = A22 - T T^T      (lower tiles)    (Schur complement)
+//   A21 = T X11                             (= L21 L11^-1)
+//   X22 = chol_inv(A22)                     (recursively)
+//   X21 = -X22 A21
+// so X = [X11 0; X21 X22] = L'^-1 overwrites A.  Blocks of NB or fewer
+// rows are factored and inverted by one workgroup (k_chol_inv_diag).  About
+// 3/4 of the 2C^3/3 flops are in the four products of the top level,
+// which run as large fp32 MFMA GEMMs; the triangular factors' zero halves
+// are skipped.  The upper triangle of A is kept at zero so the triangular
+// operands can be read as full matrices.
 // A pivot that is not > 0 (or NaN) sets *info (LAPACK potrf semantics) and
 // every later kernel of the sweep returns at once; the host then adds the
 // reference's extra damping and retries (bigptq.py:114-126).
@@ -68,13 +72,24 @@ __global__ __launch_bounds__(1024) void k_damp(float* H, int64_t ldh, int C, flo
 
 __global__ void k_set_int(int* p, int v) { *p = v; }
 
-// A[i][j] = H[C-1-i][C-1-j], lower triangle only
+// A[i][j] = H[C-1-i][C-1-j] in the lower triangle, 0 above it
 __global__ __launch_bounds__(256) void k_reverse_lower(const float* __restrict__ H, int64_t ldh,
                                                        int C, float* A, int64_t lda) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int i = (int)(idx / C), j = (int)(idx % C);
-  if (i >= C || j > i) return;
-  A[(int64_t)i * lda + j] = H[(int64_t)(C - 1 - i) * ldh + (C - 1 - j)];
+  if (i >= C) return;
+  A[(int64_t)i * lda + j] = j <= i ? H[(int64_t)(C - 1 - i) * ldh + (C - 1 - j)] : 0.f;
+}
+
+// Y[r][c] = X[r][c] for an M x N block (row strides ldx, ldy)
+__global__ __launch_bounds__(256) void k_copy2d(const float* __restrict__ X, int64_t ldx, int M,
+                                                int N, float* Y, int64_t ldy,
+                                                const int* __restrict__ stop) {
+  if (*stop) return;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int r = (int)(idx / N), c = (int)(idx % N);
+  if (r >= M) return;
+  Y[(int64_t)r * ldy + c] = X[(int64_t)r * ldx + c];
 }
 
 // U[i][j] = X[C-1-i][C-1-j] for j >= i, 0 below the diagonal
@@ -102,247 +117,357 @@ __global__ __launch_bounds__(256) void k_fallback_u(const float* __restrict__ H,
   U[(int64_t)i * ldu + j] = v;
 }
 
-// Diagonal block: Cholesky and triangular inverse of one NB x NB block,
-// blocked by 8.  256 threads as a 16 x 16 grid; thread (ty, tx) keeps the
-// 8 x 8 sub-block rows ty*8.., cols tx*8.. in registers.  Step kb of the
-// factorization: the owner of diagonal block (kb, kb) factors and inverts
-// it in registers; the owners of column kb form the panel
-// P_I = A_I,kb D_kb^T; every lower block right of column kb takes the
-// rank-8 update A_IJ -= P_I P_J^T.  The inverse X = L^-1 is the same
-// right-looking sweep on the identity: X_kb,J = D_kb B_kb,J, then
-// B_I,J -= L_I,kb X_kb,J.  Rows past bj are padded with the identity.
-__device__ __forceinline__ void chol8(float (&a)[8][8], float (&x)[8][8], int& bad) {
-  bad = -1;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const float p = a[k][k];
-    if (!(p > 0.f) && bad < 0) bad = k;
-    const float d = sqrtf(p), di = 1.f / d;
-    a[k][k] = d;
-#pragma unroll
-    for (int r = k + 1; r < 8; ++r) a[r][k] = a[r][k] * di;
-#pragma unroll
-    for (int c = k + 1; c < 8; ++c)
-#pragma unroll
-      for (int r = c; r < 8; ++r) a[r][c] = a[r][c] - a[r][k] * a[c][k];
-  }
-#pragma unroll
-  for (int r = 0; r < 8; ++r)
-#pragma unroll
-    for (int c = 0; c < 8; ++c) x[r][c] = r == c ? 1.f : 0.f;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const float di = 1.f / a[k][k];
-#pragma unroll
-    for (int c = 0; c <= k; ++c) x[k][c] = x[k][c] * di;
-#pragma unroll
-    for (int r = k + 1; r < 8; ++r)
-#pragma unroll
-      for (int c = 0; c <= k; ++c) x[r][c] = x[r][c] - a[r][k] * x[k][c];
-  }
+// Diagonal block: Cholesky factor L and its inverse X = L^-1 of one
+// bj x bj block (bj <= NB; rows past bj are padded with the identity), in
+// place.  256 threads = 4 wavefronts.
+//  * Factorization in LDS: the 128 columns form 16 panels of 8; panel b
+//    belongs to wavefront b % 4.  The owner factors its panel in registers
+//    (lane l holds rows l and l + 64; pivots broadcast with readlane) and
+//    publishes it, and after one barrier every wavefront applies the
+//    rank-8 update to its own later panels.
+//  * Inverse: recursive doubling in LDS.  With X_A, X_C the inverses of two
+//    adjacent diagonal blocks of size s and B the block below X_A,
+//    X_B = -X_C (B X_A); s = 1, 2, 4, ..., 64.
+// This factorization need not follow the reference's rounding step for
+// step (LAPACK's blocked potrf does not either), so it uses fused
+// multiply-adds and one reciprocal per pivot.
+constexpr int LDP = NB + 1;            // LDS pitch of the block (column reads conflict-free)
+constexpr int PANP = 12;               // LDS pitch of a panel row (8 used, 16-byte aligned)
+
+__device__ __forceinline__ float rdlane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-__global__ __launch_bounds__(256) void k_potrf_diag(float* A, int64_t lda, int off, int bj,
-                                                    float* D, int* info) {
-  if (*info) return;
-  __shared__ __attribute__((aligned(16))) float pan[NB][8];     // column panel of L
-  __shared__ __attribute__((aligned(16))) float Dk[NB / 8][8][8];  // inverses of diag blocks
-  __shared__ __attribute__((aligned(16))) float xr[8][NB];      // row panel of X
-  __shared__ int fail;
-  const int tid = threadIdx.x, ty = tid >> 4, tx = tid & 15;
-  const int i0 = ty * 8, j0 = tx * 8;
-  const int nkb = (bj + 7) / 8;
-  float a[8][8], x[8][8];
+struct DiagSmem {
+  float Ls[NB][LDP];
+  float pan[2][NB][PANP];
+  float Ts[64 * 64];
+  int fail;
+};
+
+// Panel b of the factorization: the owner wavefront factors columns
+// 8b..8b+7 (rows in its lanes' registers, pivots broadcast with readlane),
+// every wavefront then applies the rank-8 update to its later panels in
+// LDS.  Returns false after a bad pivot.
+__device__ __forceinline__ bool chol_panel(int B, DiagSmem& sm, int lane, int w, int off, int bj,
+                                           int* info) {
+  float (*pb)[PANP] = sm.pan[B & 1];
+  if (w == (B & 3)) {
+    float pc[2][8];
 #pragma unroll
-  for (int r = 0; r < 8; ++r)
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int i = i0 + r, j = j0 + c;
-      a[r][c] = (i < bj && j <= i) ? A[(int64_t)(off + i) * lda + off + j]
-                                   : (i == j ? 1.f : 0.f);
+      for (int q = 0; q < 8; ++q) pc[s][q] = sm.Ls[lane + 64 * s][8 * B + q];
+    const bool hi = B >= 8;            // the panel's diagonal rows are in slot 1
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int c = 8 * B + p;
+      const float piv = rdlane(hi ? pc[1][p] : pc[0][p], c & 63);
+      if (!(piv > 0.f) && lane == 0 && c < bj) {
+        sm.fail = 1;
+        atomicCAS(info, 0, off + c + 1);
+      }
+      const float d = __builtin_amdgcn_sqrtf(piv);
+      const float rd = __builtin_amdgcn_rcpf(d);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int i = lane + 64 * s;
+        pc[s][p] = i > c ? pc[s][p] * rd : (i == c ? d : 0.f);
+      }
+#pragma unroll
+      for (int q = p + 1; q < 8; ++q) {
+        const float lq = rdlane(hi ? pc[1][p] : pc[0][p], (8 * B + q) & 63);   // L[8B+q][c]
+#pragma unroll
+        for (int s = 0; s < 2; ++s) pc[s][q] = fmaf(-pc[s][p], lq, pc[s][q]);
+      }
     }
-  if (tid == 0) fail = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int i = lane + 64 * s;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) sm.Ls[i][8 * B + q] = pc[s][q];
+      *(float4*)&pb[i][0] = make_float4(pc[s][0], pc[s][1], pc[s][2], pc[s][3]);
+      *(float4*)&pb[i][4] = make_float4(pc[s][4], pc[s][5], pc[s][6], pc[s][7]);
+    }
+  }
   __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
-    if (ty == kb && tx == kb) {                       // factor + invert the diagonal block
-      int bad;
-      chol8(a, x, bad);
-      if (bad >= 0 && i0 + bad < bj) {
-        fail = 1;
-        atomicCAS(info, 0, off + i0 + bad + 1);
+  if (sm.fail) return false;
+  // rank-8 update of this wavefront's later panels; rows < 64 lie above
+  // every column >= 64
+  float pi[2][8];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const float4 u = *(const float4*)&pb[lane + 64 * s][0];
+    const float4 v = *(const float4*)&pb[lane + 64 * s][4];
+    pi[s][0] = u.x; pi[s][1] = u.y; pi[s][2] = u.z; pi[s][3] = u.w;
+    pi[s][4] = v.x; pi[s][5] = v.y; pi[s][6] = v.z; pi[s][7] = v.w;
+  }
+  for (int gb = w; gb < 16; gb += 4) {
+    if (gb <= B) continue;
+    // all 8 columns at once: loads first, then 16 independent FMA chains
+    float pj[8][8], t0[8], t1[8];
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) {
+      const int j = 8 * gb + cc;
+      const float4 u = *(const float4*)&pb[j][0];
+      const float4 v = *(const float4*)&pb[j][4];
+      pj[cc][0] = u.x; pj[cc][1] = u.y; pj[cc][2] = u.z; pj[cc][3] = u.w;
+      pj[cc][4] = v.x; pj[cc][5] = v.y; pj[cc][6] = v.z; pj[cc][7] = v.w;
+      t0[cc] = sm.Ls[lane][j];
+      t1[cc] = sm.Ls[lane + 64][j];
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+#pragma unroll
+      for (int cc = 0; cc < 8; ++cc) {
+        t0[cc] = fmaf(-pi[0][q], pj[cc][q], t0[cc]);
+        t1[cc] = fmaf(-pi[1][q], pj[cc][q], t1[cc]);
       }
 #pragma unroll
-      for (int r = 0; r < 8; ++r)
+    for (int cc = 0; cc < 8; ++cc) {
+      sm.Ls[lane][8 * gb + cc] = t0[cc];
+      sm.Ls[lane + 64][8 * gb + cc] = t1[cc];
+    }
+  }
+  return true;
+}
+
+// one level of the recursive-doubling inverse (pairs of S x S blocks)
+template <int S>
+__device__ __forceinline__ void inv_level(DiagSmem& sm, int tid) {
+  constexpr int NPAIR = NB / (2 * S);
+  if constexpr (S < 4) {
+    constexpr int NE = NPAIR * S * S;
+    for (int e = tid; e < NE; e += 256) {
+      const int q = e / (S * S), r = (e / S) % S, c = e % S, cb = 2 * S * q;
+      float t = 0.f;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) Dk[kb][r][c] = c <= r ? x[r][c] : 0.f;
+      for (int k = 0; k < S; ++k) t = fmaf(sm.Ls[cb + S + r][cb + k], sm.Ls[cb + k][cb + c], t);
+      sm.Ts[e] = t;
     }
     __syncthreads();
-    if (fail) return;
-    if (tx == kb && ty > kb) {                        // panel P_I = A_I,kb D_kb^T
-      float p[8][8];
+    for (int e = tid; e < NE; e += 256) {
+      const int q = e / (S * S), r = (e / S) % S, c = e % S, cb = 2 * S * q;
+      float t = 0.f;
 #pragma unroll
-      for (int r = 0; r < 8; ++r)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          float v = 0.f;
-#pragma unroll
-          for (int m = 0; m <= c; ++m) v = v + a[r][m] * Dk[kb][c][m];
-          p[r][c] = v;
-        }
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          a[r][c] = p[r][c];
-          pan[i0 + r][c] = p[r][c];
-        }
+      for (int k = 0; k < S; ++k) t = fmaf(sm.Ls[cb + S + r][cb + S + k], sm.Ts[q * S * S + k * S + c], t);
+      sm.Ls[cb + S + r][cb + c] = -t;
     }
     __syncthreads();
-    if (ty >= tx && tx > kb) {                        // A_IJ -= P_I P_J^T
-      float pi[8][8];
+  } else if constexpr (S < 16) {
+    constexpr int TPS = S / 4;                 // 4x4 tiles per block side
+    constexpr int NT = NPAIR * TPS * TPS;
+    // T = B X_A (X_A lower: rows k < j0 of X_A are zero in the tile's columns)
+    for (int e = tid; e < NT; e += 256) {
+      const int q = e / (TPS * TPS), ti = (e / TPS) % TPS, tj = e % TPS, cb = 2 * S * q;
+      const int i0 = 4 * ti, j0 = 4 * tj;
+      float t[4][4];
 #pragma unroll
-      for (int r = 0; r < 8; ++r)
+      for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int m = 0; m < 8; ++m) pi[r][m] = pan[i0 + r][m];
+        for (int c = 0; c < 4; ++c) t[r][c] = 0.f;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        float pj[8];
+      for (int k = 0; k < S; ++k) {
+        float b[4], x[4];
 #pragma unroll
-        for (int m = 0; m < 8; ++m) pj[m] = pan[j0 + c][m];
+        for (int r = 0; r < 4; ++r) b[r] = sm.Ls[cb + S + i0 + r][cb + k];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          float v = a[r][c];
+        for (int c = 0; c < 4; ++c) x[c] = sm.Ls[cb + k][cb + j0 + c];
 #pragma unroll
-          for (int m = 0; m < 8; ++m) v = v - pi[r][m] * pj[m];
-          a[r][c] = v;
-        }
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) t[r][c] = fmaf(b[r], x[c], t[r][c]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sm.Ts[q * S * S + (i0 + r) * S + j0 + c] = t[r][c];
+    }
+    __syncthreads();
+    // X_B = -X_C T
+    for (int e = tid; e < NT; e += 256) {
+      const int q = e / (TPS * TPS), ti = (e / TPS) % TPS, tj = e % TPS, cb = 2 * S * q;
+      const int i0 = 4 * ti, j0 = 4 * tj;
+      const float* T = sm.Ts + q * S * S;
+      float t[4][4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) t[r][c] = 0.f;
+#pragma unroll
+      for (int k = 0; k < S; ++k) {
+        float xc[4], tv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xc[r] = sm.Ls[cb + S + i0 + r][cb + S + k];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) tv[c] = T[k * S + j0 + c];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) t[r][c] = fmaf(xc[r], tv[c], t[r][c]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sm.Ls[cb + S + i0 + r][cb + j0 + c] = -t[r][c];
+    }
+    __syncthreads();
+  } else {
+    // 16 x 16 output tiles on v_mfma_f32_16x16x4_f32, one tile per
+    // wavefront at a time: lane l supplies A[l%16][k + l/16] and
+    // B[k + l/16][l%16] and receives D[4*(l/16) + r][l%16], r = 0..3.
+    constexpr int TPS = S / 16;
+    constexpr int NT = NPAIR * TPS * TPS;
+    const int lane = tid & 63, wv = tid >> 6, lr = lane & 15, lk = lane >> 4;
+    for (int e = wv; e < NT; e += 4) {        // T = B X_A, k >= 16 tj
+      const int q = e / (TPS * TPS), ti = (e / TPS) % TPS, tj = e % TPS, cb = 2 * S * q;
+      f4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+      for (int k = 16 * tj; k < S; k += 4) {
+        const float av = sm.Ls[cb + S + 16 * ti + lr][cb + k + lk];
+        const float bv = sm.Ls[cb + k + lk][cb + 16 * tj + lr];
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.Ts[q * S * S + (16 * ti + 4 * lk + r) * S + 16 * tj + lr] = acc[r];
+    }
+    __syncthreads();
+    for (int e = wv; e < NT; e += 4) {        // X_B = -X_C T, k < 16 (ti + 1)
+      const int q = e / (TPS * TPS), ti = (e / TPS) % TPS, tj = e % TPS, cb = 2 * S * q;
+      const float* T = sm.Ts + q * S * S;
+      f4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+      for (int k = 0; k < 16 * (ti + 1); k += 4) {
+        const float av = sm.Ls[cb + S + 16 * ti + lr][cb + S + k + lk];
+        const float bv = T[(k + lk) * S + 16 * tj + lr];
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.Ls[cb + S + 16 * ti + 4 * lk + r][cb + 16 * tj + lr] = -acc[r];
+    }
+    __syncthreads();
+  }
+  if constexpr (2 * S < NB) inv_level<2 * S>(sm, tid);
+}
+
+__global__ __launch_bounds__(256) void k_chol_inv_diag(float* A, int64_t lda, int off, int bj,
+                                                       int* info) {
+  if (*info) return;
+  __shared__ DiagSmem sm;
+  // the wavefront index as a scalar, so branches on it are uniform
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // ---- load the block (lower triangle), identity padding, zero above;
+  // 16 coalesced 4-float groups per thread, all in flight together
+  {
+    const bool vec = ((lda & 3) == 0) && ((((uintptr_t)A) & 15) == 0);
+    float v[16][4];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int f = tid + 256 * u, i = f >> 5, j0 = (f & 31) * 4;
+      const float* src = A + (int64_t)(off + i) * lda + off + j0;
+      if (vec && i < bj && j0 + 3 < bj) {
+        const float4 q = *(const float4*)src;
+        v[u][0] = q.x; v[u][1] = q.y; v[u][2] = q.z; v[u][3] = q.w;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[u][c] = (i < bj && j0 + c < bj) ? src[c] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int f = tid + 256 * u, i = f >> 5, j0 = (f & 31) * 4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int j = j0 + c;
+        sm.Ls[i][j] = (i < bj && j <= i) ? v[u][c] : (i == j ? 1.f : 0.f);
       }
     }
   }
-  // a: L blocks (I >= J).  X = L^-1, right-looking on the identity.
-#pragma unroll
-  for (int r = 0; r < 8; ++r)
-#pragma unroll
-    for (int c = 0; c < 8; ++c) x[r][c] = (i0 + r == j0 + c) ? 1.f : 0.f;
-  for (int kb = 0; kb < nkb; ++kb) {
-    __syncthreads();                                  // previous step's readers are done
-    if (ty == kb && tx <= kb) {                       // X_kb,J = D_kb B_kb,J
-      float y[8][8];
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          float v = 0.f;
-#pragma unroll
-          for (int m = 0; m <= r; ++m) v = v + Dk[kb][r][m] * x[m][c];
-          y[r][c] = v;
-        }
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          x[r][c] = y[r][c];
-          xr[r][j0 + c] = y[r][c];
-        }
-    }
-    if (tx == kb && ty > kb) {                        // publish L_I,kb
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-#pragma unroll
-        for (int m = 0; m < 8; ++m) pan[i0 + r][m] = a[r][m];
-    }
-    __syncthreads();
-    if (ty > kb && tx <= kb) {                        // B_I,J -= L_I,kb X_kb,J
-      float li[8][8];
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-#pragma unroll
-        for (int m = 0; m < 8; ++m) li[r][m] = pan[i0 + r][m];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        float xc[8];
-#pragma unroll
-        for (int m = 0; m < 8; ++m) xc[m] = xr[m][j0 + c];
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          float v = x[r][c];
-#pragma unroll
-          for (int m = 0; m < 8; ++m) v = v - li[r][m] * xc[m];
-          x[r][c] = v;
-        }
-      }
-    }
+  if (tid == 0) sm.fail = 0;
+  __syncthreads();
+  // ---- factorization (L overwrites the block, zeros above the diagonal)
+  for (int B = 0; B < 16; ++B)
+    if (!chol_panel(B, sm, lane, w, off, bj, info)) return;
+  __syncthreads();
+  if (tid < NB) sm.Ls[tid][tid] = 1.f / sm.Ls[tid][tid];
+  __syncthreads();
+  // ---- inverse by recursive doubling
+  inv_level<1>(sm, tid);
+  // ---- write X (zero above the diagonal)
+#pragma unroll 8
+  for (int e = tid; e < NB * NB; e += 256) {
+    const int i = e >> 7, j = e & (NB - 1);
+    if (i < bj && j < bj) A[(int64_t)(off + i) * lda + off + j] = j <= i ? sm.Ls[i][j] : 0.f;
   }
-#pragma unroll
-  for (int r = 0; r < 8; ++r)
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const int i = i0 + r, j = j0 + c;
-      if (i < bj && j < bj) {
-        const float v = j <= i ? x[r][c] : 0.f;
-        D[i * NB + j] = v;
-        A[(int64_t)(off + i) * lda + off + j] = v;
-      }
-    }
 }
 
 static inline unsigned nblocks(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 struct HinvWs {
   float* A;        // C x C (ld = C)
-  float* P;        // C x NB panel
-  float* D;        // NB x NB
+  float* T;        // panel of the recursion: half x half (ld = half)
   int* info;
   float* scal;
   uint8_t* dead;   // C
 };
 
+// rows in the first half of an n-row split (a multiple of NB, >= n - it)
+static inline int split_rows(int n) {
+  const int nblk = (n + NB - 1) / NB;
+  return (nblk + 1) / 2 * NB;
+}
+
 static void carve_hinv(WsCarver& c, int64_t C, HinvWs& w) {
+  const int64_t h = C > NB ? split_rows((int)C) : 0;
   w.A = c.take<float>((size_t)C * C);
-  w.P = c.take<float>((size_t)C * NB);
-  w.D = c.take<float>((size_t)NB * NB);
+  w.T = c.take<float>((size_t)std::max<int64_t>(h * h, 1));
   w.info = c.take<int>(4);
   w.scal = c.take<float>(4);
   w.dead = c.take<uint8_t>((size_t)C);
 }
 
+// X = L^-1 of the n x n diagonal block at offset o of A (lda), in place.
+// The factorization outcome is in *w.info; after a failure every later
+// kernel returns at once.
+static int chol_inv_rec(float* A, int64_t lda, int o, int n, HinvWs& w, hipStream_t s) {
+  if (n <= NB) {
+    k_chol_inv_diag<<<1, 256, 0, s>>>(A, lda, o, n, w.info);
+    CRBQ_LAUNCH_CHECK();
+    return CRBQ_OK;
+  }
+  const int m = split_rows(n), n2 = n - m;
+  float* A11 = A + (int64_t)o * lda + o;
+  float* A21 = A11 + (int64_t)m * lda;
+  float* A22 = A21 + m;
+  const int* stop = w.info;
+  int st = chol_inv_rec(A, lda, o, m, w, s);
+  if (st) return st;
+  // T = A21 X11^T
+  st = sgemm_launch(false, true, false, n2, m, m, 1.f, A21, lda, A11, lda, 0.f, w.T, m, stop, s,
+                    GEMM_TRI_KEND_N);
+  if (st) return st;
+  // A22 -= T T^T (lower tiles)
+  st = sgemm_launch(false, true, true, n2, n2, m, -1.f, w.T, m, w.T, m, 1.f, A22, lda, stop, s);
+  if (st) return st;
+  // A21 = T X11
+  st = sgemm_launch(false, false, false, n2, m, m, 1.f, w.T, m, A11, lda, 0.f, A21, lda, stop, s,
+                    GEMM_TRI_KBEG_N);
+  if (st) return st;
+  st = chol_inv_rec(A, lda, o + m, n2, w, s);
+  if (st) return st;
+  // X21 = -X22 A21, through T
+  st = sgemm_launch(false, false, false, n2, m, n2, -1.f, A22, lda, A21, lda, 0.f, w.T, m, stop,
+                    s, GEMM_TRI_KEND_M);
+  if (st) return st;
+  k_copy2d<<<nblocks((int64_t)n2 * m), 256, 0, s>>>(w.T, m, n2, m, A21, lda, stop);
+  CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}
+
 // One full attempt: factor and invert A in place.  Returns a launch status;
 // the factorization outcome is in *w.info.
 static int chol_inv_sweep(float* A, int64_t lda, int C, HinvWs& w, hipStream_t s) {
-  const int nblk = (C + NB - 1) / NB;
-  for (int j = 0; j < nblk; ++j) {
-    const int off = j * NB, bj = std::min(NB, C - off), rest = C - off - bj;
-    k_potrf_diag<<<1, 256, 0, s>>>(A, lda, off, bj, w.D, w.info);
-    CRBQ_LAUNCH_CHECK();
-    int st;
-    if (off > 0) {           // X[j, 0:j] = D_j X[j, 0:j]  (in place)
-      st = sgemm_launch(false, false, false, bj, off, bj, 1.f, w.D, NB, A + (int64_t)off * lda,
-                        lda, 0.f, A + (int64_t)off * lda, lda, w.info, s);
-      if (st) return st;
-    }
-    if (rest > 0) {
-      float* Apan = A + (int64_t)(off + bj) * lda + off;
-      // P = A[j+1:, j] D_j^T
-      st = sgemm_launch(false, true, false, rest, bj, bj, 1.f, Apan, lda, w.D, NB, 0.f, w.P,
-                        NB, w.info, s);
-      if (st) return st;
-      // A[j+1:, j+1:] -= P P^T (lower)
-      st = sgemm_launch(false, true, true, rest, rest, bj, -1.f, w.P, NB, w.P, NB, 1.f,
-                        A + (int64_t)(off + bj) * lda + off + bj, lda, w.info, s);
-      if (st) return st;
-      if (off > 0) {         // X[j+1:, 0:j] -= P X[j, 0:j]
-        st = sgemm_launch(false, false, false, rest, off, bj, -1.f, w.P, NB,
-                          A + (int64_t)off * lda, lda, 1.f, A + (int64_t)(off + bj) * lda, lda,
-                          w.info, s);
-        if (st) return st;
-      }
-      // X[j+1:, j] = -P D_j
-      st = sgemm_launch(false, false, false, rest, bj, bj, -1.f, w.P, NB, w.D, NB, 0.f, Apan,
-                        lda, w.info, s);
-      if (st) return st;
-    }
-  }
-  return CRBQ_OK;
+  return chol_inv_rec(A, lda, 0, C, w, s);
 }
 
 }  // namespace crbq

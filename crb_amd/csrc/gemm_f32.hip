@@ -70,14 +70,47 @@ __device__ __forceinline__ void store_tile(float* S, const float4 (&r)[4]) {
   }
 }
 
+// Output tile of linear workgroup id.  Plain products go row by row, with
+// the ids regrouped so that the workgroups one XCD receives (every 8th id)
+// cover consecutive tiles and share operand panels in that XCD's L2.  When
+// one operand is triangular the tiles go longest K range first, so the
+// short ones fill the tail; the lower-triangle product enumerates only the
+// tiles on or below the diagonal.
+__device__ __forceinline__ void gemm_tile(int id, int nwg, int TM, int TN, int tri, bool lower,
+                                          int& tm, int& tn) {
+  if (lower) {                         // id -> (tm >= tn), row tm holds tm + 1 tiles
+    int r = (int)((sqrtf(8.f * (float)id + 1.f) - 1.f) * 0.5f);
+    while ((r + 1) * (r + 2) / 2 <= id) ++r;
+    while (r * (r + 1) / 2 > id) --r;
+    tm = r;
+    tn = id - r * (r + 1) / 2;
+    return;
+  }
+  if (tri == GEMM_TRI_KEND_N) { tn = TN - 1 - id / TM; tm = id % TM; return; }
+  if (tri == GEMM_TRI_KBEG_N) { tn = id / TM; tm = id % TM; return; }
+  if (tri == GEMM_TRI_KEND_M) { tm = TM - 1 - id / TN; tn = id % TN; return; }
+  const int q = nwg / 8, r = nwg % 8, x = id % 8, k = id / 8;
+  const int lin = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + k;
+  tm = lin / TN;
+  tn = lin % TN;
+}
+
 template <bool TA, bool TB, bool LOWER>
 __global__ __launch_bounds__(256) void k_sgemm(
     int M, int N, int K, float alpha, const float* A, int64_t lda,
     const float* B, int64_t ldb, float beta, float* C,
-    int64_t ldc, const int* __restrict__ stop, int va, int vb) {
+    int64_t ldc, const int* __restrict__ stop, int va, int vb, int tri) {
   if (stop && *stop) return;
-  const int m0 = blockIdx.y * GB_M, n0 = blockIdx.x * GB_N;
-  if (LOWER && n0 > m0 + GB_M - 1) return;  // tile entirely above diagonal
+  int tm, tn;
+  gemm_tile(blockIdx.x, gridDim.x, (M + GB_M - 1) / GB_M, (N + GB_N - 1) / GB_N, tri, LOWER, tm,
+            tn);
+  const int m0 = tm * GB_M, n0 = tn * GB_N;
+  // K range of this tile when one operand is triangular (its zero part is
+  // skipped; the products skipped are exact zeros)
+  int kbeg = 0, kend = K;
+  if (tri == GEMM_TRI_KEND_N) kend = min(K, n0 + GB_N);
+  else if (tri == GEMM_TRI_KBEG_N) kbeg = min(K, n0) / GB_K * GB_K;
+  else if (tri == GEMM_TRI_KEND_M) kend = min(K, m0 + GB_M);
   __shared__ __attribute__((aligned(16))) float As[2][T_ELEMS];
   __shared__ __attribute__((aligned(16))) float Bs[2][T_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -91,11 +124,11 @@ __global__ __launch_bounds__(256) void k_sgemm(
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int nch = (K + GB_K - 1) / GB_K;
+  const int nch = kend > kbeg ? (kend - kbeg + GB_K - 1) / GB_K : 0;
   float4 ra[4], rb[4];
   if (nch > 0) {
-    load_tile<AK>(A, lda, m0, 0, M, K, va, ra);
-    load_tile<BK>(B, ldb, n0, 0, N, K, vb, rb);
+    load_tile<AK>(A, lda, m0, kbeg, M, K, va, ra);
+    load_tile<BK>(B, ldb, n0, kbeg, N, K, vb, rb);
     store_tile<AK>(As[0], ra);
     store_tile<BK>(Bs[0], rb);
   }
@@ -103,8 +136,8 @@ __global__ __launch_bounds__(256) void k_sgemm(
   for (int c = 0; c < nch; ++c) {
     const int buf = c & 1;
     if (c + 1 < nch) {
-      load_tile<AK>(A, lda, m0, (c + 1) * GB_K, M, K, va, ra);
-      load_tile<BK>(B, ldb, n0, (c + 1) * GB_K, N, K, vb, rb);
+      load_tile<AK>(A, lda, m0, kbeg + (c + 1) * GB_K, M, K, va, ra);
+      load_tile<BK>(B, ldb, n0, kbeg + (c + 1) * GB_K, N, K, vb, rb);
     }
     const float* as = As[buf];
     const float* bs = Bs[buf];
@@ -159,17 +192,21 @@ static inline bool vec_ok(const float* p, int64_t ld) {
 int sgemm_launch(bool ta, bool tb, bool lower, int64_t M, int64_t N, int64_t K,
                  float alpha, const float* A, int64_t lda, const float* B,
                  int64_t ldb, float beta, float* C, int64_t ldc,
-                 const int* stop, hipStream_t s) {
+                 const int* stop, hipStream_t s, int tri) {
   if (M <= 0 || N <= 0) return CRBQ_OK;
   if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30) || K < 0) return CRBQ_ERR_ARG;
-  dim3 grid((unsigned)((N + GB_N - 1) / GB_N), (unsigned)((M + GB_M - 1) / GB_M));
-  if (grid.y > 65535) return CRBQ_ERR_ARG;
+  const int64_t TM = (M + GB_M - 1) / GB_M, TN = (N + GB_N - 1) / GB_N;
+  // lower: the square tile grid's lower triangle (M == N)
+  if (lower && TM != TN) return CRBQ_ERR_ARG;
+  const int64_t nwg = lower ? TM * (TM + 1) / 2 : TM * TN;
+  if (nwg > 0x7fffffff) return CRBQ_ERR_ARG;
+  const dim3 grid((unsigned)nwg);
   const int m = (int)M, n = (int)N, k = (int)K;
   const int va = vec_ok(A, lda), vb = vec_ok(B, ldb);
 #define CRBQ_GEMM_CASE(TA_, TB_, LO_)                                              \
   if (ta == TA_ && tb == TB_ && lower == LO_) {                                    \
     k_sgemm<TA_, TB_, LO_><<<grid, 256, 0, s>>>(m, n, k, alpha, A, lda, B, ldb,    \
-                                                beta, C, ldc, stop, va, vb);       \
+                                                beta, C, ldc, stop, va, vb, tri);  \
     CRBQ_LAUNCH_CHECK();                                                           \
     return CRBQ_OK;                                                                \
   }
