@@ -7,8 +7,14 @@ weight changes, so the sublayers are independent; sublayers that read the
 same activation (q/k/v in OPT and Llama, gate/up in Llama) get identical
 Hessians and therefore identical inverse factors U.  This driver
   * accumulates each distinct input's Hessian once,
-  * factors the distinct Hessians concurrently on separate HIP streams,
-  * runs the sublayers' block loops concurrently on those streams,
+  * starts each distinct input's inverse factor on a stream of its own as
+    soon as that input's last add_batch has been enqueued,
+  * enqueues every sublayer's block loop right behind its factor (an event
+    wait, no host synchronisation), the widest input's chain first and on
+    a stream of its own since it is the longest,
+  * checks the factorizations once at the end and, for an input whose
+    Cholesky needed the reference's retries or fallback (bigptq.py:114-126),
+    recomputes its sublayers with the final factor,
 and writes every quantized weight back in its own dtype.  The result is
 what the per-sublayer API computes for each sublayer.
 """
@@ -32,10 +38,9 @@ class Sublayer:
 
 @dataclass
 class PhaseTimes:
-    hessian_ms: float = 0.0
-    hinv_ms: float = 0.0
-    blocks_ms: float = 0.0
-    per_group: dict = field(default_factory=dict)
+    quantize_ms: float = 0.0                     # inverse factors + block loops, overlapped
+    hinv_ms: dict = field(default_factory=dict)  # per input: its inverse factor
+    chain_ms: dict = field(default_factory=dict) # per input: factor + its sublayers' block loops
 
 
 class LayerQuantizer:
@@ -53,6 +58,7 @@ class LayerQuantizer:
         self.nstreams = max(1, int(nstreams))
         self.S = {}
         self.nsamples = {}
+        self.ready = {}
         for s in self.sublayers:
             if s.group not in self.S:
                 C = s.weight.shape[1]
@@ -68,71 +74,101 @@ class LayerQuantizer:
         nseq = inp.shape[0]
         kernels.hessian_accum(inp.reshape(-1, inp.shape[-1]), self.S[group])
         self.nsamples[group] += nseq
+        ev = self.ready.get(group)
+        if ev is None:
+            ev = self.ready[group] = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(self.dev))
 
-    def quantize(self, events: PhaseTimes | None = None) -> dict:
+    def _assign_streams(self, groups):
+        """The widest input gets stream 0 for its factor and its sublayers;
+        the other factors and sublayers share the remaining streams,
+        balanced by weight count."""
+        ns = self.nstreams
+        gstream = {}
+        for i, g in enumerate(groups):
+            gstream[g] = 0 if i == 0 or ns == 1 else 1 + (i - 1) % (ns - 1)
+        load = [0] * ns
+        sstream = {}
+        for s in sorted(self.sublayers, key=lambda s: -s.weight.numel()):
+            if s.group == groups[0] or ns == 1:
+                k = 0
+            else:
+                k = min(range(1, ns), key=lambda j: load[j])
+            load[k] += s.weight.numel()
+            sstream[s.name] = k
+        return gstream, sstream
+
+    def _blocks(self, s, U, dead):
+        W = s.weight.float() if s.weight.dtype != torch.float32 else s.weight.clone()
+        W = W.contiguous()
+        W.masked_fill_(dead[None, :], 0.0)                               # bigptq.py:105
+        losses = torch.zeros(W.shape[0], device=self.dev)
+        kernels.fasterquant_blocks(W, U, self.p, losses)
+        return W, losses
+
+    def quantize(self, times: PhaseTimes | None = None) -> dict:
         """fasterquant for every sublayer; returns {name: error}."""
         main = torch.cuda.current_stream(self.dev)
         streams = [torch.cuda.Stream(device=self.dev) for _ in range(self.nstreams)]
-        start = torch.cuda.Event()
-        start.record(main)
-        for st in streams:
-            st.wait_event(start)
+        groups = sorted(self.S.keys(), key=lambda g: -self.S[g].shape[0])
+        gstream, sstream = self._assign_streams(groups)
+        t0 = torch.cuda.Event(enable_timing=True)
+        t0.record(main)
 
-        def ev(stream):
-            e = torch.cuda.Event(enable_timing=True)
+        def timed(stream):
+            e = torch.cuda.Event(enable_timing=times is not None)
             e.record(stream)
             return e
 
-        e0 = ev(main) if events is not None else None
-        # distinct Hessians -> U, concurrently
-        groups = list(self.S.keys())
-        jobs, dead = {}, {}
-        for gi, g in enumerate(groups):
-            st = streams[gi % len(streams)]
+        jobs, dead, U, hdone, hstart = {}, {}, {}, {}, {}
+        for g in groups:
+            st = streams[gstream[g]]
+            st.wait_event(self.ready[g] if g in self.ready else t0)
             with torch.cuda.stream(st):
+                hstart[g] = timed(st)
                 n = self.nsamples[g]
                 H = kernels.hessian_finalize(self.S[g], 2.0 / n if n else 0.0, self.S[g])
                 dead[g] = torch.diag(H) == 0
                 jobs[g] = kernels.hinv_upper_async(H, None, self.percdamp)
-        U, has_dead = {}, {}
-        for g in groups:
-            Ug, retries, fb = kernels.hinv_upper_finish(jobs[g])   # synchronises g's stream
-            U[g] = Ug
-            has_dead[g] = bool(dead[g].any())
-            self.info[g] = {"retries": retries, "fallback": fb}
-        if events is not None:
-            e1 = torch.cuda.Event(enable_timing=True)
-            e1.record(main)
-            for st in streams:
-                main.wait_stream(st)
-            e1b = ev(main)
-        # every U is ready (finish synchronised its stream); block loops
-        work = []
-        for si, s in enumerate(self.sublayers):
-            st = streams[si % len(streams)]
+                U[g] = jobs[g].U
+                hdone[g] = timed(st)
+        work, sdone = {}, {}
+        # the widest input's sublayers first (their chain is the longest)
+        order = sorted(self.sublayers, key=lambda s: (groups.index(s.group), -s.weight.numel()))
+        for s in order:
+            st = streams[sstream[s.name]]
+            st.wait_event(hdone[s.group])
             U[s.group].record_stream(st)
             dead[s.group].record_stream(st)
             with torch.cuda.stream(st):
-                if events is not None:
-                    st.wait_stream(main)
-                W = s.weight.float().contiguous() if s.weight.dtype != torch.float32 else s.weight
-                if has_dead[s.group]:
-                    W[:, dead[s.group]] = 0                      # bigptq.py:105
-                losses = torch.zeros(W.shape[0], device=self.dev)
-                kernels.fasterquant_blocks(W, U[s.group], self.p, losses)
-                if s.weight.dtype != torch.float32:
-                    s.weight.copy_(W.to(s.weight.dtype))
-                work.append((s, W, losses))
-        for st in streams:
-            main.wait_stream(st)
-        e2 = ev(main) if events is not None else None
-        for s, W, losses in work:
-            W.record_stream(main)
-            losses.record_stream(main)
+                work[s.name] = self._blocks(s, U[s.group], dead[s.group])
+                sdone[s.name] = timed(st)
+        torch.cuda.synchronize(self.dev)
+        # the first attempt of every factorization has finished: read its
+        # outcome; retries / fallback (rare) recompute U and its sublayers
+        redo = set()
+        for g in groups:
+            Ug, retries, fb = kernels.hinv_upper_finish(jobs[g])
+            self.info[g] = {"retries": retries, "fallback": fb}
+            if retries or fb:
+                redo.add(g)
+        for s in order:
+            if s.group in redo:
+                work[s.name] = self._blocks(s, U[s.group], dead[s.group])
+        for s in order:
+            W, losses = work[s.name]
+            if s.weight.dtype != torch.float32:
+                s.weight.copy_(W.to(s.weight.dtype))
+            else:
+                s.weight.copy_(W)
         self.S = {g: None for g in groups}
-        self.errors = {s.name: float(losses.sum()) for s, W, losses in work}
-        if events is not None:
-            torch.cuda.synchronize()
-            events.hinv_ms += e0.elapsed_time(e1b)
-            events.blocks_ms += e1b.elapsed_time(e2)
+        self.errors = {s.name: float(work[s.name][1].sum()) for s in order}
+        if times is not None:
+            torch.cuda.synchronize(self.dev)
+            times.quantize_ms += t0.elapsed_time(max(sdone.values(), key=lambda e: t0.elapsed_time(e)))
+            for g in groups:
+                times.hinv_ms[g] = hstart[g].elapsed_time(hdone[g])
+                last = max((sdone[s.name] for s in order if s.group == g),
+                           key=lambda e: t0.elapsed_time(e))
+                times.chain_ms[g] = hstart[g].elapsed_time(last)
         return self.errors
