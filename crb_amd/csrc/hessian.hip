@@ -8,10 +8,10 @@
 // inputs use v_mfma_f32_16x16x4_f32.
 //
 // Token-major X[t][c] is staged through LDS channel-major (Xs[c][t]) so each
-// MFMA lane reads its 8 consecutive tokens with one ds_read_b128: every
-// thread loads an 8-token x 8-channel block with eight 16-byte loads and
-// transposes it in registers with v_perm_b32 before one 16-byte LDS store
-// per channel.
+// MFMA lane reads its 8 consecutive tokens with one ds_read_b128: a loading
+// thread reads a 4-token x 8-channel unit with four 16-byte loads and
+// transposes it in registers with v_perm_b32 before one 8-byte LDS store per
+// channel.
 #include "common.h"
 
 namespace crbq {
@@ -38,34 +38,26 @@ __device__ __forceinline__ f4_t mfma16<b8_t>(b8_t a, b8_t b, f4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// 16-bit inputs (T8 = h8_t or b8_t; storage is 2 bytes per element).
-// 256 x 256 output tile per 512-thread workgroup; the 8 wavefronts form a
-// 2 x 4 grid, each owning 128 x 64 outputs (8 x 4 MFMA 16x16x32 tiles).
-// Tokens are staged SK at a time through double-buffered LDS: per stage
-// thread t loads SK/32 4-token x 8-channel units of side I (t < 256) or J,
-// ahead in registers, so global latency is covered by MFMA work
-// (SK MFMAs per wavefront per stage).
+// 16-bit inputs (T8 = h8_t or b8_t; storage is 2 bytes per element):
+// 256 x 256 output tile per workgroup (k_syrk16p below).
 // Split-K: workgroup (tile, s) sums tokens [s*span, (s+1)*span) and, when
 // the grid is split, writes its partial tile to P[s] for k_sum_splits.
-#ifndef CRBQ_SYRK_SK
-#define CRBQ_SYRK_SK 64
-#endif
-#ifndef CRBQ_SYRK_DIST
-#define CRBQ_SYRK_DIST 1
-#endif
 constexpr int ST = 256;                 // output tile (channels)
-constexpr int SK = CRBQ_SYRK_SK;        // tokens per stage (multiple of 32)
-constexpr int SKP = SK + 8;             // padded LDS row (halves)
-constexpr int UNITS = SK / 32;          // 4-token x 8-channel units per thread per stage
-constexpr int SYRK_THREADS = 512;
 
+// FAST: C and ldx are multiples of 8 and X is 16-byte aligned, so every
+// in-range 8-channel group is one 16-byte load.
+template <bool FAST>
 __device__ __forceinline__ void load_unit(const uint16_t* __restrict__ X, int64_t ntok,
                                           int64_t ldx, int C, int64_t t0, int cbase,
                                           bool cvec, uint32_t (&in)[4][4]) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t t = t0 + r;
-    if (t < ntok && cvec) {
+    if (FAST) {
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (t < ntok && cbase < C) v = *(const uint4*)(X + t * ldx + cbase);
+      in[r][0] = v.x; in[r][1] = v.y; in[r][2] = v.z; in[r][3] = v.w;
+    } else if (t < ntok && cvec) {
       const uint4 v = *(const uint4*)(X + t * ldx + cbase);
       in[r][0] = v.x; in[r][1] = v.y; in[r][2] = v.z; in[r][3] = v.w;
     } else {
@@ -80,7 +72,8 @@ __device__ __forceinline__ void load_unit(const uint16_t* __restrict__ X, int64_
 }
 
 // transpose a 4-token x 8-channel unit in registers, store it channel-major
-__device__ __forceinline__ void store_unit(uint16_t (*Xs)[SKP], int crow, int tcol,
+template <int PITCH>
+__device__ __forceinline__ void store_unit(uint16_t (*Xs)[PITCH], int crow, int tcol,
                                            const uint32_t (&in)[4][4]) {
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
@@ -92,109 +85,159 @@ __device__ __forceinline__ void store_unit(uint16_t (*Xs)[SKP], int crow, int tc
   }
 }
 
-struct StageRegs {
-  uint32_t u[UNITS][4][4];
+template <int U>
+struct StageRegsT {
+  uint32_t u[U][4][4];
 };
 
+template <bool FAST, int U>
 __device__ __forceinline__ void load_stage(const uint16_t* __restrict__ X, int64_t kend,
                                            int64_t ldx, int C, int64_t t0, int cbase, bool cvec,
-                                           StageRegs& r) {
+                                           StageRegsT<U>& r) {
 #pragma unroll
-  for (int q = 0; q < UNITS; ++q) load_unit(X, kend, ldx, C, t0 + 32 * q, cbase, cvec, r.u[q]);
+  for (int q = 0; q < U; ++q)
+    load_unit<FAST>(X, kend, ldx, C, t0 + 32 * q, cbase, cvec, r.u[q]);
 }
 
-__device__ __forceinline__ void store_stage(uint16_t (*Xs)[SKP], int crow, int tcol,
-                                            const StageRegs& r) {
+template <int U, int PITCH>
+__device__ __forceinline__ void store_stage(uint16_t (*Xs)[PITCH], int crow, int tcol,
+                                            const StageRegsT<U>& r) {
 #pragma unroll
-  for (int q = 0; q < UNITS; ++q) store_unit(Xs, crow, tcol + 32 * q, r.u[q]);
+  for (int q = 0; q < U; ++q) store_unit<PITCH>(Xs, crow, tcol + 32 * q, r.u[q]);
 }
+
+// Upper-triangle tile of linear index lin, in bands of 4 tile rows: within
+// a band the tile columns ascend and each column lists the band's rows, so
+// 32 consecutive indices form a 4 x 8 block of tiles that shares 12
+// operand panels.
+__device__ __forceinline__ void tile_band(int lin, int nt, int& ti, int& tj) {
+  for (int r0 = 0; r0 < nt; r0 += 4) {
+    const int r1 = min(r0 + 4, nt) - 1;
+    for (int c = r0; c < nt; ++c) {
+      const int cnt = min(r1, c) - r0 + 1;
+      if (lin < cnt) { ti = r0 + lin; tj = c; return; }
+      lin -= cnt;
+    }
+  }
+  ti = tj = 0;
+}
+
+// Workgroup id -> linear tile index such that the workgroups one XCD
+// receives (every 8th id) take consecutive indices.
+__device__ __forceinline__ int xcd_chunk(int id, int nwg) {
+  const int q = nwg / 8, r = nwg % 8, x = id % 8, k = id / 8;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + k;
+}
+
+// Producer/consumer variant: 12 wavefronts per 256 x 256 tile.
+//  * 8 consumer wavefronts (2 x 4, 128 x 64 outputs each) only read operand
+//    fragments from LDS and issue MFMAs.
+//  * 4 producer wavefronts load X, transpose 4-token x 8-channel units in
+//    registers and store them channel-major into a ring of 3 LDS stages of
+//    SKQ tokens; loads run two stages ahead of their LDS store, so global
+//    latency stays off the MFMA wavefronts.
+// One barrier per stage: at iteration c the consumers read stage c while
+// the producers store stage c + 2 (its buffer was last read at c - 1) and
+// issue the loads of stage c + 4.
+// Barrier for LDS traffic only: waits for this wavefront's LDS operations,
+// not for its outstanding global loads (__syncthreads waits for both, which
+// would drain the producers' prefetch at every stage).
+__device__ __forceinline__ void sync_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+constexpr int SKQ = 32;                 // tokens per stage
+constexpr int SKQP = SKQ + 8;           // padded LDS row (halves)
+constexpr int SYRKP_THREADS = 768;
+constexpr int NSTAGE = 3;
+constexpr int NSET = 4;                 // stages in flight in producer registers
 
 template <typename T8>
-__device__ __forceinline__ void syrk_stage(const uint16_t (*XI)[SKP], const uint16_t (*XJ)[SKP],
-                                           int wm, int wn, int r16, int kof0, f4_t (&acc)[8][4]) {
+__device__ __forceinline__ void syrk_stage_p(const uint16_t (*XI)[SKQP],
+                                             const uint16_t (*XJ)[SKQP], int wm, int wn,
+                                             int r16, int kof, f4_t (&acc)[8][4]) {
+  T8 b[4];
 #pragma unroll
-  for (int ks = 0; ks < SK; ks += 32) {
-    const int kof = ks + kof0;
-    T8 b[4];
+  for (int j = 0; j < 4; ++j) b[j] = *(const T8*)&XJ[wn + j * 16 + r16][kof];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = *(const T8*)&XJ[wn + j * 16 + r16][kof];
+  for (int i = 0; i < 8; ++i) {
+    const T8 a = *(const T8*)&XI[wm + i * 16 + r16][kof];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const T8 a = *(const T8*)&XI[wm + i * 16 + r16][kof];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T8>(a, b[j], acc[i][j]);
-    }
+    for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T8>(a, b[j], acc[i][j]);
   }
 }
 
-template <typename T8>
-__global__ __launch_bounds__(SYRK_THREADS) void k_syrk16(const uint16_t* __restrict__ X,
-                                                         int64_t ntok, int64_t ldx, int C,
-                                                         float* S, int64_t lds, int nt,
-                                                         int64_t span, float* P) {
-  __shared__ __attribute__((aligned(16))) uint16_t Xs[2][2][ST][SKP];
+template <typename T8, bool FAST>
+__global__ __launch_bounds__(SYRKP_THREADS) void k_syrk16p(const uint16_t* __restrict__ X,
+                                                           int64_t ntok, int64_t ldx, int C,
+                                                           float* S, int64_t lds, int nt,
+                                                           int64_t span, float* P) {
+  __shared__ __attribute__((aligned(16))) uint16_t Xs[NSTAGE][2][ST][SKQP];
   int ti, tj;
-  tile_of(blockIdx.x, nt, ti, tj);
+  tile_band(xcd_chunk(blockIdx.x, gridDim.x), nt, ti, tj);
   const int64_t k_beg = (int64_t)blockIdx.y * span;
   const int64_t k_end = k_beg + span < ntok ? k_beg + span : ntok;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
+  const int nch = k_end > k_beg ? (int)((k_end - k_beg + SKQ - 1) / SKQ) : 0;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool diag = ti == tj;
-  // token group fastest across lanes: the 8 channel rows a store
-  // instruction touches then fall on distinct LDS bank groups
-  const int side = tid >> 8, lt = tid & 255;
-  const int tg = lt & 7, cg = lt >> 3;             // 8 token groups x 32 channel groups
-  const int cbase = (side ? tj : ti) * ST + cg * 8;
-  const bool cvec = (cbase + 8 <= C) && ((ldx & 7) == 0) && ((((uintptr_t)X) & 15) == 0);
-  const bool loader = !(diag && side);
+  if (wave >= 8) {
+    // ---------------- producers ----------------
+    const int p = tid - 512, tg = p & 7, cg = p >> 3;   // 8 token groups x 32 channel groups
+    const bool vecok = ((ldx & 7) == 0) && ((((uintptr_t)X) & 15) == 0);
+    const int cb0 = ti * ST + cg * 8, cb1 = tj * ST + cg * 8;
+    const bool cv0 = vecok && cb0 + 8 <= C, cv1 = vecok && cb1 + 8 <= C;
+    const int64_t t_lane = k_beg + tg * 4;
+    StageRegsT<1> r[NSET][2];                           // [set][side]
+    auto load = [&](int stage, int set) {
+      const int64_t t0 = t_lane + (int64_t)stage * SKQ;
+      load_stage<FAST, 1>(X, k_end, ldx, C, t0, cb0, cv0, r[set][0]);
+      if (!diag) load_stage<FAST, 1>(X, k_end, ldx, C, t0, cb1, cv1, r[set][1]);
+    };
+    auto store = [&](int stage, int set) {
+      const int b = stage % NSTAGE;
+      store_stage<1, SKQP>(Xs[b][0], cg * 8, tg * 4, r[set][0]);
+      if (!diag) store_stage<1, SKQP>(Xs[b][1], cg * 8, tg * 4, r[set][1]);
+    };
+    // stages 0 and 1 go straight to LDS; stage 2 + q is held in set q
+    if (nch > 0) load(0, 0);
+    if (nch > 0) store(0, 0);
+    if (nch > 1) load(1, 0);
+    if (nch > 1) store(1, 0);
+#pragma unroll
+    for (int q = 0; q < NSET; ++q)
+      if (2 + q < nch) load(2 + q, q);
+    sync_lds();
+    // at iteration c: store stage c + 2 (set c % NSET), load stage
+    // c + 2 + NSET into the same set; unrolled by NSET so the set index is
+    // static
+    for (int c0 = 0; c0 < nch; c0 += NSET) {
+#pragma unroll
+      for (int q = 0; q < NSET; ++q) {
+        const int c = c0 + q;
+        if (c >= nch) break;
+        if (c + 2 < nch) store(c + 2, q);
+        if (c + 2 + NSET < nch) load(c + 2 + NSET, q);
+        sync_lds();
+      }
+    }
+    return;
+  }
+  // ---------------- consumers ----------------
+  const int lane = tid & 63;
+  const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
   f4_t acc[8][4];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
-  const int nch = k_end > k_beg ? (int)((k_end - k_beg + SK - 1) / SK) : 0;
-  const int64_t t_lane = k_beg + tg * 4;
-  const int r16 = lane & 15, kof0 = (lane >> 4) * 8;
-#if CRBQ_SYRK_DIST == 1
-  StageRegs ra;
-  if (nch > 0 && loader) {
-    load_stage(X, k_end, ldx, C, t_lane, cbase, cvec, ra);
-    store_stage(Xs[0][side], cg * 8, tg * 4, ra);
-  }
-  __syncthreads();
+  const int r16 = lane & 15, kof = (lane >> 4) * 8;
+  sync_lds();
   for (int c = 0; c < nch; ++c) {
-    const int buf = c & 1;
-    const bool more = c + 1 < nch;
-    if (more && loader) load_stage(X, k_end, ldx, C, t_lane + (int64_t)(c + 1) * SK, cbase,
-                                   cvec, ra);
-    syrk_stage<T8>(Xs[buf][0], diag ? Xs[buf][0] : Xs[buf][1], wm, wn, r16, kof0, acc);
-    if (more && loader) store_stage(Xs[buf ^ 1][side], cg * 8, tg * 4, ra);
-    __syncthreads();
+    const int b = c % NSTAGE;
+    syrk_stage_p<T8>(Xs[b][0], diag ? Xs[b][0] : Xs[b][1], wm, wn, r16, kof, acc);
+    sync_lds();
   }
-#else
-  // two stages in flight in registers (ra: next, rb: the one after)
-  StageRegs ra, rb;
-  if (nch > 0 && loader) {
-    load_stage(X, k_end, ldx, C, t_lane, cbase, cvec, ra);
-    store_stage(Xs[0][side], cg * 8, tg * 4, ra);
-  }
-  if (nch > 1 && loader) load_stage(X, k_end, ldx, C, t_lane + SK, cbase, cvec, ra);
-  if (nch > 2 && loader) load_stage(X, k_end, ldx, C, t_lane + 2 * SK, cbase, cvec, rb);
-  __syncthreads();
-  for (int c = 0; c < nch; c += 2) {
-    syrk_stage<T8>(Xs[0][0], diag ? Xs[0][0] : Xs[0][1], wm, wn, r16, kof0, acc);
-    if (loader && c + 1 < nch) store_stage(Xs[1][side], cg * 8, tg * 4, ra);
-    if (loader && c + 3 < nch)
-      load_stage(X, k_end, ldx, C, t_lane + (int64_t)(c + 3) * SK, cbase, cvec, ra);
-    __syncthreads();
-    if (c + 1 >= nch) break;
-    syrk_stage<T8>(Xs[1][0], diag ? Xs[1][0] : Xs[1][1], wm, wn, r16, kof0, acc);
-    if (loader && c + 2 < nch) store_stage(Xs[0][side], cg * 8, tg * 4, rb);
-    if (loader && c + 4 < nch)
-      load_stage(X, k_end, ldx, C, t_lane + (int64_t)(c + 4) * SK, cbase, cvec, rb);
-    __syncthreads();
-  }
-#endif
   const int c16 = lane & 15, r4 = (lane >> 4) * 4;
   float* out = P ? P + (size_t)blockIdx.y * (size_t)C * lds : S;
 #pragma unroll
@@ -206,8 +249,8 @@ __global__ __launch_bounds__(SYRK_THREADS) void k_syrk16(const uint16_t* __restr
         const int gi = ti * ST + wm + i * 16 + r4 + r;
         const int gj = tj * ST + wn + j * 16 + c16;
         if (gi < C && gj < C && gi <= gj) {
-          float* p = out + (int64_t)gi * lds + gj;
-          *p = P ? acc[i][j][r] : *p + acc[i][j][r];
+          float* q = out + (int64_t)gi * lds + gj;
+          *q = P ? acc[i][j][r] : *q + acc[i][j][r];
         }
       }
 }
@@ -360,16 +403,20 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
   // the partial buffers are laid out like S (row stride lds)
   while (ns > 1 && (!ws || (size_t)ns * (size_t)C * (size_t)lds * sizeof(float) > ws_bytes)) --ns;
   int64_t span = (ntok + ns - 1) / ns;
-  span = (span + crbq::SK - 1) / crbq::SK * crbq::SK;
+  span = (span + crbq::SKQ - 1) / crbq::SKQ * crbq::SKQ;
   ns = (int)((ntok + span - 1) / span);
   float* P = ns > 1 ? (float*)ws : nullptr;
   dim3 grid((unsigned)ntiles, (unsigned)ns);
-  if (dtype == CRBQ_F16)
-    crbq::k_syrk16<h8_t><<<grid, crbq::SYRK_THREADS, 0, s>>>((const uint16_t*)X, ntok, ldx, (int)C, S, lds, nt,
-                                              span, P);
-  else
-    crbq::k_syrk16<b8_t><<<grid, crbq::SYRK_THREADS, 0, s>>>((const uint16_t*)X, ntok, ldx, (int)C, S, lds, nt,
-                                              span, P);
+  const bool fast = (C % 8 == 0) && (ldx % 8 == 0) && ((((uintptr_t)X) & 15) == 0);
+#define CRBQ_SYRK_GO(T8_, F_)                                                            \
+  crbq::k_syrk16p<T8_, F_><<<grid, crbq::SYRKP_THREADS, 0, s>>>(                         \
+      (const uint16_t*)X, ntok, ldx, (int)C, S, lds, nt, span, P)
+  if (dtype == CRBQ_F16) {
+    if (fast) CRBQ_SYRK_GO(h8_t, true); else CRBQ_SYRK_GO(h8_t, false);
+  } else {
+    if (fast) CRBQ_SYRK_GO(b8_t, true); else CRBQ_SYRK_GO(b8_t, false);
+  }
+#undef CRBQ_SYRK_GO
   CRBQ_LAUNCH_CHECK();
   if (P) {
     crbq::k_sum_splits<<<(unsigned)((C * C + 255) / 256), 256, 0, s>>>(P, ns, (int)C, S, lds);
