@@ -70,64 +70,91 @@ def make_inputs(dev, ntok, seed=0):
 
 
 def one_layer(subs, W0, X, method, timing):
+    """One step.  HIP events bracket every Hessian launch on the stream it
+    runs on (torch's current stream, where add_batch enqueues the SYRK)."""
     from crb_amd.driver import LayerQuantizer, PhaseTimes, Sublayer
     sl = [Sublayer(n, W0[n].clone(), g) for (n, r, c, g) in subs]
     lq = LayerQuantizer(sl, method=method)
     pt = PhaseTimes() if timing else None
     h_ev = []
+    stream = torch.cuda.current_stream()
     for grp, x in X.items():
-        if timing:
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
         lq.add_batch(grp, x)
-        if timing:
-            b.record()
-            h_ev.append((grp, x.shape[1], a, b))
+        b.record(stream)
+        h_ev.append((grp, x.shape[1], a, b))
     lq.quantize(pt)
     return lq, pt, h_ev
 
 
-def cpu_baseline(budget_s=20.0):
+def load_traffic(name):
+    """HBM bytes per launch of the dominant kernel, measured by rocprofv3
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel) and recorded in
+    profiles/; None if no such measurement is recorded."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                vals["t"] = float(line.split(":", 1)[1])
+    return vals.get("t")
+
+
+def cpu_baseline(nseq=32, nblocks=48):
     """Time the test-only CPU oracle (torch-CPU restatement of the reference
-    path) on a bounded sample and extrapolate to one OPT-6.7B layer."""
+    path) on a bounded sample of the workload (about 10-20 s on 16 cores)
+    and extrapolate to one OPT-6.7B layer."""
     from oracle import crb_oracle as O
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
     C = 4096
-    # Hessian: 2 sequences x 2048 tokens of a 4096-channel input
-    X = (torch.randn(2, 2048, C) * 0.5).half()
+    g = torch.Generator().manual_seed(0)
+    # Hessian: nseq sequences x 2048 tokens of a 4096-channel input, fed
+    # one sequence per add_batch as run.py's hooks do
+    X = (torch.randn(nseq, 2048, C, generator=g) * 0.5).half()
     H = torch.zeros(C, C)
     n = 0
     t0 = time.time()
-    for s in range(2):
+    for s in range(nseq):
         H, n = O.hessian_add_batch(H, n, X[s:s + 1].float())
     t_h = time.time() - t0
+    del X
     # per layer: 128 sequences into each of the 4 distinct inputs (3 of
     # 4096 channels, 1 of 16384); the work scales with tokens * C^2
-    h_layer = t_h * (128 / 2) * (3 * 4096 ** 2 + 16384 ** 2) / 4096 ** 2
-    # inverse factor of a 4096 Hessian, scaled by C^3 to the 4 distinct ones
-    W = torch.randn(4096, C) * 0.02
+    h_layer = t_h * (128 / nseq) * (3 * 4096 ** 2 + 16384 ** 2) / 4096 ** 2
+    # inverse factors: a 4096 one (x3 inputs) and an 8192 one scaled by
+    # C^3 to the 16384 input
+    W = torch.randn(4096, C, generator=g) * 0.02
     H += torch.eye(C) * float(H.diag().mean())
     t0 = time.time()
     O.hinv_upper(H.clone(), W.clone(), 0.01)
-    t_u = time.time() - t0
-    u_layer = t_u * (3 + 64)
-    # block loop: first 2 blocks of a 4096x4096 sublayer; a layer has
-    # sum(R*C)/128 = 1.57M row-blocks, the sample 2*4096
+    t_u4 = time.time() - t0
+    H8 = torch.block_diag(H, H) + 0.01 * torch.eye(2 * C)
     t0 = time.time()
-    O.fasterquant(W, H, method="crb", max_blocks=2)
-    t_b = time.time() - t0 - t_u   # fasterquant recomputes the factor
+    O.hinv_upper(H8, torch.zeros(1, 2 * C), 0.01)
+    t_u8 = time.time() - t0
+    del H8
+    u_layer = 3 * t_u4 + 8 * t_u8
+    # block loop: the first nblocks CRB blocks of a 4096 x 4096 sublayer;
+    # a layer has sum(R*C)/128 = 1.57M row-blocks, the sample nblocks*4096
+    t0 = time.time()
+    O.fasterquant(W, H, method="crb", max_blocks=nblocks)
+    t_b = time.time() - t0 - t_u4   # fasterquant recomputes the factor
     rowblocks = (4 * 4096 * 4096 + 2 * 4096 * 16384) / 128
-    b_layer = max(t_b, 0.0) / (2 * 4096) * rowblocks
+    b_layer = max(t_b, 0.0) / (nblocks * 4096) * rowblocks
     total = h_layer + u_layer + b_layer
     return {
         "value": total, "unit": "s/layer", "cores": ncores, "kind": "port",
-        "sample": (f"oracle (torch-CPU restatement of bigptq/binary/utils) on this host: "
-                   f"Hessian of 2x2048 tokens x 4096 ch ({t_h:.2f}s), inverse factor of a "
-                   f"4096 Hessian ({t_u:.2f}s), first 2 CRB blocks of a 4096x4096 sublayer "
-                   f"({t_b:.2f}s); extrapolated to one OPT-6.7B layer by token count, C^3 "
-                   f"and row-blocks"),
+        "sample": (f"oracle (torch-CPU restatement of bigptq/binary/utils) on this host, "
+                   f"{t_h + t_u4 + t_u8 + t_b + t_u4:.1f}s of CPU work: Hessian of {nseq}x2048 "
+                   f"tokens x 4096 ch ({t_h:.2f}s), inverse factors of a 4096 and an 8192 "
+                   f"Hessian ({t_u4:.2f}s, {t_u8:.2f}s), first {nblocks} CRB blocks of a "
+                   f"4096x4096 sublayer ({t_b:.2f}s); extrapolated to one OPT-6.7B layer by "
+                   f"token count, C^3 and row-blocks"),
         "split_s": {"hessian": h_layer, "hinv": u_layer, "blocks": b_layer},
         "cpu": platform.processor() or platform.machine(),
         "blas": torch.__config__.show().split("BLAS_INFO=")[-1].split(",")[0]
@@ -143,7 +170,18 @@ def main():
     ap.add_argument("--method", default="crb")
     ap.add_argument("--tokens", type=int, default=128 * 2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only copy a 1 GiB buffer 3 times: the known-size copy kernel that "
+                         "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE for the traffic figure")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        x = torch.ones(256 * 1024 * 1024, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": x.numel() * 4, "copies": 3}))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the path shards by "
                                    "sublayer and by calibration tokens (see DESIGN.md), "
@@ -164,22 +202,25 @@ def main():
         print(f"[bench] warmup {w} done", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     t0 = time.time()
+    evs = []
     for k in range(args.steps):
-        one_layer(subs, W0, X, args.method, timing=False)
+        evs.append(one_layer(subs, W0, X, args.method, timing=False)[2])
     torch.cuda.synchronize()
     dt = (time.time() - t0) / args.steps
     print(f"[bench] timed {args.steps} steps: {dt:.4f} s/layer", file=sys.stderr, flush=True)
-    # phase split and per-launch kernel timing (separate, instrumented step)
+    # dominant kernel: the Hessian SYRK of the fc2 input (C = 16384), one
+    # launch per step; its duration is averaged over the timed steps
+    fc2_ms = [a.elapsed_time(b) for ev in evs for (g, C, a, b) in ev if g == "fc2"]
+    T = args.tokens
+    Cfc2 = 16384
+    flops = T * Cfc2 * (Cfc2 + 1)
+    t_launch = sum(fc2_ms) / len(fc2_ms) / 1e3
+    achieved = flops / t_launch
+    # phase split (separate, instrumented step)
     lq, pt, h_ev = one_layer(subs, W0, X, args.method, timing=True)
     torch.cuda.synchronize()
     h_ms = {g: a.elapsed_time(b) for (g, C, a, b) in h_ev}
     hess_ms = sum(h_ms.values())
-    # dominant kernel: Hessian SYRK of the fc2 input (C = 16384), one launch
-    T = args.tokens
-    Cfc2 = 16384
-    flops = T * Cfc2 * (Cfc2 + 1)
-    t_launch = h_ms["fc2"] / 1e3
-    achieved = flops / t_launch
     cols = sum(c for (_, r, c, _) in subs)
     out = {
         "metric": METRIC, "value": round(dt, 5), "unit": "s/layer", "n_gpus": 1,
@@ -194,10 +235,12 @@ def main():
                      "quantize_overlapped": round(pt.quantize_ms, 3),
                      "hinv": {g: round(v, 3) for g, v in pt.hinv_ms.items()},
                      "factor_plus_blocks": {g: round(v, 3) for g, v in pt.chain_ms.items()}},
-        "roofline": {"bound": "mfma", "kernel": "k_syrk16 (Hessian, fc2 input C=16384)",
+        "roofline": {"bound": "mfma", "kernel": "k_syrk16p (Hessian, fc2 input C=16384)",
                      "achieved": round(achieved / 1e12, 2), "peak": PEAK_F16 / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_F16, 4),
-                     "traffic": None},
+                     "launch_ms": round(t_launch * 1e3, 3),
+                     "algorithmic_flop": flops,
+                     "traffic": load_traffic("syrk_fc2_opt67b_traffic.md")},
     }
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
