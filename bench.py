@@ -50,11 +50,14 @@ def make_layer(dev, seed=0):
     return subs, Ws
 
 
-def make_inputs(dev, ntok, seed=0):
-    """One [ntok, C] fp16 activation per distinct sublayer input.  The fc2
-    input (C = 16384) comes first: its Hessian, factor and block loop form
-    the layer's longest chain, and the other inputs' work overlaps it."""
-    shapes = {"fc2": 16384, "qkv": 4096, "out": 4096, "fc1": 4096}
+def make_inputs(dev, ntok, seed=0, fc2_first=True):
+    """One [ntok, C] fp16 activation per distinct sublayer input, in the
+    order their Hessians are accumulated.  With fc2_first the fc2 input
+    (C = 16384), whose Hessian, factor and block loop form the layer's
+    longest chain, comes first and the other inputs' work overlaps it."""
+    shapes = {"qkv": 4096, "out": 4096, "fc1": 4096, "fc2": 16384}
+    if fc2_first:
+        shapes = {"fc2": 16384, **{k: v for k, v in shapes.items() if k != "fc2"}}
     X = {}
     for j, (grp, C) in enumerate(shapes.items()):
         s = synth.channel_scales(C, seed + j, kind="student_t4", device=dev)
@@ -170,6 +173,8 @@ def main():
     ap.add_argument("--method", default="crb")
     ap.add_argument("--tokens", type=int, default=128 * 2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--fc2-last", action="store_true",
+                    help="accumulate the fc2 input's Hessian last (forward order)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy a 1 GiB buffer 3 times: the known-size copy kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE for the traffic figure")
@@ -194,7 +199,7 @@ def main():
     print(f"[bench] building OPT-6.7B layer inputs ({args.tokens} tokens)", file=sys.stderr,
           flush=True)
     subs, W0 = make_layer(dev)
-    X = make_inputs(dev, args.tokens)
+    X = make_inputs(dev, args.tokens, fc2_first=not args.fc2_last)
     torch.cuda.synchronize()
     for w in range(args.warmup):
         one_layer(subs, W0, X, args.method, timing=False)
