@@ -73,23 +73,16 @@ def make_inputs(dev, ntok, seed=0, fc2_first=True):
 
 
 def one_layer(subs, W0, X, method, timing):
-    """One step.  HIP events bracket every Hessian launch on the stream it
-    runs on (torch's current stream, where add_batch enqueues the SYRK)."""
+    """One step.  The driver brackets every Hessian launch with HIP events on
+    the stream it runs on (LayerQuantizer.syrk_ms)."""
     from crb_amd.driver import LayerQuantizer, PhaseTimes, Sublayer
     sl = [Sublayer(n, W0[n].clone(), g) for (n, r, c, g) in subs]
     lq = LayerQuantizer(sl, method=method)
     pt = PhaseTimes() if timing else None
-    h_ev = []
-    stream = torch.cuda.current_stream()
     for grp, x in X.items():
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
         lq.add_batch(grp, x)
-        b.record(stream)
-        h_ev.append((grp, x.shape[1], a, b))
     lq.quantize(pt)
-    return lq, pt, h_ev
+    return lq, pt
 
 
 def load_traffic(name):
@@ -205,26 +198,32 @@ def main():
         one_layer(subs, W0, X, args.method, timing=False)
         torch.cuda.synchronize()
         print(f"[bench] warmup {w} done", file=sys.stderr, flush=True)
+    from crb_amd import kernels
     torch.cuda.synchronize()
+    kernels.syrk_timing_collect()
+    # the library brackets every SYRK kernel launch with HIP events on the
+    # stream it is launched on
+    kernels.syrk_timing(True)
     t0 = time.time()
-    evs = []
     for k in range(args.steps):
-        evs.append(one_layer(subs, W0, X, args.method, timing=False)[2])
+        one_layer(subs, W0, X, args.method, timing=False)
     torch.cuda.synchronize()
     dt = (time.time() - t0) / args.steps
+    kernels.syrk_timing(False)
     print(f"[bench] timed {args.steps} steps: {dt:.4f} s/layer", file=sys.stderr, flush=True)
     # dominant kernel: the Hessian SYRK of the fc2 input (C = 16384), one
     # launch per step; its duration is averaged over the timed steps
-    fc2_ms = [a.elapsed_time(b) for ev in evs for (g, C, a, b) in ev if g == "fc2"]
     T = args.tokens
     Cfc2 = 16384
+    fc2_ms = [ms for (c, ms) in kernels.syrk_timing_collect() if c == Cfc2]
+    assert len(fc2_ms) == args.steps, fc2_ms
     flops = T * Cfc2 * (Cfc2 + 1)
     t_launch = sum(fc2_ms) / len(fc2_ms) / 1e3
     achieved = flops / t_launch
     # phase split (separate, instrumented step)
-    lq, pt, h_ev = one_layer(subs, W0, X, args.method, timing=True)
+    lq, pt = one_layer(subs, W0, X, args.method, timing=True)
     torch.cuda.synchronize()
-    h_ms = {g: a.elapsed_time(b) for (g, C, a, b) in h_ev}
+    h_ms = {g: lq.syrk_ms(g) for g in X}
     hess_ms = sum(h_ms.values())
     cols = sum(c for (_, r, c, _) in subs)
     out = {
@@ -240,7 +239,7 @@ def main():
                      "quantize_overlapped": round(pt.quantize_ms, 3),
                      "hinv": {g: round(v, 3) for g, v in pt.hinv_ms.items()},
                      "factor_plus_blocks": {g: round(v, 3) for g, v in pt.chain_ms.items()}},
-        "roofline": {"bound": "mfma", "kernel": "k_syrk16p (Hessian, fc2 input C=16384)",
+        "roofline": {"bound": "mfma", "kernel": "k_syrk16k (Hessian SYRK, fc2 input C=16384)",
                      "achieved": round(achieved / 1e12, 2), "peak": PEAK_F16 / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_F16, 4),
                      "launch_ms": round(t_launch * 1e3, 3),

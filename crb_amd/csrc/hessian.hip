@@ -7,11 +7,21 @@
 // fp32 accumulate) computes the same sums up to summation order.  fp32
 // inputs use v_mfma_f32_16x16x4_f32.
 //
-// Token-major X[t][c] is staged through LDS channel-major (Xs[c][t]) so each
-// MFMA lane reads its 8 consecutive tokens with one ds_read_b128: a loading
-// thread reads a 4-token x 8-channel unit with four 16-byte loads and
-// transposes it in registers with v_perm_b32 before one 8-byte LDS store per
-// channel.
+// Each MFMA lane reads its 8 consecutive tokens with one ds_read_b128 from a
+// channel-major LDS stage (Xs[c][t]).  Two ways to get there from the
+// token-major activations X[t][c]:
+//  * channel-major path (k_xpose16 + k_syrk16k, used when the workspace can
+//    hold a transposed copy): X is transposed once into the workspace and
+//    the SYRK streams token-contiguous rows straight into LDS;
+//  * token-major path (k_syrk16p): a loading thread reads a 4-token x
+//    8-channel unit with four 16-byte loads and transposes it in registers
+//    with v_perm_b32 before one 8-byte LDS store per channel.
+#include <stdlib.h>
+
+#include <mutex>
+#include <type_traits>
+#include <vector>
+
 #include "common.h"
 
 namespace crbq {
@@ -255,6 +265,196 @@ __global__ __launch_bounds__(SYRKP_THREADS) void k_syrk16p(const uint16_t* __res
       }
 }
 
+// ---------------------------------------------------------------------------
+// Channel-major path.  X[t][c] is first transposed into a workspace
+// Xt[c][t] (k_xpose16), zero-padded to Cp = 256-multiple channels and tpad =
+// 64-multiple tokens; k_syrk16k then reads operand rows that are already
+// token-contiguous, so a loading thread moves 16 bytes from global memory to
+// LDS without a register transpose and every stage touches whole 128-byte
+// lines.  For the same split boundaries both paths issue the same MFMAs on
+// the same 32-token slices in the same order, so their sums are bitwise
+// equal.
+
+// X[t][c] -> Xt[c][t] for c < Cp, t < tpad; zeros where t >= ntok or
+// c >= C.  A wavefront moves 64 tokens x 64 channels; each lane transposes
+// an 8-token x 8-channel block in registers (v_perm_b32), reading 16 bytes
+// of 8 token rows and writing 16 bytes of 8 channel rows, so both sides are
+// whole 128-byte lines per 8 lanes.
+template <bool FAST>
+__global__ __launch_bounds__(256) void k_xpose16(const uint16_t* __restrict__ X, int64_t ntok,
+                                                 int64_t ldx, int C, uint16_t* __restrict__ Xt,
+                                                 int64_t ldt, int64_t tpad, int Cp) {
+  const int lane = threadIdx.x & 63;
+  const int tg = lane & 7, cg = lane >> 3;
+  const int nwc = Cp / 64;
+  const int64_t nw = (tpad / 64) * nwc;
+  for (int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); w < nw;
+       w += (int64_t)gridDim.x * 4) {
+    const int64_t wt = w / nwc;
+    const int c0 = (int)(w - wt * nwc) * 64 + cg * 8;
+    const int64_t t0 = wt * 64 + tg * 8;
+    uint32_t in[8][4];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int64_t t = t0 + r;
+      if (FAST) {
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (t < ntok && c0 < C) v = *(const uint4*)(X + t * ldx + c0);
+        in[r][0] = v.x; in[r][1] = v.y; in[r][2] = v.z; in[r][3] = v.w;
+      } else {
+        uint16_t h[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          h[q] = (t < ntok && c0 + q < C) ? X[t * ldx + c0 + q] : (uint16_t)0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) in[r][q] = (uint32_t)h[2 * q] | ((uint32_t)h[2 * q + 1] << 16);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+      uint4 o;
+      o.x = __builtin_amdgcn_perm(in[1][c >> 1], in[0][c >> 1], sel);
+      o.y = __builtin_amdgcn_perm(in[3][c >> 1], in[2][c >> 1], sel);
+      o.z = __builtin_amdgcn_perm(in[5][c >> 1], in[4][c >> 1], sel);
+      o.w = __builtin_amdgcn_perm(in[7][c >> 1], in[6][c >> 1], sel);
+      *(uint4*)(Xt + (int64_t)(c0 + c) * ldt + t0) = o;
+    }
+  }
+}
+
+constexpr int KQ = 64;                  // tokens per stage (one 128-byte line per row)
+constexpr int KQP = KQ + 8;             // LDS row pitch (halves): 16 rows hit distinct banks
+constexpr int KUPS = ST * KQ / 8 / 256; // 16-byte units per producer thread per side
+typedef unsigned u4_t __attribute__((ext_vector_type(4)));
+
+// Producer/consumer kernel on Xt (12 wavefronts per 256 x 256 tile):
+//  * 8 consumer wavefronts (2 x 4, 128 x 64 outputs each) read operand
+//    fragments from a 2-stage LDS ring and issue MFMAs, two 32-token
+//    slices per stage;
+//  * 4 producer wavefronts load each stage with raw buffer loads (one lane
+//    offset per side, per-row offsets in scalar registers; a tile's
+//    256-row panel spans less than 2^31 bytes) into one of two register
+//    sets and store it to LDS.  At iteration c they store stage c + 1 and
+//    issue the loads of stage c + 3; the loads are never predicated (past
+//    the last stage they repeat it) so the compiler's wait counts stay
+//    exact and one whole stage of loads is always in flight.
+// Requires Cp = nt * 256 rows in Xt, ldt, span and tpad multiples of KQ.
+template <typename T8>
+__global__ __launch_bounds__(SYRKP_THREADS) void k_syrk16k(const uint16_t* __restrict__ Xt,
+                                                           int64_t ldt, int64_t tpad, int C,
+                                                           float* S, int64_t lds, int nt,
+                                                           int64_t span, float* P) {
+  __shared__ __attribute__((aligned(16))) uint16_t Xs[2][2][ST][KQP];
+  int ti, tj;
+  tile_band(xcd_chunk(blockIdx.x, gridDim.x), nt, ti, tj);
+  const int64_t k_beg = (int64_t)blockIdx.y * span;
+  const int64_t k_end = k_beg + span < tpad ? k_beg + span : tpad;
+  const int nch = k_end > k_beg ? (int)((k_end - k_beg) / KQ) : 0;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (wave >= 8) {
+    // ---------------- producers ----------------
+    const int p = tid - 512;
+    constexpr int LPR = KQ / 8;           // lanes per row
+    constexpr int RPI = 64 / LPR;         // rows per load instruction
+    const int rsub = (p & 63) / LPR, chunk = (p & 63) % LPR;
+    const int rbase = (p >> 6) * (ST / 4) + rsub;
+    const int nrec = (int)((int64_t)ST * ldt * 2);
+    const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(Xt + (int64_t)ti * ST * ldt + k_beg), 0, nrec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(Xt + (int64_t)tj * ST * ldt + k_beg), 0, nrec, 0x00020000);
+    const int voff = (rbase * (int)ldt + chunk * 8) * 2;
+    const int rstep = RPI * (int)ldt * 2;
+    struct Set { u4_t v[2][KUPS]; };
+    auto load = [&](int stage, Set& r) {
+      const int k = stage * KQ * 2;
+#pragma unroll
+      for (int i = 0; i < KUPS; ++i) {
+        r.v[0][i] = __builtin_amdgcn_raw_buffer_load_b128(rs0, voff, k + i * rstep, 0);
+        r.v[1][i] = __builtin_amdgcn_raw_buffer_load_b128(rs1, voff, k + i * rstep, 0);
+      }
+    };
+    uint16_t* dst = &Xs[0][0][rbase][chunk * 8];
+    constexpr int SIDE = ST * KQP, BUF = 2 * ST * KQP;
+    auto store = [&](auto bsel, const Set& r) {
+      constexpr int b = decltype(bsel)::value;
+#pragma unroll
+      for (int i = 0; i < KUPS; ++i) {
+        *(u4_t*)(dst + b * BUF + i * RPI * KQP) = r.v[0][i];
+        *(u4_t*)(dst + b * BUF + SIDE + i * RPI * KQP) = r.v[1][i];
+      }
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    Set r0, r1;
+    if (nch > 0) {
+      const int last = nch - 1;
+      load(0, r0);
+      load(min(1, last), r1);
+      store(B0{}, r0);
+      load(min(2, last), r0);
+      sync_lds();
+      for (int c = 0;; c += 2) {
+        store(B1{}, r1);
+        load(min(c + 3, last), r1);
+        sync_lds();
+        if (c + 1 >= nch) break;
+        store(B0{}, r0);
+        load(min(c + 4, last), r0);
+        sync_lds();
+        if (c + 2 >= nch) break;
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+      sync_lds();
+    }
+    return;
+  }
+  // ---------------- consumers ----------------
+  const int lane = tid & 63;
+  const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
+  f4_t acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+  const int r16 = lane & 15, kof = (lane >> 4) * 8;
+  sync_lds();
+  for (int c = 0; c < nch; ++c) {
+    const int b = c & 1;
+#pragma unroll
+    for (int h = 0; h < KQ / 32; ++h) {
+      T8 bb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bb[j] = *(const T8*)&Xs[b][1][wn + j * 16 + r16][kof + 32 * h];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const T8 a = *(const T8*)&Xs[b][0][wm + i * 16 + r16][kof + 32 * h];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T8>(a, bb[j], acc[i][j]);
+      }
+    }
+    sync_lds();
+  }
+  const int c16 = lane & 15, r4 = (lane >> 4) * 4;
+  float* out = P ? P + (size_t)blockIdx.y * (size_t)C * lds : S;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int gi = ti * ST + wm + i * 16 + r4 + r;
+        const int gj = tj * ST + wn + j * 16 + c16;
+        if (gi < C && gj < C && gi <= gj) {
+          float* q = out + (int64_t)gi * lds + gj;
+          *q = P ? acc[i][j][r] : *q + acc[i][j][r];
+        }
+      }
+}
+
 // S[i][j] += sum_s P[s][i][j] in split order, upper triangle
 __global__ __launch_bounds__(256) void k_sum_splits(const float* __restrict__ P, int nsplit,
                                                     int C, float* S, int64_t lds) {
@@ -373,10 +573,74 @@ static int choose_splits(int64_t ntok, int64_t C, int cus) {
 }
 }  // namespace crbq
 
+namespace crbq {
+// SYRK launch timing (crbq_syrk_timing): while enabled, every SYRK kernel
+// launch of crbq_hessian_accum is bracketed by two HIP events recorded on
+// the launch's stream.
+struct SyrkRec {
+  hipEvent_t a, b;
+  int64_t C;
+};
+static std::mutex g_tmu;
+static bool g_timing = false;
+static std::vector<SyrkRec> g_recs;
+
+struct SyrkTimer {
+  SyrkRec r{nullptr, nullptr, 0};
+  bool on = false;
+  SyrkTimer(hipStream_t s, int64_t C) {
+    {
+      std::lock_guard<std::mutex> g(g_tmu);
+      on = g_timing;
+    }
+    if (!on) return;
+    r.C = C;
+    if (hipEventCreate(&r.a) != hipSuccess || hipEventCreate(&r.b) != hipSuccess ||
+        hipEventRecord(r.a, s) != hipSuccess)
+      on = false;
+  }
+  void stop(hipStream_t s) {
+    if (!on || hipEventRecord(r.b, s) != hipSuccess) return;
+    std::lock_guard<std::mutex> g(g_tmu);
+    g_recs.push_back(r);
+    on = false;
+  }
+};
+
+// Geometry of the channel-major path: a call of ntok tokens runs in passes
+// of at most tch tokens, each transposed into Xt[Cp][ldt].  A pass's Xt is
+// at most 8 GiB, and ldt <= 2^21 keeps a tile's 256-row panel of Xt below
+// the 2^31-byte reach of a buffer load's offsets.  The environment variable
+// CRBQ_XT_PASS_TOKENS lowers the pass length (tests use it to run several
+// passes on small inputs).
+struct XtPlan {
+  int64_t Cp, tch, ldt;
+  size_t xt_bytes;    // 256-byte aligned
+};
+static XtPlan xt_plan(int64_t ntok, int64_t C) {
+  XtPlan p;
+  p.Cp = (C + ST - 1) / ST * ST;
+  int64_t cap = ((int64_t)1 << 33) / (2 * p.Cp);
+  cap = cap < ((int64_t)1 << 21) ? cap : ((int64_t)1 << 21);
+  if (const char* e = getenv("CRBQ_XT_PASS_TOKENS")) {
+    const long long v = atoll(e);
+    if (v > 0 && v < cap) cap = v;
+  }
+  cap = cap / KQ * KQ;
+  if (cap < KQ) cap = KQ;
+  p.tch = ntok < cap ? ntok : cap;
+  p.ldt = (p.tch + KQ - 1) / KQ * KQ;
+  p.xt_bytes = ((size_t)p.Cp * (size_t)p.ldt * 2 + 255) & ~(size_t)255;
+  return p;
+}
+}  // namespace crbq
+
 extern "C" size_t crbq_hessian_workspace_size(int64_t ntok, int64_t C) {
   if (ntok <= 0 || C <= 0) return 0;
-  const int ns = crbq::choose_splits(ntok, C, crbq::num_cus());
-  return ns > 1 ? (size_t)ns * (size_t)C * (size_t)C * sizeof(float) : 0;
+  const crbq::XtPlan pl = crbq::xt_plan(ntok, C);
+  const int64_t tpad = (pl.tch + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
+  const int ns = crbq::choose_splits(tpad, C, crbq::num_cus());
+  return pl.xt_bytes + (ns > 1 ? (size_t)ns * (size_t)C * (size_t)C * sizeof(float) : 0);
 }
 
 extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_t ldx,
@@ -399,6 +663,51 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
   const int nt = (int)((C + crbq::ST - 1) / crbq::ST);
   const int64_t ntiles = (int64_t)nt * (nt + 1) / 2;
   if (ntiles > 0x7fffffff) return CRBQ_ERR_ARG;
+  const bool fast = (C % 8 == 0) && (ldx % 8 == 0) && ((((uintptr_t)X) & 15) == 0);
+  const crbq::XtPlan pl = crbq::xt_plan(ntok, C);
+  if (ws && ws_bytes >= pl.xt_bytes) {
+    // channel-major path: transpose each pass into the workspace, then SYRK
+    uint16_t* Xt = (uint16_t*)ws;
+    float* Pbuf = (float*)((char*)ws + pl.xt_bytes);
+    const size_t pcap = ws_bytes - pl.xt_bytes;
+    for (int64_t t0 = 0; t0 < ntok; t0 += pl.tch) {
+      const int64_t n = ntok - t0 < pl.tch ? ntok - t0 : pl.tch;
+      const int64_t tpad = (n + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
+      const uint16_t* Xc = (const uint16_t*)X + t0 * ldx;
+      const int64_t nw = (tpad / 64) * (pl.Cp / 64);
+      const unsigned nblk = (unsigned)((nw + 3) / 4 < 4096 ? (nw + 3) / 4 : 4096);
+      if (fast)
+        crbq::k_xpose16<true><<<nblk, 256, 0, s>>>(Xc, n, ldx, (int)C, Xt, pl.ldt, tpad,
+                                                   (int)pl.Cp);
+      else
+        crbq::k_xpose16<false><<<nblk, 256, 0, s>>>(Xc, n, ldx, (int)C, Xt, pl.ldt, tpad,
+                                                    (int)pl.Cp);
+      CRBQ_LAUNCH_CHECK();
+      int ns = crbq::choose_splits(tpad, C, crbq::num_cus());
+      while (ns > 1 && (size_t)ns * (size_t)C * (size_t)lds * sizeof(float) > pcap) --ns;
+      int64_t span = (tpad + ns - 1) / ns;
+      span = (span + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
+      ns = (int)((tpad + span - 1) / span);
+      float* P = ns > 1 ? Pbuf : nullptr;
+      dim3 grid((unsigned)ntiles, (unsigned)ns);
+      crbq::SyrkTimer tm(s, C);
+      if (dtype == CRBQ_F16)
+        crbq::k_syrk16k<h8_t><<<grid, crbq::SYRKP_THREADS, 0, s>>>(Xt, pl.ldt, tpad, (int)C, S,
+                                                                   lds, nt, span, P);
+      else
+        crbq::k_syrk16k<b8_t><<<grid, crbq::SYRKP_THREADS, 0, s>>>(Xt, pl.ldt, tpad, (int)C, S,
+                                                                   lds, nt, span, P);
+      CRBQ_LAUNCH_CHECK();
+      tm.stop(s);
+      if (P) {
+        crbq::k_sum_splits<<<(unsigned)((C * C + 255) / 256), 256, 0, s>>>(P, ns, (int)C, S,
+                                                                           lds);
+        CRBQ_LAUNCH_CHECK();
+      }
+    }
+    return CRBQ_OK;
+  }
+  // token-major path (workspace too small for the transposed copy)
   int ns = crbq::choose_splits(ntok, C, crbq::num_cus());
   // the partial buffers are laid out like S (row stride lds)
   while (ns > 1 && (!ws || (size_t)ns * (size_t)C * (size_t)lds * sizeof(float) > ws_bytes)) --ns;
@@ -407,7 +716,7 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
   ns = (int)((ntok + span - 1) / span);
   float* P = ns > 1 ? (float*)ws : nullptr;
   dim3 grid((unsigned)ntiles, (unsigned)ns);
-  const bool fast = (C % 8 == 0) && (ldx % 8 == 0) && ((((uintptr_t)X) & 15) == 0);
+  crbq::SyrkTimer tm(s, C);
 #define CRBQ_SYRK_GO(T8_, F_)                                                            \
   crbq::k_syrk16p<T8_, F_><<<grid, crbq::SYRKP_THREADS, 0, s>>>(                         \
       (const uint16_t*)X, ntok, ldx, (int)C, S, lds, nt, span, P)
@@ -418,11 +727,42 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
   }
 #undef CRBQ_SYRK_GO
   CRBQ_LAUNCH_CHECK();
+  tm.stop(s);
   if (P) {
     crbq::k_sum_splits<<<(unsigned)((C * C + 255) / 256), 256, 0, s>>>(P, ns, (int)C, S, lds);
     CRBQ_LAUNCH_CHECK();
   }
   return CRBQ_OK;
+}
+
+extern "C" int crbq_syrk_timing(int on) {
+  std::lock_guard<std::mutex> g(crbq::g_tmu);
+  crbq::g_timing = on != 0;
+  return CRBQ_OK;
+}
+
+extern "C" int crbq_syrk_timing_collect(float* ms, int64_t* C, int max, int* n) {
+  if (!n || max < 0 || (max > 0 && (!ms || !C))) return CRBQ_ERR_ARG;
+  std::vector<crbq::SyrkRec> recs;
+  {
+    std::lock_guard<std::mutex> g(crbq::g_tmu);
+    recs.swap(crbq::g_recs);
+  }
+  int k = 0, rc = CRBQ_OK;
+  for (const crbq::SyrkRec& r : recs) {
+    float t = 0.f;
+    if (hipEventSynchronize(r.b) != hipSuccess || hipEventElapsedTime(&t, r.a, r.b) != hipSuccess)
+      rc = CRBQ_ERR_HIP;
+    if (k < max) {
+      ms[k] = t;
+      C[k] = r.C;
+    }
+    ++k;
+    hipEventDestroy(r.a);
+    hipEventDestroy(r.b);
+  }
+  *n = k;
+  return rc;
 }
 
 extern "C" int crbq_hessian_finalize(const float* S, int64_t lds, int64_t C, float scale,

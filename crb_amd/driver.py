@@ -8,7 +8,7 @@ same activation (q/k/v in OPT and Llama, gate/up in Llama) get identical
 Hessians and therefore identical inverse factors U.  This driver
   * accumulates each distinct input's Hessian once,
   * starts each distinct input's inverse factor on a stream of its own as
-    soon as that input's last add_batch has been enqueued,
+    soon as that input's Hessian is complete,
   * enqueues every sublayer's block loop right behind its factor (an event
     wait, no host synchronisation), the widest input's chain first and on
     a stream of its own since it is the longest,
@@ -59,6 +59,7 @@ class LayerQuantizer:
         self.S = {}
         self.nsamples = {}
         self.ready = {}
+        self.syrk_ev = {}          # group -> (start, end) events around its Hessian updates
         for s in self.sublayers:
             if s.group not in self.S:
                 C = s.weight.shape[1]
@@ -72,12 +73,29 @@ class LayerQuantizer:
         if inp.dim() == 2:
             inp = inp.unsqueeze(0)
         nseq = inp.shape[0]
-        kernels.hessian_accum(inp.reshape(-1, inp.shape[-1]), self.S[group])
         self.nsamples[group] += nseq
+        cur = torch.cuda.current_stream(self.dev)
+        self._accum(group, inp, cur)
         ev = self.ready.get(group)
         if ev is None:
             ev = self.ready[group] = torch.cuda.Event()
-        ev.record(torch.cuda.current_stream(self.dev))
+        ev.record(cur)
+
+    def _accum(self, group, inp, stream):
+        """Hessian update of `group` on `stream`, bracketed by timing events."""
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        kernels.hessian_accum(inp.reshape(-1, inp.shape[-1]), self.S[group])
+        b.record(stream)
+        first = self.syrk_ev.get(group)
+        self.syrk_ev[group] = (first[0] if first else a, b)
+
+    def syrk_ms(self, group: str) -> float:
+        """GPU time from the first to the last Hessian update of `group`
+        (after the work has completed)."""
+        a, b = self.syrk_ev[group]
+        return a.elapsed_time(b)
 
     def _assign_streams(self, groups):
         """The widest input gets stream 0 for its factor and its sublayers;

@@ -33,11 +33,29 @@ def hessian_accum(X: torch.Tensor, S: torch.Tensor) -> None:
         X = X.float()
     T, C = X.shape
     lib = _lib.ready(X.device)
-    nb = lib.crbq_hessian_workspace_size(T, C) if S.stride(0) == C else 0
+    nb = (lib.crbq_hessian_workspace_size(T, C)
+          if S.stride(0) == C and X.dtype != torch.float32 else 0)
     ws = _ws(nb, X.device) if nb else None
     check(lib.crbq_hessian_accum(X.data_ptr(), _lib.DTYPES[X.dtype], T, X.stride(0), C,
                                  S.data_ptr(), S.stride(0), ptr(ws), nb, stream_of(S)),
           "crbq_hessian_accum")
+
+
+def syrk_timing(on: bool) -> None:
+    """Switch the per-launch SYRK timing of hessian_accum on or off."""
+    check(_lib.load().crbq_syrk_timing(1 if on else 0), "crbq_syrk_timing")
+
+
+def syrk_timing_collect(max_records: int = 4096):
+    """[(C, ms)] of the SYRK launches recorded since the last collect
+    (waits for them to finish)."""
+    lib = _lib.load()
+    ms = (ctypes.c_float * max_records)()
+    cs = (ctypes.c_int64 * max_records)()
+    n = ctypes.c_int32(0)
+    check(lib.crbq_syrk_timing_collect(ms, cs, max_records, ctypes.byref(n)),
+          "crbq_syrk_timing_collect")
+    return [(int(cs[i]), float(ms[i])) for i in range(min(n.value, max_records))]
 
 
 def hessian_finalize(S: torch.Tensor, scale: float, H: torch.Tensor | None = None) -> torch.Tensor:

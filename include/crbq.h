@@ -98,13 +98,27 @@ int         crbq_set_percentiles(const float* q81);
  * accumulate in fp32 on MFMA; fp32 inputs use the fp32 MFMA.
  * The reference's running rescale H *= n/(n+b); H += (2/n) X^T X is applied
  * once, in crbq_hessian_finalize, which gives the same H up to rounding.
- * ws (optional, crbq_hessian_workspace_size bytes; may be NULL) holds
- * per-split partial sums when the token range is split across workgroups
- * to fill the GPU (small C); they are added to S in a fixed order. */
+ * ws (optional, crbq_hessian_workspace_size bytes; may be NULL) holds a
+ * channel-major copy of X (16-bit inputs: C rounded up to 256 rows of up to
+ * 2^21 tokens, at most 8 GiB per pass; longer inputs run in passes), from
+ * which the SYRK streams whole cache lines, followed by the per-split
+ * partial sums when the token range is split across workgroups to fill the
+ * GPU; the partials are added to S in a fixed order.  With a smaller ws
+ * (or NULL) the SYRK reads X in place, a slower path with the same result
+ * up to summation order.  fp32 inputs use no workspace.  The environment
+ * variable CRBQ_XT_PASS_TOKENS (read per call) lowers the pass length. */
 size_t crbq_hessian_workspace_size(int64_t ntok, int64_t C);
 int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_t ldx,
                        int64_t C, float* S, int64_t lds, void* ws, size_t ws_bytes,
                        void* stream);
+/* SYRK launch timing, a profiling aid with no counterpart in the reference.
+ * While on != 0, crbq_hessian_accum records a pair of HIP events on its
+ * stream right before and right after each SYRK kernel launch (process-wide
+ * switch).  crbq_syrk_timing_collect waits for the recorded launches,
+ * writes up to max (ms, C) pairs, oldest first, sets *n to the number
+ * recorded, and forgets them. */
+int crbq_syrk_timing(int on);
+int crbq_syrk_timing_collect(float* ms, int64_t* C, int max, int* n);
 /* H[i,j] = scale * S[min(i,j), max(i,j)] for all i, j (H may alias S). */
 int crbq_hessian_finalize(const float* S, int64_t lds, int64_t C, float scale,
                           float* H, int64_t ldh, void* stream);

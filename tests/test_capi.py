@@ -54,6 +54,19 @@ def test_status_strings_without_gpu():
     assert lib.crbq_sgemm(0, 0, 1, 1, 1, 1.0, None, 1, None, 1, 0.0, None, 1, None) == -1
 
 
+def test_syrk_timing_switch_without_gpu():
+    """The timing switch and an empty collect make no device call."""
+    from crb_amd import kernels
+    kernels.syrk_timing(True)
+    kernels.syrk_timing(False)
+    assert kernels.syrk_timing_collect() == []
+    from crb_amd import _lib
+    n = ctypes.c_int32(7)
+    assert _lib.load().crbq_syrk_timing_collect(None, None, 0, ctypes.byref(n)) == 0
+    assert n.value == 0
+    assert _lib.load().crbq_syrk_timing_collect(None, None, 4, ctypes.byref(n)) == -1
+
+
 PROBE = r"""
 #include <stdio.h>
 #include <stddef.h>

@@ -115,6 +115,84 @@ def test_hessian_accum_split_k(dtype, T, C):
     assert torch.equal(torch.triu(S2).cpu(), torch.triu(S).cpu())
 
 
+def _accum_raw(X, S, ws_bytes):
+    """crbq_hessian_accum with a workspace of exactly ws_bytes (0: NULL)."""
+    from crb_amd import _lib
+    lib = _lib.ready(X.device)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=X.device)
+    _lib.check(lib.crbq_hessian_accum(X.data_ptr(), _lib.DTYPES[X.dtype], X.shape[0],
+                                      X.stride(0), X.shape[1], S.data_ptr(), S.stride(0),
+                                      ws.data_ptr() if ws_bytes else None, ws_bytes,
+                                      _lib.stream_of(S)), "crbq_hessian_accum")
+
+
+def _hess_want(X, S0):
+    Xd = X.double()
+    return Xd.t() @ Xd + S0
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("T,C,ldx", [(300, 200, 200), (1000, 384, 392), (77, 8, 13),
+                                     (8192, 520, 520)])
+def test_hessian_token_major_path(dtype, T, C, ldx):
+    """The in-place SYRK taken when the workspace cannot hold the
+    channel-major copy: NULL workspace, and a workspace sized for the split
+    partials only."""
+    print(f"hessian token-major {dtype} T={T} C={C} ldx={ldx}", flush=True)
+    from crb_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(T + 3 * C)
+    Xf = (torch.randn(T, ldx, generator=g) * torch.exp(torch.randn(ldx, generator=g))).to(dtype)
+    X = Xf.to(DEV)[:, :C]
+    want = _hess_want(Xf[:, :C], 0.25)
+    iu = torch.triu_indices(C, C)
+    xt_bytes = -(-C // 256) * 256 * (-(-T // 64) * 64) * 2     # the channel-major copy
+    part = 4 * C * C * 4                       # room for 4 split partials
+    nbs = (0, part) if part < xt_bytes else (0,)
+    if T >= 8192:
+        assert len(nbs) == 2 and lib.crbq_hessian_workspace_size(T, C) > xt_bytes
+    for nb in nbs:
+        S = torch.full((C, C), 0.25, device=DEV)
+        _accum_raw(X, S, nb)
+        torch.cuda.synchronize()
+        got = S.cpu().double()
+        assert rel(got[iu[0], iu[1]], want[iu[0], iu[1]]) < 1e-5, nb
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("T,C,ldx,pass_tok", [(5000, 200, 200, 1024), (3000, 520, 528, 700),
+                                              (129, 64, 72, 64)])
+def test_hessian_channel_major_passes(dtype, T, C, ldx, pass_tok, monkeypatch):
+    """Inputs longer than one transposed pass run in several passes (the pass
+    length is lowered through CRBQ_XT_PASS_TOKENS); ragged last pass, C not a
+    multiple of the 256-channel tile, strided rows."""
+    print(f"hessian passes {dtype} T={T} C={C} pass={pass_tok}", flush=True)
+    from crb_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(T + 5 * C)
+    Xf = (torch.randn(T, ldx, generator=g) * torch.exp(torch.randn(ldx, generator=g))).to(dtype)
+    X = Xf.to(DEV)[:, :C]
+    want = _hess_want(Xf[:, :C], 1.0)
+    iu = torch.triu_indices(C, C)
+    one = torch.ones(C, C, device=DEV)
+    S1 = one.clone()
+    _accum_raw(X, S1, lib.crbq_hessian_workspace_size(T, C))       # one pass
+    monkeypatch.setenv("CRBQ_XT_PASS_TOKENS", str(pass_tok))
+    nb = lib.crbq_hessian_workspace_size(T, C)
+    S = one.clone()
+    _accum_raw(X, S, nb)
+    # passes = calls on consecutive token slices of the pass length
+    S2 = one.clone()
+    step = max(64, pass_tok // 64 * 64)
+    for t0 in range(0, T, step):
+        _accum_raw(X[t0:t0 + step], S2, nb)
+    torch.cuda.synchronize()
+    for got in (S1, S):
+        got = got.cpu().double()
+        assert rel(got[iu[0], iu[1]], want[iu[0], iu[1]]) < 1e-5
+    assert torch.equal(torch.triu(S).cpu(), torch.triu(S2).cpu())
+
+
 def test_hessian_matches_reference_add_batch():
     """Incremental rescale of bigptq.py:50-53 vs. one 2/n scaling."""
     print("hessian add_batch", flush=True)
