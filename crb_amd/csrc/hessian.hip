@@ -19,7 +19,6 @@
 #include <stdlib.h>
 
 #include <mutex>
-#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -269,8 +268,8 @@ __global__ __launch_bounds__(SYRKP_THREADS) void k_syrk16p(const uint16_t* __res
 // Channel-major path.  X[t][c] is first transposed into a workspace
 // Xt[c][t] (k_xpose16), zero-padded to Cp = 256-multiple channels and tpad =
 // 64-multiple tokens; k_syrk16k then reads operand rows that are already
-// token-contiguous, so a loading thread moves 16 bytes from global memory to
-// LDS without a register transpose and every stage touches whole 128-byte
+// token-contiguous, so every 16-byte chunk goes from L2 straight into LDS
+// (a direct-to-LDS buffer load) and every stage touches whole 128-byte
 // lines.  For the same split boundaries both paths issue the same MFMAs on
 // the same 32-token slices in the same order, so their sums are bitwise
 // equal.
@@ -323,29 +322,63 @@ __global__ __launch_bounds__(256) void k_xpose16(const uint16_t* __restrict__ X,
   }
 }
 
-constexpr int KQ = 64;                  // tokens per stage (one 128-byte line per row)
-constexpr int KQP = KQ + 8;             // LDS row pitch (halves): 16 rows hit distinct banks
-constexpr int KUPS = ST * KQ / 8 / 256; // 16-byte units per producer thread per side
-typedef unsigned u4_t __attribute__((ext_vector_type(4)));
+constexpr int KQ = 64;                  // tokens per stage: one 128-byte line per row
+constexpr int SYRKD_THREADS = 512;
+typedef int i4_t __attribute__((ext_vector_type(4)));
 
-// Producer/consumer kernel on Xt (12 wavefronts per 256 x 256 tile):
-//  * 8 consumer wavefronts (2 x 4, 128 x 64 outputs each) read operand
-//    fragments from a 2-stage LDS ring and issue MFMAs, two 32-token
-//    slices per stage;
-//  * 4 producer wavefronts load each stage with raw buffer loads (one lane
-//    offset per side, per-row offsets in scalar registers; a tile's
-//    256-row panel spans less than 2^31 bytes) into one of two register
-//    sets and store it to LDS.  At iteration c they store stage c + 1 and
-//    issue the loads of stage c + 3; the loads are never predicated (past
-//    the last stage they repeat it) so the compiler's wait counts stay
-//    exact and one whole stage of loads is always in flight.
-// Requires Cp = nt * 256 rows in Xt, ldt, span and tpad multiples of KQ.
+// 16-byte chunk slot of chunk c in LDS row r (rows are 128 bytes, unpadded):
+// the MFMA reads of 8 consecutive rows at one chunk hit 8 distinct slots.
+__device__ __forceinline__ int xt_slot(int c, int r) { return c ^ (r & 7); }
+
+// Raw buffer descriptor (gfx950 layout): 48-bit base, stride 0, nrec bytes.
+__device__ __forceinline__ i4_t xt_rsrc(const uint16_t* base, int nrec) {
+  const uint64_t a = (uint64_t)base;
+  return i4_t{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+              __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffff)),
+              __builtin_amdgcn_readfirstlane(nrec), 0x00020000};
+}
+
+// One wavefront's share of a stage: 8-row groups g = 4w .. 4w+3 of both
+// operand panels (1 KB per group and side: one buffer_load_dwordx4 ... lds,
+// whose 64 lanes write 16 bytes each at M0 + 16 * lane).  Lane l fills slot
+// l & 7 of row l >> 3 of the group, so it reads the chunk that belongs
+// there.  Issued through inline assembly; the caller waits for it.
+__device__ __forceinline__ void xt_stage_loads(uint16_t* buf, int stage, int wave, i4_t rs0,
+                                               i4_t rs1, int voff, int gstep) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int g = wave * 4 + q;
+    const int soff = __builtin_amdgcn_readfirstlane(g * gstep + stage * KQ * 2);
+    const unsigned d0 = __builtin_amdgcn_readfirstlane(
+        (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)(buf + g * 8 * KQ));
+    const unsigned d1 = __builtin_amdgcn_readfirstlane(
+        (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)(buf + (ST + g * 8) * KQ));
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :: "v"(voff), "s"(rs0), "s"(soff), "{m0}"(d0) : "memory");
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :: "v"(voff), "s"(rs1), "s"(soff), "{m0}"(d1) : "memory");
+  }
+}
+
+// SYRK on Xt, 256 x 256 upper tiles, 8 wavefronts.  Each wavefront computes
+// a 128 x 64 block of outputs (v_mfma_f32_16x16x32, two 32-token slices per
+// stage) from a 2-stage LDS ring of 64-token stages, and also loads a
+// quarter of every stage with direct-to-LDS buffer loads (L2 straight into
+// LDS, no VGPR round trip, no loader wavefronts, so each wavefront may use
+// 256 registers).  At the top of iteration c the loads of stage c + 1 go
+// into the buffer every wavefront finished reading at the barrier that
+// ended iteration c - 1; each wavefront waits for its own loads
+// (vmcnt(0)) before the barrier that ends iteration c.  The compiler does
+// not see these loads, so it cannot hold the operand reads of the other
+// buffer behind them.
+// Requires Cp = nt * 256 rows in Xt, ldt, span and tpad multiples of KQ, and
+// 256 * ldt * 2 < 2^31 (a tile's panel is addressed with 32-bit offsets).
 template <typename T8>
-__global__ __launch_bounds__(SYRKP_THREADS) void k_syrk16k(const uint16_t* __restrict__ Xt,
+__global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __restrict__ Xt,
                                                            int64_t ldt, int64_t tpad, int C,
                                                            float* S, int64_t lds, int nt,
                                                            int64_t span, float* P) {
-  __shared__ __attribute__((aligned(16))) uint16_t Xs[2][2][ST][KQP];
+  __shared__ __attribute__((aligned(1024))) uint16_t Xs[2][2][ST][KQ];   // [buffer][side]
   int ti, tj;
   tile_band(xcd_chunk(blockIdx.x, gridDim.x), nt, ti, tj);
   const int64_t k_beg = (int64_t)blockIdx.y * span;
@@ -353,89 +386,44 @@ __global__ __launch_bounds__(SYRKP_THREADS) void k_syrk16k(const uint16_t* __res
   const int nch = k_end > k_beg ? (int)((k_end - k_beg) / KQ) : 0;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  if (wave >= 8) {
-    // ---------------- producers ----------------
-    const int p = tid - 512;
-    constexpr int LPR = KQ / 8;           // lanes per row
-    constexpr int RPI = 64 / LPR;         // rows per load instruction
-    const int rsub = (p & 63) / LPR, chunk = (p & 63) % LPR;
-    const int rbase = (p >> 6) * (ST / 4) + rsub;
-    const int nrec = (int)((int64_t)ST * ldt * 2);
-    const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(Xt + (int64_t)ti * ST * ldt + k_beg), 0, nrec, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(Xt + (int64_t)tj * ST * ldt + k_beg), 0, nrec, 0x00020000);
-    const int voff = (rbase * (int)ldt + chunk * 8) * 2;
-    const int rstep = RPI * (int)ldt * 2;
-    struct Set { u4_t v[2][KUPS]; };
-    auto load = [&](int stage, Set& r) {
-      const int k = stage * KQ * 2;
-#pragma unroll
-      for (int i = 0; i < KUPS; ++i) {
-        r.v[0][i] = __builtin_amdgcn_raw_buffer_load_b128(rs0, voff, k + i * rstep, 0);
-        r.v[1][i] = __builtin_amdgcn_raw_buffer_load_b128(rs1, voff, k + i * rstep, 0);
-      }
-    };
-    uint16_t* dst = &Xs[0][0][rbase][chunk * 8];
-    constexpr int SIDE = ST * KQP, BUF = 2 * ST * KQP;
-    auto store = [&](auto bsel, const Set& r) {
-      constexpr int b = decltype(bsel)::value;
-#pragma unroll
-      for (int i = 0; i < KUPS; ++i) {
-        *(u4_t*)(dst + b * BUF + i * RPI * KQP) = r.v[0][i];
-        *(u4_t*)(dst + b * BUF + SIDE + i * RPI * KQP) = r.v[1][i];
-      }
-    };
-    using B0 = std::integral_constant<int, 0>;
-    using B1 = std::integral_constant<int, 1>;
-    Set r0, r1;
-    if (nch > 0) {
-      const int last = nch - 1;
-      load(0, r0);
-      load(min(1, last), r1);
-      store(B0{}, r0);
-      load(min(2, last), r0);
-      sync_lds();
-      for (int c = 0;; c += 2) {
-        store(B1{}, r1);
-        load(min(c + 3, last), r1);
-        sync_lds();
-        if (c + 1 >= nch) break;
-        store(B0{}, r0);
-        load(min(c + 4, last), r0);
-        sync_lds();
-        if (c + 2 >= nch) break;
-      }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    } else {
-      sync_lds();
-    }
-    return;
-  }
-  // ---------------- consumers ----------------
   const int lane = tid & 63;
+  const int nrec = (int)((int64_t)ST * ldt * 2);
+  const i4_t rs0 = xt_rsrc(Xt + (int64_t)ti * ST * ldt + k_beg, nrec);
+  const i4_t rs1 = xt_rsrc(Xt + (int64_t)tj * ST * ldt + k_beg, nrec);
+  // lane -> (row l >> 3 of the group, slot l & 7) -> source chunk
+  const int lr = lane >> 3;
+  const int voff = (lr * (int)ldt + xt_slot(lane & 7, lr) * 8) * 2;
+  const int gstep = 8 * (int)ldt * 2;
   const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
   f4_t acc[8][4];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
-  const int r16 = lane & 15, kof = (lane >> 4) * 8;
+  const int r16 = lane & 15;
+  if (nch > 0) xt_stage_loads(&Xs[0][0][0][0], 0, wave, rs0, rs1, voff, gstep);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   sync_lds();
   for (int c = 0; c < nch; ++c) {
-    const int b = c & 1;
+    if (c + 1 < nch)
+      xt_stage_loads(&Xs[(c + 1) & 1][0][0][0], c + 1, wave, rs0, rs1, voff, gstep);
+    const uint16_t (*XA)[KQ] = Xs[c & 1][0];
+    const uint16_t (*XB)[KQ] = Xs[c & 1][1];
 #pragma unroll
     for (int h = 0; h < KQ / 32; ++h) {
+      // rows wm + 16i + r16 and wn + 16j + r16 share r16's low 3 bits
+      const int slot = xt_slot((lane >> 4) + 4 * h, r16) * 8;
       T8 bb[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bb[j] = *(const T8*)&Xs[b][1][wn + j * 16 + r16][kof + 32 * h];
+      for (int j = 0; j < 4; ++j) bb[j] = *(const T8*)&XB[wn + j * 16 + r16][slot];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const T8 a = *(const T8*)&Xs[b][0][wm + i * 16 + r16][kof + 32 * h];
+        const T8 a = *(const T8*)&XA[wm + i * 16 + r16][slot];
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T8>(a, bb[j], acc[i][j]);
       }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     sync_lds();
   }
   const int c16 = lane & 15, r4 = (lane >> 4) * 4;
@@ -692,10 +680,10 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
       dim3 grid((unsigned)ntiles, (unsigned)ns);
       crbq::SyrkTimer tm(s, C);
       if (dtype == CRBQ_F16)
-        crbq::k_syrk16k<h8_t><<<grid, crbq::SYRKP_THREADS, 0, s>>>(Xt, pl.ldt, tpad, (int)C, S,
+        crbq::k_syrk16k<h8_t><<<grid, crbq::SYRKD_THREADS, 0, s>>>(Xt, pl.ldt, tpad, (int)C, S,
                                                                    lds, nt, span, P);
       else
-        crbq::k_syrk16k<b8_t><<<grid, crbq::SYRKP_THREADS, 0, s>>>(Xt, pl.ldt, tpad, (int)C, S,
+        crbq::k_syrk16k<b8_t><<<grid, crbq::SYRKD_THREADS, 0, s>>>(Xt, pl.ldt, tpad, (int)C, S,
                                                                    lds, nt, span, P);
       CRBQ_LAUNCH_CHECK();
       tm.stop(s);
