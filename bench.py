@@ -100,6 +100,40 @@ def load_traffic(name):
     return vals.get("t")
 
 
+def stack_run(dev, nlayers, ntok, chunk=8, seed=0):
+    """The model-level driver (crb_amd/stack.py) on an OPT-6.7B-shaped decoder
+    stack of nlayers random-init layers, calibration 128 x 2048 uniform token
+    ids: per layer the hooked capture forward, the quantization and the
+    forward with the quantized weights.  Layer 0 (first use of the forward
+    kernels) is not averaged."""
+    from transformers import OPTConfig, OPTForCausalLM
+    from crb_amd.stack import StackQuantizer
+    torch.manual_seed(seed)
+    cfg = OPTConfig(hidden_size=4096, ffn_dim=16384, num_attention_heads=32,
+                    num_hidden_layers=nlayers, max_position_embeddings=2048, vocab_size=50272,
+                    word_embed_proj_dim=4096, torch_dtype=torch.float16)
+    with torch.device(dev):
+        model = OPTForCausalLM(cfg).half().eval()
+    seq = 2048
+    g = torch.Generator().manual_seed(seed + 1)
+    samples = torch.randint(0, cfg.vocab_size, (ntok // seq, seq), generator=g).to(dev)
+    sq = StackQuantizer(model, chunk=chunk)
+    t0 = time.time()
+    stats = sq.run(samples)
+    torch.cuda.synchronize()
+    wall = time.time() - t0
+    used = stats[1:] if len(stats) > 1 else stats
+    mean = lambda f: sum(f(s) for s in used) / len(used)
+    cap, hs = mean(lambda s: s.capture_ms), mean(lambda s: s.hessian_ms)
+    qz, fw = mean(lambda s: s.quantize_ms), mean(lambda s: s.forward_ms)
+    return {"layers": nlayers, "layers_averaged": len(used), "chunk": chunk,
+            "s_per_layer_with_capture": round((cap + hs + qz + fw) / 1e3, 4),
+            "s_per_layer_quantize": round((hs + qz) / 1e3, 4),
+            "capture_forward_ms": round(cap, 2), "hessian_ms": round(hs, 2),
+            "factors_blocks_ms": round(qz, 2), "quantized_forward_ms": round(fw, 2),
+            "wall_s_all_layers": round(wall, 2)}
+
+
 def cpu_baseline(nseq=32, nblocks=48):
     """Time the test-only CPU oracle (torch-CPU restatement of the reference
     path) on a bounded sample of the workload (about 10-20 s on 16 cores)
@@ -166,6 +200,8 @@ def main():
     ap.add_argument("--method", default="crb")
     ap.add_argument("--tokens", type=int, default=128 * 2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--stack-layers", type=int, default=3,
+                    help="layers of the OPT-6.7B-shaped stack run (0: skip)")
     ap.add_argument("--fc2-last", action="store_true",
                     help="accumulate the fc2 input's Hessian last (forward order)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -246,6 +282,12 @@ def main():
                      "algorithmic_flop": flops,
                      "traffic": load_traffic("syrk_fc2_opt67b_traffic.md")},
     }
+    if args.stack_layers > 0:
+        del X
+        torch.cuda.empty_cache()
+        print(f"[bench] stack run, {args.stack_layers} layers", file=sys.stderr, flush=True)
+        out["with_capture"] = stack_run(dev, args.stack_layers, args.tokens)
+        print(f"[bench] stack: {out['with_capture']}", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline()
