@@ -134,6 +134,54 @@ def stack_run(dev, nlayers, ntok, chunk=8, seed=0):
             "wall_s_all_layers": round(wall, 2)}
 
 
+def packed_gemv(dev, R=4096, C=16384, reps=20):
+    """Packed 3-bit GEMV (crbq_gemv_packed) on the fc2 shape against torch's
+    dense fp16 GEMV of the same weights, per launch, from captured HIP graphs
+    of `reps` launches (host call overhead excluded).  Random packed data:
+    the kernel's work does not depend on the values."""
+    from crb_amd import kernels
+    torch.manual_seed(0)
+    nblk = C // 128
+    codes = torch.randint(0, 256, (R, nblk * 32), dtype=torch.uint8, device=dev)
+    lut = torch.sort(torch.randn(R, nblk, 8, device=dev) * 0.02, dim=-1)[0].half()
+    sal = torch.randint(0, 256, (nblk, 16), dtype=torch.uint8, device=dev)
+    W = kernels.unpack(codes, lut, sal, C)
+    nbytes = codes.numel() + lut.numel() * 2 + sal.numel()
+
+    def graph_us(fn):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(5):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / (5 * reps)
+
+    out = {"shape": [R, C], "dtype": "f16", "packed_bytes": nbytes,
+           "bits_per_weight": round(nbytes * 8 / (R * C), 3), "per_nvec": {}}
+    for nvec in (1, 8, 16):
+        x = torch.randn(nvec, C, device=dev).half()
+        tp = graph_us(lambda: kernels.gemv_packed(codes, lut, sal, C, x))
+        td = graph_us(lambda: torch.nn.functional.linear(x, W))
+        out["per_nvec"][nvec] = {"packed_us": round(tp, 2), "dense_fp16_us": round(td, 2),
+                                 "packed_weight_GB_s": round(nbytes / tp / 1e3, 1),
+                                 "dense_weight_GB_s": round(R * C * 2 / td / 1e3, 1)}
+    return out
+
+
 def cpu_baseline(nseq=32, nblocks=48):
     """Time the test-only CPU oracle (torch-CPU restatement of the reference
     path) on a bounded sample of the workload (about 10-20 s on 16 cores)
@@ -200,6 +248,7 @@ def main():
     ap.add_argument("--method", default="crb")
     ap.add_argument("--tokens", type=int, default=128 * 2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-packed", action="store_true", help="skip the packed GEMV timing")
     ap.add_argument("--stack-layers", type=int, default=3,
                     help="layers of the OPT-6.7B-shaped stack run (0: skip)")
     ap.add_argument("--fc2-last", action="store_true",
@@ -288,6 +337,9 @@ def main():
         print(f"[bench] stack run, {args.stack_layers} layers", file=sys.stderr, flush=True)
         out["with_capture"] = stack_run(dev, args.stack_layers, args.tokens)
         print(f"[bench] stack: {out['with_capture']}", file=sys.stderr, flush=True)
+    if not args.no_packed:
+        out["packed_gemv"] = packed_gemv(dev)
+        print(f"[bench] packed gemv: {out['packed_gemv']}", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline()

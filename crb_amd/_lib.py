@@ -83,6 +83,11 @@ _SIGS = {
                               ctypes.c_float, ctypes.c_float, c_i32, c_vp, c_i64, c_vp]),
     "crbq_sgemm": (c_i32, [c_i32, c_i32, c_i64, c_i64, c_i64, ctypes.c_float, c_vp, c_i64,
                            c_vp, c_i64, ctypes.c_float, c_vp, c_i64, c_vp]),
+    "crbq_pack": (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,
+                          c_vp, c_vp, c_vp]),
+    "crbq_unpack": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_vp]),
+    "crbq_gemv_packed": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64,
+                                 c_i32, c_vp, c_i64, c_vp]),
 }
 
 _lock = threading.Lock()

@@ -20,7 +20,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_obj")
 LIB = os.path.join(HERE, "libcrbq.so")
-SOURCES = ["capi.hip", "gemm_f32.hip", "hessian.hip", "chol.hip", "block.hip"]
+SOURCES = ["capi.hip", "gemm_f32.hip", "hessian.hip", "chol.hip", "block.hip", "packed.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

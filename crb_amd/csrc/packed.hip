@@ -1,0 +1,330 @@
+// Packed low-bit storage of CRB/BRAQ-quantized weights and its GEMV.
+//
+// The reference stores the quantized layer as fake-quantized fp16/bf16
+// weights (bigptq.py:278-280).  Within one 128-column block of one row,
+// those weights take at most 2 distinct values in each non-salient group
+// (mask1, mask2: order-1 binarization, mu +- alpha) and at most 4 on the
+// salient columns (mask3: order 2, mu + a1 s1 + a2 s2); the salient columns
+// of a block are whole columns, the same for every row
+// (utils/structure.py:8-20).  So the layer is stored exactly as
+//   codes [R][nblk * 32] bytes : 2 bits per weight, element j of a block at
+//                                byte j / 4, bits 2 (j % 4) .. +1;
+//   lut   [R][nblk][8]         : the block row's values in the weight
+//                                dtype: mask1 {lo, hi}, mask2 {lo, hi},
+//                                mask3 4 values, each ascending;
+//   sal   [nblk][16] bytes     : salient-column bitmap of each block;
+// with weight = lut[r][b][4 * sal + code], code = (mask2 ? 2 : 0) + rank
+// for non-salient weights and rank (0..3) for salient ones: 3 bits per
+// weight instead of 16, and unpacking reproduces the weights bit for bit.
+#include "common.h"
+
+namespace crbq {
+
+constexpr int PB = 128;   // packing block (columns)
+
+// Order-preserving 16-bit keys: -0 sorts just below +0, so the two zeros
+// are distinct values and round-trip exactly.
+__device__ __forceinline__ int key16(uint32_t u) {
+  return (u & 0x8000u) ? (int)(~u & 0xffffu) : (int)(u | 0x8000u);
+}
+__device__ __forceinline__ uint16_t unkey16(int k) {
+  return (k & 0x8000) ? (uint16_t)(k & 0x7fff) : (uint16_t)(~k & 0xffff);
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, CRBQ_WAVE));
+  return v;
+}
+__device__ __forceinline__ int wave_or_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, CRBQ_WAVE);
+  return v;
+}
+
+__global__ void k_zero_status(int* status) { *status = 0; }
+
+// One wavefront per (row, block); lane l holds elements l and 64 + l.
+__global__ __launch_bounds__(256) void k_pack(const uint16_t* __restrict__ Q, int64_t ldq,
+                                              const uint8_t* __restrict__ M, int64_t ldm,
+                                              int R, int C, int nblk,
+                                              uint8_t* __restrict__ codes, int64_t ldc,
+                                              uint16_t* __restrict__ lut,
+                                              uint8_t* __restrict__ sal, int* status) {
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= (int64_t)R * nblk) return;   // whole wavefronts
+  const int r = (int)(w / nblk), b = (int)(w % nblk), lane = threadIdx.x & 63;
+  int key[2], grp[2];
+  bool sal0[2], inside[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int c = b * PB + s * 64 + lane;
+    inside[s] = c < C;
+    key[s] = inside[s] ? key16(Q[(int64_t)r * ldq + c]) : 0;
+    grp[s] = inside[s] ? M[(int64_t)r * ldm + c] : 0;
+    sal0[s] = inside[s] && M[c] == 3;          // row 0 defines the salient columns
+  }
+  int err = 0;
+  const uint64_t my0 = __ballot(grp[0] == 3), my1 = __ballot(grp[1] == 3);
+  if (my0 != __ballot(sal0[0]) || my1 != __ballot(sal0[1])) err |= 2;
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+    if (inside[s] && (grp[s] < 1 || grp[s] > 3)) err |= 4;
+  int code[2] = {0, 0};
+  uint32_t lv[8];
+#pragma unroll
+  for (int G = 1; G <= 3; ++G) {
+    const int cap = G == 3 ? 4 : 2, base = G == 1 ? 0 : (G == 2 ? 2 : 4);
+    int keys[4], found = 0, prev = -1;
+#pragma unroll
+    for (int k = 0; k < cap; ++k) {
+      int cand = 0x10000;
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        if (grp[s] == G && key[s] > prev) cand = min(cand, key[s]);
+      cand = wave_min_i(cand);
+      keys[k] = cand;
+      if (cand < 0x10000) {
+        found = k + 1;
+        prev = cand;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      if (grp[s] != G) continue;
+      int rk = -1;
+#pragma unroll
+      for (int k = 0; k < cap; ++k)
+        if (k < found && keys[k] == key[s]) rk = k;
+      if (rk < 0) err |= 1;                      // more distinct values than codes
+      else code[s] = (G == 2 ? 2 : 0) + rk;
+    }
+#pragma unroll
+    for (int k = 0; k < cap; ++k)
+      lv[base + k] = found ? unkey16(keys[k < found ? k : found - 1]) : 0u;
+  }
+  err = wave_or_i(err);
+  if (lane == 0 && err) atomicOr(status, err);
+  // byte t (lanes 0..31) packs elements 4t .. 4t+3, all in slot t / 16
+  uint32_t byte = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int src = (4 * lane + i) & 63;
+    const int c0 = __shfl(code[0], src, CRBQ_WAVE), c1 = __shfl(code[1], src, CRBQ_WAVE);
+    byte |= (uint32_t)((lane < 16 ? c0 : c1) & 3) << (2 * i);
+  }
+  if (lane < 32) codes[(int64_t)r * ldc + b * 32 + lane] = (uint8_t)byte;
+  if (lane < 4) {
+    uint32_t v = lv[0] | (lv[1] << 16);
+    if (lane == 1) v = lv[2] | (lv[3] << 16);
+    if (lane == 2) v = lv[4] | (lv[5] << 16);
+    if (lane == 3) v = lv[6] | (lv[7] << 16);
+    ((uint32_t*)(lut + ((int64_t)r * nblk + b) * 8))[lane] = v;
+  }
+  if (r == 0 && lane == 0) {
+    uint64_t* sp = (uint64_t*)(sal + (int64_t)b * 16);
+    sp[0] = my0;
+    sp[1] = my1;
+  }
+}
+
+// One thread per code byte (4 weights).
+__global__ __launch_bounds__(256) void k_unpack(const uint8_t* __restrict__ codes, int64_t ldc,
+                                                const uint16_t* __restrict__ lut,
+                                                const uint8_t* __restrict__ sal, int R, int C,
+                                                int nblk, uint16_t* __restrict__ Q, int64_t ldq) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (int64_t)R * nblk * 32) return;
+  const int t = (int)(id & 31);
+  const int64_t rb = id >> 5;
+  const int r = (int)(rb / nblk), b = (int)(rb % nblk);
+  const uint32_t cb = codes[(int64_t)r * ldc + b * 32 + t];
+  const uint32_t sb = (uint32_t)(sal[(int64_t)b * 16 + (t >> 1)] >> (4 * (t & 1))) & 0xfu;
+  const uint16_t* L = lut + ((int64_t)r * nblk + b) * 8;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = b * PB + 4 * t + i;
+    if (c < C) Q[(int64_t)r * ldq + c] = L[4 * ((sb >> i) & 1) + ((cb >> (2 * i)) & 3)];
+  }
+}
+
+constexpr int GV_MAXVEC = 16;
+
+// Two weights (elements 2p, 2p+1 of a lane's 8) from the block's table L:
+// v_perm_b32 picks the 16-bit entries of codes (c_a, c_b) among the four
+// non-salient entries and among the four salient ones; selb (from the two
+// salient bits) takes each half from the salient or the non-salient pick.
+__device__ __forceinline__ uint32_t decode_pair(uint32_t cw, int p, uint4 L, uint32_t sb) {
+  const uint32_t n = (cw >> (4 * p)) & 0xfu;
+  const uint32_t t = (n & 3u) | ((n & 0xcu) << 14);
+  const uint32_t sel = t * 0x202u + 0x01000100u;
+  const uint32_t wn = __builtin_amdgcn_perm(L.y, L.x, sel);
+  const uint32_t ws = __builtin_amdgcn_perm(L.w, L.z, sel);
+  const uint32_t s2 = (sb >> (2 * p)) & 3u;
+  const uint32_t selb = 0x03020100u + (s2 & 1u) * 0x0404u + (s2 >> 1) * 0x04040000u;
+  return __builtin_amdgcn_perm(ws, wn, selb);
+}
+
+template <typename T8>
+__device__ __forceinline__ f4_t mfma_gv(T8 a, T8 b, f4_t c);
+template <>
+__device__ __forceinline__ f4_t mfma_gv<h8_t>(h8_t a, h8_t b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f4_t mfma_gv<b8_t>(b8_t a, b8_t b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// y[v][r] = sum_c W[r][c] x[v][c] for up to 16 vectors, W packed, x in the
+// weights' 16-bit dtype, fp32 sums, on v_mfma_f32_16x16x32.  A workgroup
+// takes 16 rows; its 16 wavefronts split the row's 128-column blocks into
+// contiguous ranges.  Per block, lane l takes the 32 contiguous columns
+// 32 (l >> 4) .. +31 of row l & 15 (8 bytes of codes, 4 of salient bits,
+// the row-block's table) and the same columns of vector l & 15 (64 bytes),
+// and feeds them to four MFMAs as 8-column slices: the MFMA sums over k in
+// any order as long as A and B agree, so the columns need not be in the
+// instruction's natural k order.  Decoding is the only per-weight vector
+// work whatever nvec.  The wavefronts' 16 x 16 partial products are
+// summed in LDS.
+constexpr int GV_WAVES = 16;
+
+template <typename T8>
+__device__ __forceinline__ void gv_block(const uint8_t* crow, const uint4* lrow,
+                                         const uint8_t* sal, const uint16_t* xv, int b, int kq,
+                                         int C, bool row_ok, bool vec_ok, f4_t& acc) {
+  const int c = b * PB + kq * 32;                // this lane's 32 columns
+  const uint2 cw = row_ok ? *(const uint2*)(crow + b * 32 + kq * 8) : make_uint2(0u, 0u);
+  const uint32_t sb = *(const uint32_t*)(sal + (int64_t)b * 16 + kq * 4);
+  const uint4 L = row_ok ? lrow[b] : make_uint4(0u, 0u, 0u, 0u);
+  uint4 xs[4];
+  if (c + 32 <= C) {                             // all blocks but a ragged last one
+    const uint4* xp = (const uint4*)(xv + c);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xs[k] = vec_ok ? xp[k] : make_uint4(0u, 0u, 0u, 0u);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int cc = c + 8 * k + e;
+        h[e] = vec_ok && cc < C ? xv[cc] : 0u;
+      }
+      xs[k] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                         h[6] | (h[7] << 16));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t cws = (k < 2 ? cw.x : cw.y) >> (16 * (k & 1));
+    const uint32_t sbs = sb >> (8 * k);
+    uint4 a;
+    a.x = decode_pair(cws, 0, L, sbs);
+    a.y = decode_pair(cws, 1, L, sbs);
+    a.z = decode_pair(cws, 2, L, sbs);
+    a.w = decode_pair(cws, 3, L, sbs);
+    acc = mfma_gv<T8>(__builtin_bit_cast(T8, a), __builtin_bit_cast(T8, xs[k]), acc);
+  }
+}
+
+template <typename T8>
+__global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_packed(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ lut,
+    const uint8_t* __restrict__ sal, int R, int C, int nblk, const uint16_t* __restrict__ x,
+    int64_t ldx, int nvec, float* __restrict__ y, int64_t ldy) {
+  __shared__ float red[GV_WAVES][16][17];
+  const int r0 = blockIdx.x * 16;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = r0 + (lane & 15), kq = lane >> 4, vec = lane & 15;
+  const bool row_ok = row < R, vec_ok = vec < nvec;
+  const int b_beg = (int)((int64_t)nblk * wave / GV_WAVES);
+  const int b_end = (int)((int64_t)nblk * (wave + 1) / GV_WAVES);
+  const uint8_t* crow = codes + (int64_t)(row_ok ? row : 0) * ldc;
+  const uint4* lrow = (const uint4*)(lut + (int64_t)(row_ok ? row : 0) * nblk * 8);
+  const uint16_t* xv = x + (int64_t)(vec_ok ? vec : 0) * ldx;
+  f4_t acc = {0.f, 0.f, 0.f, 0.f};
+  int b = b_beg;
+  for (; b + 1 < b_end; b += 2) {
+    gv_block<T8>(crow, lrow, sal, xv, b, kq, C, row_ok, vec_ok, acc);
+    gv_block<T8>(crow, lrow, sal, xv, b + 1, kq, C, row_ok, vec_ok, acc);
+  }
+  if (b < b_end) gv_block<T8>(crow, lrow, sal, xv, b, kq, C, row_ok, vec_ok, acc);
+  // acc[i] = partial y[vector lane & 15][row r0 + 4 (lane >> 4) + i]
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[wave][4 * (lane >> 4) + i][lane & 15] = acc[i];
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < 256) {
+    const int rr = t >> 4, v = t & 15;
+    if (v < nvec && r0 + rr < R) {
+      float s0 = 0.f;
+#pragma unroll
+      for (int w = 0; w < GV_WAVES; ++w) s0 += red[w][rr][v];
+      y[(int64_t)v * ldy + r0 + rr] = s0;
+    }
+  }
+}
+
+}  // namespace crbq
+
+extern "C" int crbq_pack(const void* Q, int dtype, int64_t R, int64_t C, int64_t ldq,
+                         const uint8_t* masks, int64_t ldm, uint8_t* codes, int64_t ldc,
+                         void* lut, uint8_t* sal, int* status, void* stream) {
+  if (!Q || !masks || !codes || !lut || !sal || !status) return CRBQ_ERR_ARG;
+  if (dtype != CRBQ_F16 && dtype != CRBQ_BF16) return CRBQ_ERR_ARG;
+  if (R <= 0 || C <= 0 || R > 0x7fffffff || C > 0x7fffffff || ldq < C || ldm < C)
+    return CRBQ_ERR_ARG;
+  const int64_t nblk = (C + crbq::PB - 1) / crbq::PB;
+  if (ldc < nblk * 32 || (ldc & 7) || (((uintptr_t)lut) & 15) || (((uintptr_t)sal) & 7) ||
+      (((uintptr_t)codes) & 7))
+    return CRBQ_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+  crbq::k_zero_status<<<1, 1, 0, s>>>(status);
+  CRBQ_LAUNCH_CHECK();
+  const int64_t waves = R * nblk;
+  crbq::k_pack<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(
+      (const uint16_t*)Q, ldq, masks, ldm, (int)R, (int)C, (int)nblk, codes, ldc,
+      (uint16_t*)lut, sal, status);
+  CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}
+
+extern "C" int crbq_unpack(const uint8_t* codes, int64_t ldc, const void* lut, const uint8_t* sal,
+                           int dtype, int64_t R, int64_t C, void* Q, int64_t ldq, void* stream) {
+  if (!codes || !lut || !sal || !Q) return CRBQ_ERR_ARG;
+  if (dtype != CRBQ_F16 && dtype != CRBQ_BF16) return CRBQ_ERR_ARG;
+  if (R <= 0 || C <= 0 || R > 0x7fffffff || C > 0x7fffffff || ldq < C) return CRBQ_ERR_ARG;
+  const int64_t nblk = (C + crbq::PB - 1) / crbq::PB;
+  if (ldc < nblk * 32) return CRBQ_ERR_ARG;
+  const int64_t n = R * nblk * 32;
+  crbq::k_unpack<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+      codes, ldc, (const uint16_t*)lut, sal, (int)R, (int)C, (int)nblk, (uint16_t*)Q, ldq);
+  CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}
+
+extern "C" int crbq_gemv_packed(const uint8_t* codes, int64_t ldc, const void* lut,
+                                const uint8_t* sal, int dtype, int64_t R, int64_t C,
+                                const void* x, int64_t ldx, int nvec, float* y, int64_t ldy,
+                                void* stream) {
+  if (!codes || !lut || !sal || !x || !y) return CRBQ_ERR_ARG;
+  if (dtype != CRBQ_F16 && dtype != CRBQ_BF16) return CRBQ_ERR_ARG;
+  if (R <= 0 || C <= 0 || R > 0x7fffffff || C > 0x7fffffff) return CRBQ_ERR_ARG;
+  if (nvec < 1 || nvec > crbq::GV_MAXVEC || ldx < C || ldy < R) return CRBQ_ERR_ARG;
+  const int64_t nblk = (C + crbq::PB - 1) / crbq::PB;
+  if (ldc < nblk * 32 || (ldc & 7) || (ldx & 7) || (((uintptr_t)x) & 15) ||
+      (((uintptr_t)lut) & 15) || (((uintptr_t)codes) & 7) || (((uintptr_t)sal) & 3))
+    return CRBQ_ERR_ARG;
+  const unsigned grid = (unsigned)((R + 15) / 16);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == CRBQ_BF16)
+    crbq::k_gemv_packed<b8_t><<<grid, 64 * crbq::GV_WAVES, 0, s>>>(
+        codes, ldc, (const uint16_t*)lut, sal, (int)R, (int)C, (int)nblk, (const uint16_t*)x,
+        ldx, nvec, y, ldy);
+  else
+    crbq::k_gemv_packed<h8_t><<<grid, 64 * crbq::GV_WAVES, 0, s>>>(
+        codes, ldc, (const uint16_t*)lut, sal, (int)R, (int)C, (int)nblk, (const uint16_t*)x,
+        ldx, nvec, y, ldy);
+  CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}

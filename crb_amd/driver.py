@@ -48,7 +48,8 @@ class LayerQuantizer:
 
     def __init__(self, sublayers, method="crb", metric="hessian", blocksize=128,
                  percdamp=0.01, partition=3, orders=(1, 1, 2), refine_iters=1,
-                 lam=1e-5, corr_damp=0.1, disable_gptq=False, nstreams=NSTREAMS):
+                 lam=1e-5, corr_damp=0.1, disable_gptq=False, nstreams=NSTREAMS,
+                 keep_masks=False):
         self.sublayers = list(sublayers)
         self.p = _lib.params(method, metric=metric, blocksize=blocksize, partition=partition,
                              orders=orders, up_lim=50, refine_iters=refine_iters,
@@ -56,6 +57,8 @@ class LayerQuantizer:
         self.percdamp = percdamp
         self.dev = self.sublayers[0].weight.device
         self.nstreams = max(1, int(nstreams))
+        self.keep_masks = bool(keep_masks)
+        self.masks = {}            # keep_masks: name -> uint8 [R, C] mask codes 1/2/3
         self.S = {}
         self.nsamples = {}
         self.ready = {}
@@ -121,8 +124,8 @@ class LayerQuantizer:
         W = W.contiguous()
         W.masked_fill_(dead[None, :], 0.0)                               # bigptq.py:105
         losses = torch.zeros(W.shape[0], device=self.dev)
-        kernels.fasterquant_blocks(W, U, self.p, losses)
-        return W, losses
+        masks, _ = kernels.fasterquant_blocks(W, U, self.p, losses, want_masks=self.keep_masks)
+        return W, losses, masks
 
     def quantize(self, times: PhaseTimes | None = None) -> dict:
         """fasterquant for every sublayer; returns {name: error}."""
@@ -174,7 +177,9 @@ class LayerQuantizer:
             if s.group in redo:
                 work[s.name] = self._blocks(s, U[s.group], dead[s.group])
         for s in order:
-            W, losses = work[s.name]
+            W, losses, masks = work[s.name]
+            if masks is not None:
+                self.masks[s.name] = masks
             if s.weight.dtype != torch.float32:
                 s.weight.copy_(W.to(s.weight.dtype))
             else:

@@ -226,3 +226,77 @@ def sgemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, alpha: float = 1.0,
                          A.stride(0), B.data_ptr(), B.stride(0), float(beta), C.data_ptr(),
                          C.stride(0), stream_of(C)), "crbq_sgemm")
     return C
+
+
+# -- packed low-bit storage ---------------------------------------------------
+PACK_BLOCK = 128
+PACK_ERRORS = {1: "a group has more distinct values than its codes (blocksize not a "
+                  "multiple of 128, or weights not from the binarizer)",
+               2: "salient columns differ between rows",
+               4: "mask code outside 1..3"}
+
+
+def pack(Q: torch.Tensor, masks: torch.Tensor):
+    """Packed form (codes, lut, sal) of quantized fp16/bf16 weights Q [R, C]
+    with their mask codes (uint8 1/2/3).  Raises CrbqError if Q does not
+    have the per-block structure the format stores exactly."""
+    _dev_check(Q, masks)
+    if Q.dtype not in (torch.float16, torch.bfloat16) or Q.dim() != 2 or Q.stride(1) != 1:
+        raise _lib.CrbqError("pack takes a row-major fp16/bf16 [R, C] weight")
+    if masks.dtype != torch.uint8 or masks.shape != Q.shape or masks.stride(1) != 1:
+        raise _lib.CrbqError("pack takes uint8 mask codes shaped like the weight")
+    R, C = Q.shape
+    nblk = (C + PACK_BLOCK - 1) // PACK_BLOCK
+    codes = torch.empty((R, nblk * 32), dtype=torch.uint8, device=Q.device)
+    lut = torch.empty((R, nblk, 8), dtype=Q.dtype, device=Q.device)
+    sal = torch.empty((nblk, 16), dtype=torch.uint8, device=Q.device)
+    status = torch.empty(1, dtype=torch.int32, device=Q.device)
+    lib = _lib.ready(Q.device)
+    check(lib.crbq_pack(Q.data_ptr(), _lib.DTYPES[Q.dtype], R, C, Q.stride(0),
+                        masks.data_ptr(), masks.stride(0), codes.data_ptr(), codes.stride(0),
+                        lut.data_ptr(), sal.data_ptr(), status.data_ptr(), stream_of(Q)),
+          "crbq_pack")
+    st = int(status.item())
+    if st:
+        why = "; ".join(v for k, v in PACK_ERRORS.items() if st & k)
+        raise _lib.CrbqError(f"crbq_pack: {why}")
+    return codes, lut, sal
+
+
+def unpack(codes: torch.Tensor, lut: torch.Tensor, sal: torch.Tensor, C: int) -> torch.Tensor:
+    """The weights [R, C] (lut's dtype) a packed triple encodes."""
+    _dev_check(codes, lut, sal)
+    R = codes.shape[0]
+    Q = torch.empty((R, C), dtype=lut.dtype, device=codes.device)
+    lib = _lib.ready(codes.device)
+    check(lib.crbq_unpack(codes.data_ptr(), codes.stride(0), lut.data_ptr(), sal.data_ptr(),
+                          _lib.DTYPES[lut.dtype], R, C, Q.data_ptr(), Q.stride(0),
+                          stream_of(Q)), "crbq_unpack")
+    return Q
+
+
+def gemv_packed(codes: torch.Tensor, lut: torch.Tensor, sal: torch.Tensor, C: int,
+                x: torch.Tensor) -> torch.Tensor:
+    """y [nvec, R] (fp32) = x [nvec, C] @ W^T for the packed W, nvec <= 16."""
+    _dev_check(codes, lut, sal, x)
+    if x.dim() == 1:
+        x = x.unsqueeze(0)
+    if x.dtype != lut.dtype:
+        x = x.to(lut.dtype)
+    nvec = x.shape[0]
+    if not 1 <= nvec <= 16 or x.shape[1] != C:
+        raise _lib.CrbqError("gemv_packed takes 1..16 vectors of the weight's width")
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+        if C % 8:
+            xp = torch.zeros((nvec, (C + 7) // 8 * 8), dtype=x.dtype, device=x.device)
+            xp[:, :C] = x
+            x = xp
+    R = codes.shape[0]
+    y = torch.empty((nvec, R), dtype=torch.float32, device=x.device)
+    lib = _lib.ready(x.device)
+    check(lib.crbq_gemv_packed(codes.data_ptr(), codes.stride(0), lut.data_ptr(),
+                               sal.data_ptr(), _lib.DTYPES[lut.dtype], R, C, x.data_ptr(),
+                               x.stride(0), nvec, y.data_ptr(), y.stride(0), stream_of(y)),
+          "crbq_gemv_packed")
+    return y

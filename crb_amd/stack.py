@@ -26,6 +26,9 @@ Differences in mechanism, not in result:
     [tokens, C] store and its Hessian is accumulated by one call over all
     tokens at quantization time (the per-call SYRK launches of many small
     chunks cost more than the copy);
+  * with pack=True every quantized nn.Linear is replaced, after the layer's
+    quantized forward, by a PackedLinear holding the same weights in 3
+    bits each (crb_amd/packed.py);
   * the hooked pass only needs the sublayers' inputs, so after the first
     chunk it stops at the input of the last hooked sublayer to run (OPT's
     fc2, Llama's down_proj) instead of computing the layer output that
@@ -118,6 +121,7 @@ class LayerStats:
     hessian_ms: float = 0.0           # deferred Hessian accumulation
     quantize_ms: float = 0.0          # inverse factors + block loops
     forward_ms: float = 0.0           # forward with the quantized weights
+    packed_bytes: int = 0             # pack=True: bytes of the packed sublayers
     phase: PhaseTimes = field(default_factory=PhaseTimes)
 
 
@@ -126,7 +130,7 @@ class StackQuantizer:
 
     def __init__(self, model, method="crb", salient_metric="hessian", blocksize=128,
                  percdamp=0.01, chunk=8, defer_hessian=True, name_filter=None,
-                 layer_quantizer=LayerQuantizer, **quant_kw):
+                 pack=False, layer_quantizer=LayerQuantizer, **quant_kw):
         self.model = model
         self.layers = decoder_layers(model)
         self.method = method
@@ -137,7 +141,10 @@ class StackQuantizer:
         self.defer = bool(defer_hessian)
         self.name_filter = name_filter or (lambda i, name: True)
         self.layer_quantizer = layer_quantizer
-        self.quant_kw = quant_kw
+        self.quant_kw = dict(quant_kw)
+        self.pack = bool(pack)
+        if self.pack:
+            self.quant_kw["keep_masks"] = True
         self.kwargs = {}
         self.kw_batch = 0
 
@@ -301,6 +308,12 @@ class StackQuantizer:
             self._forward(layer, inps, outs)
         clock.mark()
         stats.capture_ms, stats.hessian_ms, stats.quantize_ms, stats.forward_ms = clock.spans()
+        if self.pack:
+            from .packed import PackedLinear, replace_linears
+            subset = find_linears(layer)
+            packed = {k: PackedLinear.from_linear(subset[k], lq.masks[k]) for k in lq.masks}
+            replace_linears(layer, packed)
+            stats.packed_bytes = sum(p.packed_bytes() for p in packed.values())
         return stats
 
     @torch.no_grad()

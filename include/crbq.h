@@ -187,6 +187,39 @@ int crbq_sgemm(int transa, int transb, int64_t M, int64_t N, int64_t K,
                float alpha, const float* A, int64_t lda, const float* B,
                int64_t ldb, float beta, float* C, int64_t ldc, void* stream);
 
+/* ---- packed low-bit storage and GEMV -------------------------------------
+ * No counterpart in the reference, which keeps fake-quantized fp16/bf16
+ * weights (bigptq.py:278-280); for inference callers that want the
+ * quantized layer in 3 bits per weight.  Within a 128-column block of a
+ * row the quantized weights take <= 2 values per non-salient group
+ * (mask 1, mask 2, order 1) and <= 4 on the salient columns (mask 3, order
+ * 2), and the salient columns are the same for every row.  With
+ * nblk = ceil(C / 128):
+ *   codes [R][ldc] bytes, ldc >= nblk * 32 (multiple of 8, 8-byte aligned): 2 bits per
+ *     weight, column j of block b at byte b * 32 + j / 4, bits 2 (j % 4);
+ *   lut [R][nblk][8] in the weight dtype (16-byte aligned): mask1 lo, hi,
+ *     mask2 lo, hi, mask3 4 values, ascending (-0 below +0);
+ *   sal [nblk][16] bytes (8-byte aligned): bit j % 8 of byte j / 8 marks salient column j;
+ *   weight = lut[r][b][4 * salient + code].
+ * crbq_pack reads the quantized weights Q (fp16/bf16) and the mask codes
+ * (1/2/3, as crbq_fasterquant writes them) and sets the device int *status
+ * to 0, or to an OR of 1 (a group with more distinct values than codes),
+ * 2 (salient columns differ between rows), 4 (mask code outside 1..3);
+ * the caller reads it after the stream.  Blocksizes that are multiples of
+ * 128 satisfy the structure.  crbq_unpack writes the weights back bit for
+ * bit.  crbq_gemv_packed: y[v][r] = sum_c W[r][c] x[v][c] for nvec <= 16
+ * vectors x in the weights' dtype (ldx multiple of 8, 16-byte aligned),
+ * fp32 y. */
+int crbq_pack(const void* Q, int dtype, int64_t R, int64_t C, int64_t ldq,
+              const uint8_t* masks, int64_t ldm, uint8_t* codes, int64_t ldc,
+              void* lut, uint8_t* sal, int* status, void* stream);
+int crbq_unpack(const uint8_t* codes, int64_t ldc, const void* lut, const uint8_t* sal,
+                int dtype, int64_t R, int64_t C, void* Q, int64_t ldq, void* stream);
+int crbq_gemv_packed(const uint8_t* codes, int64_t ldc, const void* lut,
+                     const uint8_t* sal, int dtype, int64_t R, int64_t C,
+                     const void* x, int64_t ldx, int nvec, float* y, int64_t ldy,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

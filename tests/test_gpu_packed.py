@@ -1,0 +1,155 @@
+"""Packed low-bit storage on the GPU: crbq_pack / crbq_unpack byte-for-byte
+against the NumPy statement of the format (tests/packed_ref.py) and bit-exact
+round trips of layers quantized by the block loop; crbq_gemv_packed against
+float64 products of the unpacked weights; PackedLinear and the stack
+driver's pack option.
+
+GEMV bar: |y - y64| <= 1e-5 * sum_c |w_c x_c| per output (fp32 sums of
+exact 16-bit products)."""
+import numpy as np
+import pytest
+import torch
+
+from packed_ref import pack_ref, structured, unpack_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _k():
+    from crb_amd import kernels
+    return kernels
+
+
+@pytest.mark.parametrize("R,C,dtype", [(37, 300, torch.float16), (64, 512, torch.bfloat16),
+                                       (5, 128, torch.float16), (200, 1000, torch.bfloat16)])
+def test_pack_matches_format_statement(R, C, dtype):
+    print(f"pack structured {R}x{C} {dtype}", flush=True)
+    q, masks = structured(R, C, seed=R + C, dtype=np.float16)
+    bits = q.view(np.uint16)
+    if dtype == torch.bfloat16:          # reinterpret the same bit patterns as bf16
+        Q = torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16).to(DEV)
+    else:
+        Q = torch.from_numpy(q).to(DEV)
+    M = torch.from_numpy(masks).to(DEV)
+    codes, lut, sal = _k().pack(Q, M)
+    rc, rl, rs, st = pack_ref(bits, masks)
+    assert st == 0
+    assert np.array_equal(codes.cpu().numpy(), rc)
+    assert np.array_equal(lut.cpu().view(torch.int16).numpy().view(np.uint16), rl)
+    assert np.array_equal(sal.cpu().numpy(), rs)
+    back = _k().unpack(codes, lut, sal, C)
+    assert torch.equal(back.view(torch.int16).cpu(), Q.view(torch.int16).cpu())
+
+
+def test_pack_reports_structure_errors():
+    print("pack errors", flush=True)
+    from crb_amd._lib import CrbqError
+    q, masks = structured(8, 256, seed=3)
+    col = int(np.nonzero(masks[2, :128] == 1)[0][0])
+    bad = q.copy()
+    bad[2, col] = np.float16(0.123)
+    with pytest.raises(CrbqError, match="more distinct values"):
+        _k().pack(torch.from_numpy(bad).to(DEV), torch.from_numpy(masks).to(DEV))
+    m2 = masks.copy()
+    m2[5, int(np.nonzero(masks[0, :128] == 3)[0][0])] = 1
+    with pytest.raises(CrbqError, match="salient columns differ"):
+        _k().pack(torch.from_numpy(q).to(DEV), torch.from_numpy(m2).to(DEV))
+    # a valid layer afterwards still packs (the status word is cleared per call)
+    _k().pack(torch.from_numpy(q).to(DEV), torch.from_numpy(masks).to(DEV))
+
+
+@pytest.mark.parametrize("method,dtype,R,C", [("crb", torch.float16, 96, 320),
+                                              ("braq", torch.bfloat16, 64, 384),
+                                              ("crbog", torch.float16, 48, 256)])
+def test_quantized_layer_round_trip(method, dtype, R, C):
+    """Layers from the block loop (LayerQuantizer with keep_masks) pack and
+    unpack bit for bit (C = 320: a ragged last block of 64 columns, above the
+    salient search's 50-column minimum)."""
+    print(f"pack quantized {method} {R}x{C}", flush=True)
+    from crb_amd.driver import LayerQuantizer, Sublayer
+    g = torch.Generator().manual_seed(R * C)
+    W = (torch.randn(R, C, generator=g) * 0.02).to(dtype).to(DEV)
+    X = (torch.randn(4, 256, C, generator=g) * torch.exp(torch.randn(C, generator=g))).to(dtype)
+    lq = LayerQuantizer([Sublayer("w", W, "x")], method=method, keep_masks=True)
+    lq.add_batch("x", X.to(DEV))
+    lq.quantize()
+    codes, lut, sal = _k().pack(W, lq.masks["w"])
+    assert torch.equal(_k().unpack(codes, lut, sal, C).view(torch.int16), W.view(torch.int16))
+    rc, rl, rs, st = pack_ref(W.view(torch.int16).cpu().numpy().view(np.uint16),
+                              lq.masks["w"].cpu().numpy())
+    assert st == 0 and np.array_equal(codes.cpu().numpy(), rc)
+
+
+@pytest.mark.parametrize("R,C,dtype,nvec", [(37, 300, torch.float16, 1),
+                                            (256, 1024, torch.float16, 3),
+                                            (130, 640, torch.bfloat16, 8),
+                                            (1000, 4096, torch.bfloat16, 1),
+                                            (512, 2000, torch.float16, 5),
+                                            (64, 1000, torch.float16, 16),
+                                            (17, 136, torch.bfloat16, 11)])
+def test_gemv_against_float64(R, C, dtype, nvec):
+    print(f"gemv {R}x{C} {dtype} nvec={nvec}", flush=True)
+    q, masks = structured(R, C, seed=7 * R + C)
+    if dtype == torch.bfloat16:
+        Q = torch.from_numpy(q.view(np.uint16).astype(np.int16)).view(torch.bfloat16).to(DEV)
+    else:
+        Q = torch.from_numpy(q).to(DEV)
+    codes, lut, sal = _k().pack(Q, torch.from_numpy(masks).to(DEV))
+    g = torch.Generator().manual_seed(C)
+    xf = torch.randn(nvec, C + 24, generator=g)
+    x = xf.to(dtype).to(DEV)[:, :C]        # rows strided by C + 24
+    y = _k().gemv_packed(codes, lut, sal, C, x)
+    torch.cuda.synchronize()
+    W64 = Q.double().cpu()
+    x64 = x.double().cpu()
+    ref = x64 @ W64.t()
+    scale = x64.abs() @ W64.abs().t()
+    err = (y.double().cpu() - ref).abs()
+    assert (err <= 1e-5 * scale + 1e-30).all(), float((err / scale.clamp_min(1e-30)).max())
+
+
+def test_packed_linear_forward():
+    print("packed linear", flush=True)
+    from crb_amd.packed import PackedLinear
+    q, masks = structured(192, 512, seed=11)
+    lin = torch.nn.Linear(512, 192).to(DEV).half()
+    lin.weight.data = torch.from_numpy(q).to(DEV)
+    pl = PackedLinear.from_linear(lin, torch.from_numpy(masks).to(DEV))
+    assert torch.equal(pl.weight(), lin.weight.data)
+    assert pl.packed_bytes() * 8 / (192 * 512) < 3.1
+    g = torch.Generator().manual_seed(0)
+    for ntok in (1, 8, 40):                # 2 and 16 tokens: GEMV; 80: unpack
+        x = torch.randn(2, ntok, 512, generator=g).half().to(DEV)
+        with torch.no_grad():
+            got = pl(x).float()
+            want = torch.nn.functional.linear(x.float(), lin.weight.float(), lin.bias.float())
+        assert got.shape == (2, ntok, 192)
+        assert ((got - want).abs() <= 2e-3 * want.abs() + 2e-3).all(), ntok
+
+
+def test_stack_pack_option():
+    """StackQuantizer(pack=True) leaves PackedLinear modules that decode to
+    exactly the weights the unpacked run produces."""
+    print("stack pack", flush=True)
+    from test_gpu_stack import _samples, tiny_model
+    from crb_amd.packed import PackedLinear
+    from crb_amd.stack import StackQuantizer, find_linears
+    samples = _samples(n=6, seq=96)
+    a = tiny_model("opt")
+    StackQuantizer(a, chunk=3).run(samples)
+    b = tiny_model("opt")
+    stats = StackQuantizer(b, chunk=3, pack=True).run(samples)
+    assert all(st.packed_bytes > 0 for st in stats)
+    for la, lb in zip(a.model.decoder.layers, b.model.decoder.layers):
+        dense = find_linears(la)
+        for name, m in dense.items():
+            mod = lb
+            for p in name.split("."):
+                mod = getattr(mod, p)
+            assert isinstance(mod, PackedLinear), name
+            assert torch.equal(mod.weight(), m.weight.data), name
+    with torch.no_grad():
+        x = samples[:1, :5]
+        la_, lb_ = a(x).logits.float(), b(x).logits.float()
+    assert torch.allclose(la_, lb_, rtol=2e-2, atol=2e-2)
