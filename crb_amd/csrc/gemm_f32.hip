@@ -22,7 +22,8 @@ constexpr int P_MK = GB_K + 4;    // pitch of a row-of-K layout (m- or n-major)
 // LDS floats of one operand tile of a BT x BT output tile (either layout).
 template <int BT>
 struct TileCfg {
-  static constexpr int P_KM = BT + 4;                 // pitch of a K-major layout
+  static constexpr int P_KM = BT + 16;                // pitch of a K-major layout: the 4 lane
+                                                      // groups (k .. k+3) hit disjoint banks
   static constexpr int ELEMS = BT * P_MK > GB_K * P_KM ? BT * P_MK : GB_K * P_KM;
   static constexpr int NE = BT * GB_K / 4 / 256;      // float4 per thread per operand
   static constexpr int WT = BT / 2;                   // wavefront tile side (2 x 2 waves)
@@ -59,6 +60,25 @@ __device__ __forceinline__ void load_tile(const float* X, int64_t ld, int mn0, i
     } else {
       const int m = f >> 3, c = (f & 7) * 4;
       r[e] = ld4(X, ld, mn0 + m, k0 + c, MN, K, vec);
+    }
+  }
+}
+
+// The same tile when it lies wholly inside the matrix and rows are 16-byte
+// aligned: unconditional float4 loads.
+template <int BT, bool KMAJ>
+__device__ __forceinline__ void load_tile_in(const float* X, int64_t ld, int mn0, int k0,
+                                             float4 (&r)[TileCfg<BT>::NE]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int e = 0; e < TileCfg<BT>::NE; ++e) {
+    const int f = tid + 256 * e;
+    if (KMAJ) {
+      const int k = f / (BT / 4), c = (f % (BT / 4)) * 4;
+      r[e] = *(const float4*)(X + (int64_t)(k0 + k) * ld + mn0 + c);
+    } else {
+      const int m = f >> 3, c = (f & 7) * 4;
+      r[e] = *(const float4*)(X + (int64_t)(mn0 + m) * ld + k0 + c);
     }
   }
 }
@@ -135,6 +155,9 @@ __global__ __launch_bounds__(256) void k_sgemm(
     for (int j = 0; j < MT; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nch = kend > kbeg ? (kend - kbeg + GB_K - 1) / GB_K : 0;
+  // interior tile: every chunk but a ragged last one loads without bounds checks
+  const bool in_mn = va && vb && m0 + BT <= M && n0 + BT <= N;
+  const int nfull = in_mn ? (kend - kbeg) / GB_K : 0;
   float4 ra[NE], rb[NE];
   if (nch > 0) {
     load_tile<BT, AK>(A, lda, m0, kbeg, M, K, va, ra);
@@ -145,7 +168,10 @@ __global__ __launch_bounds__(256) void k_sgemm(
   __syncthreads();
   for (int c = 0; c < nch; ++c) {
     const int buf = c & 1;
-    if (c + 1 < nch) {
+    if (c + 1 < nfull) {
+      load_tile_in<BT, AK>(A, lda, m0, kbeg + (c + 1) * GB_K, ra);
+      load_tile_in<BT, BK>(B, ldb, n0, kbeg + (c + 1) * GB_K, rb);
+    } else if (c + 1 < nch) {
       load_tile<BT, AK>(A, lda, m0, kbeg + (c + 1) * GB_K, M, K, va, ra);
       load_tile<BT, BK>(B, ldb, n0, kbeg + (c + 1) * GB_K, N, K, vb, rb);
     }
