@@ -119,235 +119,267 @@ __global__ __launch_bounds__(256) void k_fallback_u(const float* __restrict__ H,
 
 // Diagonal block: Cholesky factor L and its inverse X = L^-1 of one
 // bj x bj block (bj <= NB; rows past bj are padded with the identity), in
-// place.  256 threads = 4 wavefronts.
-//  * Factorization in LDS: the 128 columns form 16 panels of 8; panel b
-//    belongs to wavefront b % 4.  The owner factors its panel in registers
-//    (lane l holds rows l and l + 64; pivots broadcast with readlane) and
-//    publishes it, and after one barrier every wavefront applies the
-//    rank-8 update to its own later panels.
-//  * Inverse: recursive doubling in LDS.  With X_A, X_C the inverses of two
-//    adjacent diagonal blocks of size s and B the block below X_A,
-//    X_B = -X_C (B X_A); s = 1, 2, 4, ..., 64.
+// place in LDS.  256 threads = 4 wavefronts.  The block is split
+// recursively like the whole matrix (X11, T = A21 X11^T, A22 -= T T^T,
+// A21 = T X11, X22, X21 = -X22 A21):
+//  * 16 x 16 leaves: one wavefront, lane i & 15 holding row i in
+//    registers; Cholesky by columns and the inverse by forward
+//    substitution over rows, the values other lanes need broadcast with
+//    readlane.
+//  * 32 x 32 blocks: one wavefront runs both leaves and the four 16 x 16
+//    products (v_mfma_f32_16x16x4f32), so no workgroup barrier is needed.
+//  * the 64 and 128 levels: the products' 16 x 16 output tiles are spread
+//    over the 4 wavefronts, one barrier between dependent products.
 // This factorization need not follow the reference's rounding step for
 // step (LAPACK's blocked potrf does not either), so it uses fused
-// multiply-adds and one reciprocal per pivot.
+// multiply-adds and hardware square root and reciprocal per pivot.
 constexpr int LDP = NB + 1;            // LDS pitch of the block (column reads conflict-free)
-constexpr int PANP = 12;               // LDS pitch of a panel row (8 used, 16-byte aligned)
-
-__device__ __forceinline__ float rdlane(float v, int l) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
+constexpr int TSP = NB / 2 + 1;        // LDS pitch of the product scratch T
 
 struct DiagSmem {
   float Ls[NB][LDP];
-  float pan[2][NB][PANP];
-  float Ts[64 * 64];
+  float Ts[(NB / 2) * TSP];
   int fail;
 };
 
-// Panel b of the factorization: the owner wavefront factors columns
-// 8b..8b+7 (rows in its lanes' registers, pivots broadcast with readlane),
-// every wavefront then applies the rank-8 update to its later panels in
-// LDS.  Returns false after a bad pivot.
-__device__ __forceinline__ bool chol_panel(int B, DiagSmem& sm, int lane, int w, int off, int bj,
-                                           int* info) {
-  float (*pb)[PANP] = sm.pan[B & 1];
-  if (w == (B & 3)) {
-    float pc[2][8];
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int q = 0; q < 8; ++q) pc[s][q] = sm.Ls[lane + 64 * s][8 * B + q];
-    const bool hi = B >= 8;            // the panel's diagonal rows are in slot 1
-#pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const int c = 8 * B + p;
-      const float piv = rdlane(hi ? pc[1][p] : pc[0][p], c & 63);
-      if (!(piv > 0.f) && lane == 0 && c < bj) {
-        sm.fail = 1;
-        atomicCAS(info, 0, off + c + 1);
-      }
-      const float d = __builtin_amdgcn_sqrtf(piv);
-      const float rd = __builtin_amdgcn_rcpf(d);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const int i = lane + 64 * s;
-        pc[s][p] = i > c ? pc[s][p] * rd : (i == c ? d : 0.f);
-      }
-#pragma unroll
-      for (int q = p + 1; q < 8; ++q) {
-        const float lq = rdlane(hi ? pc[1][p] : pc[0][p], (8 * B + q) & 63);   // L[8B+q][c]
-#pragma unroll
-        for (int s = 0; s < 2; ++s) pc[s][q] = fmaf(-pc[s][p], lq, pc[s][q]);
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int i = lane + 64 * s;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) sm.Ls[i][8 * B + q] = pc[s][q];
-      *(float4*)&pb[i][0] = make_float4(pc[s][0], pc[s][1], pc[s][2], pc[s][3]);
-      *(float4*)&pb[i][4] = make_float4(pc[s][4], pc[s][5], pc[s][6], pc[s][7]);
-    }
-  }
-  __syncthreads();
-  if (sm.fail) return false;
-  // rank-8 update of this wavefront's later panels; rows < 64 lie above
-  // every column >= 64
-  float pi[2][8];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const float4 u = *(const float4*)&pb[lane + 64 * s][0];
-    const float4 v = *(const float4*)&pb[lane + 64 * s][4];
-    pi[s][0] = u.x; pi[s][1] = u.y; pi[s][2] = u.z; pi[s][3] = u.w;
-    pi[s][4] = v.x; pi[s][5] = v.y; pi[s][6] = v.z; pi[s][7] = v.w;
-  }
-  for (int gb = w; gb < 16; gb += 4) {
-    if (gb <= B) continue;
-    // all 8 columns at once: loads first, then 16 independent FMA chains
-    float pj[8][8], t0[8], t1[8];
-#pragma unroll
-    for (int cc = 0; cc < 8; ++cc) {
-      const int j = 8 * gb + cc;
-      const float4 u = *(const float4*)&pb[j][0];
-      const float4 v = *(const float4*)&pb[j][4];
-      pj[cc][0] = u.x; pj[cc][1] = u.y; pj[cc][2] = u.z; pj[cc][3] = u.w;
-      pj[cc][4] = v.x; pj[cc][5] = v.y; pj[cc][6] = v.z; pj[cc][7] = v.w;
-      t0[cc] = sm.Ls[lane][j];
-      t1[cc] = sm.Ls[lane + 64][j];
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-#pragma unroll
-      for (int cc = 0; cc < 8; ++cc) {
-        t0[cc] = fmaf(-pi[0][q], pj[cc][q], t0[cc]);
-        t1[cc] = fmaf(-pi[1][q], pj[cc][q], t1[cc]);
-      }
-#pragma unroll
-    for (int cc = 0; cc < 8; ++cc) {
-      sm.Ls[lane][8 * gb + cc] = t0[cc];
-      sm.Ls[lane + 64][8 * gb + cc] = t1[cc];
-    }
-  }
-  return true;
+// Orders one wavefront's LDS accesses on both sides (lanes exchange data
+// through LDS between the phases of a single-wavefront block).
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
-// one level of the recursive-doubling inverse (pairs of S x S blocks)
-template <int S>
-__device__ __forceinline__ void inv_level(DiagSmem& sm, int tid) {
-  constexpr int NPAIR = NB / (2 * S);
-  if constexpr (S < 4) {
-    constexpr int NE = NPAIR * S * S;
-    for (int e = tid; e < NE; e += 256) {
-      const int q = e / (S * S), r = (e / S) % S, c = e % S, cb = 2 * S * q;
-      float t = 0.f;
-#pragma unroll
-      for (int k = 0; k < S; ++k) t = fmaf(sm.Ls[cb + S + r][cb + k], sm.Ls[cb + k][cb + c], t);
-      sm.Ts[e] = t;
-    }
-    __syncthreads();
-    for (int e = tid; e < NE; e += 256) {
-      const int q = e / (S * S), r = (e / S) % S, c = e % S, cb = 2 * S * q;
-      float t = 0.f;
-#pragma unroll
-      for (int k = 0; k < S; ++k) t = fmaf(sm.Ls[cb + S + r][cb + S + k], sm.Ts[q * S * S + k * S + c], t);
-      sm.Ls[cb + S + r][cb + c] = -t;
-    }
-    __syncthreads();
-  } else if constexpr (S < 16) {
-    constexpr int TPS = S / 4;                 // 4x4 tiles per block side
-    constexpr int NT = NPAIR * TPS * TPS;
-    // T = B X_A (X_A lower: rows k < j0 of X_A are zero in the tile's columns)
-    for (int e = tid; e < NT; e += 256) {
-      const int q = e / (TPS * TPS), ti = (e / TPS) % TPS, tj = e % TPS, cb = 2 * S * q;
-      const int i0 = 4 * ti, j0 = 4 * tj;
-      float t[4][4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) t[r][c] = 0.f;
-#pragma unroll
-      for (int k = 0; k < S; ++k) {
-        float b[4], x[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) b[r] = sm.Ls[cb + S + i0 + r][cb + k];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) x[c] = sm.Ls[cb + k][cb + j0 + c];
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) t[r][c] = fmaf(b[r], x[c], t[r][c]);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) sm.Ts[q * S * S + (i0 + r) * S + j0 + c] = t[r][c];
-    }
-    __syncthreads();
-    // X_B = -X_C T
-    for (int e = tid; e < NT; e += 256) {
-      const int q = e / (TPS * TPS), ti = (e / TPS) % TPS, tj = e % TPS, cb = 2 * S * q;
-      const int i0 = 4 * ti, j0 = 4 * tj;
-      const float* T = sm.Ts + q * S * S;
-      float t[4][4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) t[r][c] = 0.f;
-#pragma unroll
-      for (int k = 0; k < S; ++k) {
-        float xc[4], tv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) xc[r] = sm.Ls[cb + S + i0 + r][cb + S + k];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) tv[c] = T[k * S + j0 + c];
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) t[r][c] = fmaf(xc[r], tv[c], t[r][c]);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) sm.Ls[cb + S + i0 + r][cb + j0 + c] = -t[r][c];
-    }
-    __syncthreads();
-  } else {
-    // 16 x 16 output tiles on v_mfma_f32_16x16x4_f32, one tile per
-    // wavefront at a time: lane l supplies A[l%16][k + l/16] and
-    // B[k + l/16][l%16] and receives D[4*(l/16) + r][l%16], r = 0..3.
-    constexpr int TPS = S / 16;
-    constexpr int NT = NPAIR * TPS * TPS;
-    const int lane = tid & 63, wv = tid >> 6, lr = lane & 15, lk = lane >> 4;
-    for (int e = wv; e < NT; e += 4) {        // T = B X_A, k >= 16 tj
-      const int q = e / (TPS * TPS), ti = (e / TPS) % TPS, tj = e % TPS, cb = 2 * S * q;
-      f4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int k = 16 * tj; k < S; k += 4) {
-        const float av = sm.Ls[cb + S + 16 * ti + lr][cb + k + lk];
-        const float bv = sm.Ls[cb + k + lk][cb + 16 * tj + lr];
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sm.Ts[q * S * S + (16 * ti + 4 * lk + r) * S + 16 * tj + lr] = acc[r];
-    }
-    __syncthreads();
-    for (int e = wv; e < NT; e += 4) {        // X_B = -X_C T, k < 16 (ti + 1)
-      const int q = e / (TPS * TPS), ti = (e / TPS) % TPS, tj = e % TPS, cb = 2 * S * q;
-      const float* T = sm.Ts + q * S * S;
-      f4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int k = 0; k < 16 * (ti + 1); k += 4) {
-        const float av = sm.Ls[cb + S + 16 * ti + lr][cb + S + k + lk];
-        const float bv = T[(k + lk) * S + 16 * tj + lr];
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sm.Ls[cb + S + 16 * ti + 4 * lk + r][cb + 16 * tj + lr] = -acc[r];
-    }
-    __syncthreads();
+__device__ __forceinline__ f4_t mfma4(float a, float b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Value of lane L of each 16-lane row in every lane of that row (DPP
+// row_newbcast).  In the leaves the four rows of a wavefront hold the same
+// data, so this is lane L's value in VGPRs, with no scalar registers.
+template <int L>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xf, 0xf,
+                                                    false));
+}
+__device__ __forceinline__ float row_bcast(float v, int l) {   // l is a constant after unrolling
+  switch (l) {
+    case 0: return row_bcast<0>(v);   case 1: return row_bcast<1>(v);
+    case 2: return row_bcast<2>(v);   case 3: return row_bcast<3>(v);
+    case 4: return row_bcast<4>(v);   case 5: return row_bcast<5>(v);
+    case 6: return row_bcast<6>(v);   case 7: return row_bcast<7>(v);
+    case 8: return row_bcast<8>(v);   case 9: return row_bcast<9>(v);
+    case 10: return row_bcast<10>(v); case 11: return row_bcast<11>(v);
+    case 12: return row_bcast<12>(v); case 13: return row_bcast<13>(v);
+    case 14: return row_bcast<14>(v); default: return row_bcast<15>(v);
   }
-  if constexpr (2 * S < NB) inv_level<2 * S>(sm, tid);
+}
+
+// 16 x 16 leaf at (o, o): L = chol(A), then X = L^-1 written over it (zeros
+// above the diagonal).  One wavefront; each 16-lane row repeats lanes 0..15.
+//  * Cholesky with lane i holding row i: at column j the pivot comes from
+//    lane j and L[k][j] from lane k (row broadcasts); lanes i <= j keep
+//    scratch in column j, never read.
+//  * Inverse with lane c holding column c of X: forward substitution
+//    X[r][c] = (delta_rc - sum_{k<r} L[r][k] X[k][c]) / L[r][r], the L
+//    values broadcast from lane r, so no lane masks are needed.
+__device__ __forceinline__ void leaf16(DiagSmem& sm, int o, int lane, int off, int bj,
+                                       int* info) {
+  const int i = lane & 15;
+  float a[16], rdg[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) a[c] = sm.Ls[o + i][o + c];
+  int badl = 16;   // first bad pivot (the same in every lane)
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float piv = row_bcast(a[j], j);
+    badl = (!(piv > 0.f) && o + j < bj && badl == 16) ? j : badl;
+    const float rd = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(piv));
+    rdg[j] = rd;
+    a[j] *= rd;
+#pragma unroll
+    for (int k = j + 1; k < 16; ++k) a[k] = fmaf(-a[j], row_bcast(a[j], k), a[k]);
+  }
+  const int bad = __builtin_amdgcn_readfirstlane(badl);
+  if (bad < 16 && lane == 0) {
+    sm.fail = 1;
+    atomicCAS(info, 0, off + o + bad + 1);
+  }
+  float y[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float acc = i == r ? 1.f : 0.f;
+#pragma unroll
+    for (int k = 0; k < r; ++k) acc = fmaf(-row_bcast(a[k], r), y[k], acc);
+    y[r] = acc * rdg[r];
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sm.Ls[o + r][o + i] = y[r];
+  }
+}
+
+// 32 x 32 block at (o, o) by one wavefront: lane l supplies A[l%16][k + l/16]
+// and B[k + l/16][l%16] to each MFMA and receives D[4*(l/16) + r][l%16].
+__device__ __forceinline__ void block32(DiagSmem& sm, int o, int lane, int off, int bj,
+                                        int* info) {
+  const int lr = lane & 15, lk = lane >> 4, p = o + 16;
+  leaf16(sm, o, lane, off, bj, info);
+  wave_lds_sync();
+  f4_t t = {0.f, 0.f, 0.f, 0.f};              // T = A21 X11^T
+#pragma unroll
+  for (int k = 0; k < 16; k += 4) t = mfma4(sm.Ls[p + lr][o + k + lk], sm.Ls[o + lr][o + k + lk], t);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sm.Ts[(4 * lk + r) * TSP + lr] = t[r];
+  wave_lds_sync();
+  f4_t s = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < 16; k += 4) {
+    const float tv = sm.Ts[lr * TSP + k + lk];
+    s = mfma4(tv, tv, s);                      // T T^T
+    u = mfma4(tv, sm.Ls[o + k + lk][o + lr], u);   // T X11
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int rr = 4 * lk + r;
+    if (lr <= rr) sm.Ls[p + rr][p + lr] -= s[r];
+    sm.Ls[p + rr][o + lr] = u[r];
+  }
+  wave_lds_sync();
+  leaf16(sm, p, lane, off, bj, info);
+  wave_lds_sync();
+  f4_t x = {0.f, 0.f, 0.f, 0.f};              // X21 = -X22 A21
+#pragma unroll
+  for (int k = 0; k < 16; k += 4) x = mfma4(sm.Ls[p + lr][p + k + lk], sm.Ls[p + k + lk][o + lr], x);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sm.Ls[p + 4 * lk + r][o + lr] = -x[r];
+  wave_lds_sync();
+}
+
+// Lower-triangle tile e (row-major over ti >= tj) of an NTL x NTL tile grid.
+__device__ __forceinline__ void lower_tile(int e, int& ti, int& tj) {
+  ti = 0;
+  while ((ti + 1) * (ti + 2) / 2 <= e) ++ti;
+  tj = e - ti * (ti + 1) / 2;
+}
+
+// The products of a level with H-row halves at (o, o), 16 x 16 tiles over
+// the 4 wavefronts.  Full-depth products (the triangular operands' zero
+// halves included) so that every operand read of a tile can be issued
+// before its MFMA chain, with a wavefront's tiles interleaved.  Ends with a
+// barrier.
+template <int H>
+__device__ __forceinline__ void level_panel(DiagSmem& sm, int o, int wv, int lane) {
+  constexpr int NTL = H / 16, TPW = NTL * NTL / 4, NL = NTL * (NTL + 1) / 2;
+  constexpr int LPW = (NL + 3) / 4;
+  const int lr = lane & 15, lk = lane >> 4, p = o + H;
+  {                                            // T = A21 X11^T
+    f4_t t[TPW];
+    int ti[TPW], tj[TPW];
+#pragma unroll
+    for (int q = 0; q < TPW; ++q) {
+      ti[q] = (wv + 4 * q) / NTL;
+      tj[q] = (wv + 4 * q) % NTL;
+      t[q] = f4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int k = 0; k < H; k += 4)
+#pragma unroll
+      for (int q = 0; q < TPW; ++q)
+        t[q] = mfma4(sm.Ls[p + 16 * ti[q] + lr][o + k + lk],
+                     sm.Ls[o + 16 * tj[q] + lr][o + k + lk], t[q]);
+#pragma unroll
+    for (int q = 0; q < TPW; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        sm.Ts[(16 * ti[q] + 4 * lk + r) * TSP + 16 * tj[q] + lr] = t[q][r];
+  }
+  __syncthreads();
+  {                                            // A22 -= T T^T (lower tiles)
+    f4_t s[LPW];
+    int ti[LPW], tj[LPW];
+#pragma unroll
+    for (int q = 0; q < LPW; ++q) {
+      const int e = wv + 4 * q;
+      lower_tile(e < NL ? e : NL - 1, ti[q], tj[q]);
+      s[q] = f4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int k = 0; k < H; k += 4)
+#pragma unroll
+      for (int q = 0; q < LPW; ++q)
+        s[q] = mfma4(sm.Ts[(16 * ti[q] + lr) * TSP + k + lk],
+                     sm.Ts[(16 * tj[q] + lr) * TSP + k + lk], s[q]);
+    f4_t u[TPW];                               // A21 = T X11
+    int ui[TPW], uj[TPW];
+#pragma unroll
+    for (int q = 0; q < TPW; ++q) {
+      ui[q] = (wv + 4 * q) / NTL;
+      uj[q] = (wv + 4 * q) % NTL;
+      u[q] = f4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int k = 0; k < H; k += 4)
+#pragma unroll
+      for (int q = 0; q < TPW; ++q)
+        u[q] = mfma4(sm.Ts[(16 * ui[q] + lr) * TSP + k + lk],
+                     sm.Ls[o + k + lk][o + 16 * uj[q] + lr], u[q]);
+#pragma unroll
+    for (int q = 0; q < LPW; ++q) {
+      if (wv + 4 * q < NL) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int rr = 16 * ti[q] + 4 * lk + r, cc = 16 * tj[q] + lr;
+          if (cc <= rr) sm.Ls[p + rr][p + cc] -= s[q][r];
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < TPW; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sm.Ls[p + 16 * ui[q] + 4 * lk + r][o + 16 * uj[q] + lr] = u[q][r];
+  }
+  __syncthreads();
+}
+
+// X21 = -X22 A21 of a level (full depth, as above); results are held in
+// registers until every wavefront has read A21.  Ends with a barrier.
+template <int H>
+__device__ __forceinline__ void level_x21(DiagSmem& sm, int o, int wv, int lane) {
+  constexpr int NTL = H / 16, TPW = NTL * NTL / 4;
+  const int lr = lane & 15, lk = lane >> 4, p = o + H;
+  f4_t x[TPW];
+  int ti[TPW], tj[TPW];
+#pragma unroll
+  for (int q = 0; q < TPW; ++q) {
+    ti[q] = (wv + 4 * q) / NTL;
+    tj[q] = (wv + 4 * q) % NTL;
+    x[q] = f4_t{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int k = 0; k < H; k += 4)
+#pragma unroll
+    for (int q = 0; q < TPW; ++q)
+      x[q] = mfma4(sm.Ls[p + 16 * ti[q] + lr][p + k + lk], sm.Ls[p + k + lk][o + 16 * tj[q] + lr],
+                   x[q]);
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < TPW; ++q)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sm.Ls[p + 16 * ti[q] + 4 * lk + r][o + 16 * tj[q] + lr] = -x[q][r];
+  __syncthreads();
+}
+
+// 64 x 64 block at (o, o).  Returns false after a bad pivot (uniformly).
+__device__ __forceinline__ bool block64(DiagSmem& sm, int o, int wv, int lane, int off, int bj,
+                                        int* info) {
+  if (wv == 0) block32(sm, o, lane, off, bj, info);
+  __syncthreads();
+  if (sm.fail) return false;
+  level_panel<32>(sm, o, wv, lane);
+  if (wv == 0) block32(sm, o + 32, lane, off, bj, info);
+  __syncthreads();
+  if (sm.fail) return false;
+  level_x21<32>(sm, o, wv, lane);
+  return true;
 }
 
 __global__ __launch_bounds__(256) void k_chol_inv_diag(float* A, int64_t lda, int off, int bj,
@@ -356,10 +388,10 @@ __global__ __launch_bounds__(256) void k_chol_inv_diag(float* A, int64_t lda, in
   __shared__ DiagSmem sm;
   // the wavefront index as a scalar, so branches on it are uniform
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool vec = ((lda & 3) == 0) && ((((uintptr_t)A) & 15) == 0) && ((off & 3) == 0);
   // ---- load the block (lower triangle), identity padding, zero above;
   // 16 coalesced 4-float groups per thread, all in flight together
   {
-    const bool vec = ((lda & 3) == 0) && ((((uintptr_t)A) & 15) == 0);
     float v[16][4];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
@@ -385,19 +417,26 @@ __global__ __launch_bounds__(256) void k_chol_inv_diag(float* A, int64_t lda, in
   }
   if (tid == 0) sm.fail = 0;
   __syncthreads();
-  // ---- factorization (L overwrites the block, zeros above the diagonal)
-  for (int B = 0; B < 16; ++B)
-    if (!chol_panel(B, sm, lane, w, off, bj, info)) return;
-  __syncthreads();
-  if (tid < NB) sm.Ls[tid][tid] = 1.f / sm.Ls[tid][tid];
-  __syncthreads();
-  // ---- inverse by recursive doubling
-  inv_level<1>(sm, tid);
-  // ---- write X (zero above the diagonal)
-#pragma unroll 8
-  for (int e = tid; e < NB * NB; e += 256) {
-    const int i = e >> 7, j = e & (NB - 1);
-    if (i < bj && j < bj) A[(int64_t)(off + i) * lda + off + j] = j <= i ? sm.Ls[i][j] : 0.f;
+  // ---- X = L^-1 over the block (L is not kept)
+  if (!block64(sm, 0, w, lane, off, bj, info)) return;
+  level_panel<64>(sm, 0, w, lane);
+  if (!block64(sm, 64, w, lane, off, bj, info)) return;
+  level_x21<64>(sm, 0, w, lane);
+  // ---- write X (zero above the diagonal), 16-byte stores where aligned
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int f = tid + 256 * u, i = f >> 5, j0 = (f & 31) * 4;
+    float* dst = A + (int64_t)(off + i) * lda + off + j0;
+    float q[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) q[c] = j0 + c <= i ? sm.Ls[i][j0 + c] : 0.f;
+    if (vec && i < bj && j0 + 3 < bj) {
+      *(float4*)dst = make_float4(q[0], q[1], q[2], q[3]);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (i < bj && j0 + c < bj) dst[c] = q[c];
+    }
   }
 }
 
