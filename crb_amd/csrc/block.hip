@@ -234,9 +234,13 @@ __global__ __launch_bounds__(CS_THREADS) void k_colscore(
 // e = r - m2, E1 = sum |e|, E2 = sum e^2, nz = #(e != 0).  Group sums of x
 // come from a wave prefix scan; sum |x - m1| and the sign counts (which give
 // sum r in closed form, s1 taking the three fp32 values m1 +- a1 and m1)
-// from one pass; E1, E2, nz from a second pass in which r and e are formed
-// with the reference's fp32 operations, so every sign decision is the
-// reference's.  All sums are fp64.
+// from one pass; E1, E2, nz from a second pass in which s1, r and e are
+// formed with the reference's fp32 operations, so every sign decision is
+// the reference's.  Sums run in fp32 over chunks of 8 elements and are
+// accumulated in fp64; counts are integers.  Ranks below ncand are the
+// only ones a candidate's salient group can hold ("mixed" ranks, where each
+// element is routed to its group by a select); the rest always belong to
+// the complement.
 #ifndef CRBQ_PA_WAVES
 #define CRBQ_PA_WAVES 16
 #endif
@@ -244,56 +248,107 @@ constexpr int PA_WAVES = CRBQ_PA_WAVES;
 
 struct GroupA {         // per-lane accumulators of one group
   double ad, e1, e2;
-  float npos, nneg, nz;
+  int npos, nneg, nz;
 };
 
+struct ParA {           // a group's fp32 parameters for the residual pass
+  float m1, hi, lo, m2;   // hi = fl(a1 + m1), lo = fl(-a1 + m1)
+};
+
+// sum |x - m1| and the sign counts of x - m1 over ranks [c0, c1)
 template <bool MIXED>
-__device__ __forceinline__ void pass_abs(const float* xs, int c0, int c1, int i, float m1S,
-                                         float m1C, GroupA& S, GroupA& Cg) {
-  for (int c = c0; c < c1; ++c) {
-    const float x = xs[c];
-    const bool inS = MIXED && c < i;
-    const float d = x - (inS ? m1S : m1C);
-    const double ad = (double)fabsf(d);
-    const float pos = d > 0.f ? 1.f : 0.f, neg = d < 0.f ? 1.f : 0.f;
-    if (MIXED) {
-      S.ad += inS ? ad : 0.0;
-      S.npos += inS ? pos : 0.f;
-      S.nneg += inS ? neg : 0.f;
-    }
-    Cg.ad += inS ? 0.0 : ad;
-    Cg.npos += inS ? 0.f : pos;
-    Cg.nneg += inS ? 0.f : neg;
+__device__ __forceinline__ void abs_elem(float x, bool inS, float m1S, float m1C, float& pS,
+                                         float& pC, GroupA& S, GroupA& Cg) {
+  const float d = x - (inS ? m1S : m1C);
+  const float ad = fabsf(d);
+  const int pos = d > 0.f ? 1 : 0, neg = d < 0.f ? 1 : 0;
+  if (MIXED) {
+    pS += inS ? ad : 0.f;
+    S.npos += inS ? pos : 0;
+    S.nneg += inS ? neg : 0;
+    pC += inS ? 0.f : ad;
+    Cg.npos += inS ? 0 : pos;
+    Cg.nneg += inS ? 0 : neg;
+  } else {
+    pC += ad;
+    Cg.npos += pos;
+    Cg.nneg += neg;
   }
 }
 
 template <bool MIXED>
-__device__ __forceinline__ void pass_res(const float* xs, int c0, int c1, int i,
-                                         const float (&m1)[2], const float (&a1)[2],
-                                         const float (&m2)[2], GroupA& S, GroupA& Cg) {
-  for (int c = c0; c < c1; ++c) {
-    const float x = xs[c];
-    const bool inS = MIXED && c < i;
-    const int g = inS ? 0 : 1;
-    const float m = MIXED ? (inS ? m1[0] : m1[1]) : m1[1];
-    const float a = MIXED ? (inS ? a1[0] : a1[1]) : a1[1];
-    const float mm = MIXED ? (inS ? m2[0] : m2[1]) : m2[1];
-    (void)g;
-    float s1 = tsign(x - m) * a;                 // binary.py:32-34
-    s1 = s1 + m;
-    const float r = x - s1;                      // binary.py:26 (order 2)
-    const float e = r - mm;
-    const double ae = (double)fabsf(e), e2 = (double)e * (double)e;
-    const float nz = e != 0.f ? 1.f : 0.f;
-    if (MIXED) {
-      S.e1 += inS ? ae : 0.0;
-      S.e2 += inS ? e2 : 0.0;
-      S.nz += inS ? nz : 0.f;
-    }
-    Cg.e1 += inS ? 0.0 : ae;
-    Cg.e2 += inS ? 0.0 : e2;
-    Cg.nz += inS ? 0.f : nz;
+__device__ __forceinline__ void pass_abs(const float* xs, int c0, int c1, int i, float m1S,
+                                         float m1C, GroupA& S, GroupA& Cg) {
+  int c = c0;
+  for (; c + 8 <= c1; c += 8) {
+    float pS = 0.f, pC = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) abs_elem<MIXED>(xs[c + u], MIXED && c + u < i, m1S, m1C, pS, pC, S, Cg);
+    if (MIXED) S.ad += (double)pS;
+    Cg.ad += (double)pC;
   }
+  float pS = 0.f, pC = 0.f;
+  for (; c < c1; ++c) abs_elem<MIXED>(xs[c], MIXED && c < i, m1S, m1C, pS, pC, S, Cg);
+  if (MIXED) S.ad += (double)pS;
+  Cg.ad += (double)pC;
+}
+
+// e = (x - s1) - m2 with s1 = sign(x - m1)*a1 + m1 in fp32 (binary.py:26,
+// 32-34): sign*a1 is exact, so s1 is one of hi, lo, m1
+__device__ __forceinline__ float resid(float x, const ParA& g) {
+  const float d = x - g.m1;
+  const float s1 = d > 0.f ? g.hi : (d < 0.f ? g.lo : g.m1);
+  const float r = x - s1;
+  return r - g.m2;
+}
+
+template <bool MIXED>
+__device__ __forceinline__ void res_elem(float x, bool inS, const ParA& PS, const ParA& PC,
+                                         float& p1S, float& p2S, float& p1C, float& p2C,
+                                         GroupA& S, GroupA& Cg) {
+  ParA g = PC;
+  if (MIXED) {
+    g.m1 = inS ? PS.m1 : PC.m1;
+    g.hi = inS ? PS.hi : PC.hi;
+    g.lo = inS ? PS.lo : PC.lo;
+    g.m2 = inS ? PS.m2 : PC.m2;
+  }
+  const float e = resid(x, g);
+  const float ae = fabsf(e);
+  const float e2 = e * e;
+  const int nz = e != 0.f ? 1 : 0;
+  if (MIXED) {
+    p1S += inS ? ae : 0.f;
+    p2S += inS ? e2 : 0.f;
+    S.nz += inS ? nz : 0;
+    p1C += inS ? 0.f : ae;
+    p2C += inS ? 0.f : e2;
+    Cg.nz += inS ? 0 : nz;
+  } else {
+    p1C += ae;
+    p2C += e2;
+    Cg.nz += nz;
+  }
+}
+
+template <bool MIXED>
+__device__ __forceinline__ void pass_res(const float* xs, int c0, int c1, int i, const ParA& PS,
+                                         const ParA& PC, GroupA& S, GroupA& Cg) {
+  int c = c0;
+  for (; c + 8 <= c1; c += 8) {
+    float p1S = 0.f, p2S = 0.f, p1C = 0.f, p2C = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      res_elem<MIXED>(xs[c + u], MIXED && c + u < i, PS, PC, p1S, p2S, p1C, p2C, S, Cg);
+    if (MIXED) { S.e1 += (double)p1S; S.e2 += (double)p2S; }
+    Cg.e1 += (double)p1C;
+    Cg.e2 += (double)p2C;
+  }
+  float p1S = 0.f, p2S = 0.f, p1C = 0.f, p2C = 0.f;
+  for (; c < c1; ++c) res_elem<MIXED>(xs[c], MIXED && c < i, PS, PC, p1S, p2S, p1C, p2C, S, Cg);
+  if (MIXED) { S.e1 += (double)p1S; S.e2 += (double)p2S; }
+  Cg.e1 += (double)p1C;
+  Cg.e2 += (double)p2C;
 }
 
 __global__ __launch_bounds__(64 * PA_WAVES) void k_phase_a(
@@ -312,7 +367,7 @@ __global__ __launch_bounds__(64 * PA_WAVES) void k_phase_a(
   if (c1 < nc) { const float dg = U[(int64_t)c1 * ldu + c1]; d21 = dg * dg; }
   const int i = lane + 1;                        // candidate (salient columns)
   const float nS = (float)i, nC = (float)(nc - i);
-  const int mix_end = min(nc, 64);               // ranks >= 64 are never salient
+  const int mix_end = min(nc, ncand);            // ranks >= ncand are never salient
   double acc = 0.0;
   for (int r0 = blockIdx.x * PA_WAVES; r0 < R; r0 += gridDim.x * PA_WAVES) {
     const int row = r0 + wv;
@@ -336,7 +391,7 @@ __global__ __launch_bounds__(64 * PA_WAVES) void k_phase_a(
       const double tot = wave_sum(y0 + y1);
       const float m1S = (float)ps / nS;
       const float m1C = nC > 0.f ? (float)(tot - ps) / nC : 0.f;
-      GroupA S = {0.0, 0.0, 0.0, 0.f, 0.f, 0.f}, Cg = {0.0, 0.0, 0.0, 0.f, 0.f, 0.f};
+      GroupA S = {0.0, 0.0, 0.0, 0, 0, 0}, Cg = {0.0, 0.0, 0.0, 0, 0, 0};
       pass_abs<true>(x, 0, mix_end, i, m1S, m1C, S, Cg);
       pass_abs<false>(x, mix_end, nc, i, m1S, m1C, S, Cg);
       const float a1S = (float)S.ad / nS;
@@ -349,9 +404,9 @@ __global__ __launch_bounds__(64 * PA_WAVES) void k_phase_a(
                          ((double)nC - Cg.npos - Cg.nneg) * (double)m1C;
       const float m2S = (float)(ps - s1S) / nS;
       const float m2C = nC > 0.f ? (float)((tot - ps) - s1C) / nC : 0.f;
-      const float m1v[2] = {m1S, m1C}, a1v[2] = {a1S, a1C}, m2v[2] = {m2S, m2C};
-      pass_res<true>(x, 0, mix_end, i, m1v, a1v, m2v, S, Cg);
-      pass_res<false>(x, mix_end, nc, i, m1v, a1v, m2v, S, Cg);
+      const ParA PS = {m1S, hiS, loS, m2S}, PC = {m1C, hiC, loC, m2C};
+      pass_res<true>(x, 0, mix_end, i, PS, PC, S, Cg);
+      pass_res<false>(x, mix_end, nc, i, PS, PC, S, Cg);
       const double a2S = (double)((float)S.e1 / nS);
       const double a2C = nC > 0.f ? (double)((float)Cg.e1 / nC) : 0.0;
       const double eS = S.e2 - 2.0 * a2S * S.e1 + a2S * a2S * (double)S.nz;
