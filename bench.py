@@ -266,9 +266,9 @@ def main():
         print(json.dumps({"calibrate_copy_bytes": x.numel() * 4, "copies": 3}))
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; the path shards by "
-                                   "sublayer and by calibration tokens (see DESIGN.md), "
-                                   "but no multi-GPU figure is produced"}))
+        print(json.dumps({"error": "this build runs on one GPU only; the path would shard "
+                                   "by sublayer and by calibration tokens, but no "
+                                   "multi-GPU figure is produced"}))
         sys.exit(2)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
