@@ -135,10 +135,11 @@ def stack_run(dev, nlayers, ntok, chunk=8, seed=0):
 
 
 def packed_gemv(dev, R=4096, C=16384, reps=20):
-    """Packed 3-bit GEMV (crbq_gemv_packed) on the fc2 shape against torch's
-    dense fp16 GEMV of the same weights, per launch, from captured HIP graphs
-    of `reps` launches (host call overhead excluded).  Random packed data:
-    the kernel's work does not depend on the values."""
+    """Packed 3-bit GEMV (crbq_gemv_packed, 1-16 tokens) and GEMM
+    (crbq_gemm_packed, 64 and 256 tokens) on the fc2 shape against torch's
+    dense fp16 product with the same weights, per launch, from captured HIP
+    graphs of `reps` launches (host call overhead excluded).  Random packed
+    data: the kernels' work does not depend on the values."""
     from crb_amd import kernels
     torch.manual_seed(0)
     nblk = C // 128
@@ -179,6 +180,13 @@ def packed_gemv(dev, R=4096, C=16384, reps=20):
         out["per_nvec"][nvec] = {"packed_us": round(tp, 2), "dense_fp16_us": round(td, 2),
                                  "packed_weight_GB_s": round(nbytes / tp / 1e3, 1),
                                  "dense_weight_GB_s": round(R * C * 2 / td / 1e3, 1)}
+    out["gemm_per_ntok"] = {}
+    for ntok in (64, 256):
+        x = torch.randn(ntok, C, device=dev).half()
+        tp = graph_us(lambda: kernels.gemm_packed(codes, lut, sal, C, x))
+        td = graph_us(lambda: torch.nn.functional.linear(x, W))
+        out["gemm_per_ntok"][ntok] = {"packed_us": round(tp, 2), "dense_fp16_us": round(td, 2),
+                                      "packed_TFLOP_s": round(2 * R * C * ntok / tp / 1e6, 1)}
     return out
 
 

@@ -16,6 +16,8 @@
 // with weight = lut[r][b][4 * sal + code], code = (mask2 ? 2 : 0) + rank
 // for non-salient weights and rank (0..3) for salient ones: 3 bits per
 // weight instead of 16, and unpacking reproduces the weights bit for bit.
+#include <algorithm>
+
 #include "common.h"
 
 namespace crbq {
@@ -265,6 +267,142 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_packed(
   }
 }
 
+// Y[t][r] = sum_c W[r][c] X[t][c] for many tokens (prefill), W packed:
+// the GEMV's decode, with each decoded fragment reused for a tile of
+// tokens.  A workgroup of GM_WAVES wavefronts covers 16 * GM_WAVES rows x
+// TT tokens (64, or 128 for more than 64 tokens); per 128-column block each wavefront decodes its 16 rows'
+// 128 columns (lane l: row l & 15, columns 32 (l >> 4) .. +31, four
+// 8-column MFMA slices) and multiplies them with every 16-token group of
+// the X tile, which the whole workgroup stages in LDS (rows padded to 136
+// halves so a 16-lane group's 16-byte reads of 16 tokens fall on disjoint
+// banks).  The X tile of the next block is loaded into registers while the
+// current one is used.  When row and token tiles alone would leave CUs idle
+// the block range is split over gridDim.z workgroups, each writing an fp32
+// partial [T][R] slice that k_gemm_packed_sum adds in split order.
+constexpr int GM_WAVES = 8;
+constexpr int GM_ROWS = 16 * GM_WAVES;
+constexpr int GM_XP = PB + 8;                     // LDS pitch of an X tile row (halves)
+
+static inline int gemm_packed_tt(int64_t T) { return T > 64 ? 128 : 64; }
+
+template <typename T8, int GM_TT>
+__global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_packed(
+    const uint8_t* __restrict__ codes, int64_t ldc, const uint16_t* __restrict__ lut,
+    const uint8_t* __restrict__ sal, int R, int C, int nblk, const uint16_t* __restrict__ x,
+    int64_t ldx, int T, int bps, float* __restrict__ y, int64_t ldy) {
+  __shared__ __attribute__((aligned(16))) uint16_t Xs[2][GM_TT][GM_XP];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int r0 = blockIdx.x * GM_ROWS, t0 = blockIdx.y * GM_TT;
+  const int b_beg = blockIdx.z * bps, b_end = min(nblk, b_beg + bps);
+  const int row = r0 + wave * 16 + (lane & 15), kq = lane >> 4;
+  const bool row_ok = row < R;
+  const uint8_t* crow = codes + (int64_t)(row_ok ? row : 0) * ldc;
+  const uint4* lrow = (const uint4*)(lut + (int64_t)(row_ok ? row : 0) * nblk * 8);
+  // X tile loader: thread -> (token xt, XPT 8-column chunks from xc)
+  constexpr int XPT = GM_TT * PB / 8 / (64 * GM_WAVES);     // 16-byte chunks per thread
+  constexpr int TPR = PB / 8 / XPT;                         // threads per token row
+  const int xt = tid / TPR, xc = (tid % TPR) * XPT * 8;
+  const int tok = t0 + xt;
+  const bool tok_ok = tok < T;
+  const uint16_t* xrow = x + (int64_t)(tok_ok ? tok : 0) * ldx;
+  auto load_x = [&](int b, uint4 (&u)[XPT]) {
+    const int c = b * PB + xc;
+    if (tok_ok && c + 8 * XPT <= C) {
+#pragma unroll
+      for (int k = 0; k < XPT; ++k) u[k] = *(const uint4*)(xrow + c + 8 * k);
+    } else {
+#pragma unroll
+      for (int k = 0; k < XPT; ++k) {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = tok_ok && c + 8 * k + e < C ? xrow[c + 8 * k + e] : 0u;
+        u[k] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                          h[6] | (h[7] << 16));
+      }
+    }
+  };
+  f4_t acc[GM_TT / 16];
+#pragma unroll
+  for (int g = 0; g < GM_TT / 16; ++g) acc[g] = f4_t{0.f, 0.f, 0.f, 0.f};
+  uint4 u[XPT];
+  if (b_beg < b_end) load_x(b_beg, u);
+  for (int b = b_beg; b < b_end; ++b) {
+    const int buf = (b - b_beg) & 1;
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) *(uint4*)&Xs[buf][xt][xc + 8 * k] = u[k];
+    __syncthreads();
+    if (b + 1 < b_end) load_x(b + 1, u);
+    const uint2 cw = row_ok ? *(const uint2*)(crow + b * 32 + kq * 8) : make_uint2(0u, 0u);
+    const uint32_t sb = *(const uint32_t*)(sal + (int64_t)b * 16 + kq * 4);
+    const uint4 L = row_ok ? lrow[b] : make_uint4(0u, 0u, 0u, 0u);
+    T8 a[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t cws = (k < 2 ? cw.x : cw.y) >> (16 * (k & 1));
+      const uint32_t sbs = sb >> (8 * k);
+      uint4 q;
+      q.x = decode_pair(cws, 0, L, sbs);
+      q.y = decode_pair(cws, 1, L, sbs);
+      q.z = decode_pair(cws, 2, L, sbs);
+      q.w = decode_pair(cws, 3, L, sbs);
+      a[k] = __builtin_bit_cast(T8, q);
+    }
+#pragma unroll
+    for (int g = 0; g < GM_TT / 16; ++g) {
+      if (t0 + g * 16 >= T) break;                // token groups past the end (uniform)
+      const uint16_t* xr = &Xs[buf][g * 16 + (lane & 15)][kq * 32];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        acc[g] = mfma_gv<T8>(a[k], *(const T8*)(xr + 8 * k), acc[g]);
+    }
+    // the other buffer is written next; this one is only read again after
+    // the following iteration's barrier
+  }
+  // acc[g][i] = y[token t0 + 16 g + (lane & 15)][row r0 + 16 wave + 4 (lane >> 4) + i]
+  float* out = y + (size_t)blockIdx.z * (size_t)T * (size_t)ldy;
+  const int rb = r0 + wave * 16 + 4 * kq;
+#pragma unroll
+  for (int g = 0; g < GM_TT / 16; ++g) {
+    const int t = t0 + g * 16 + (lane & 15);
+    if (t >= T) continue;
+    float* o = out + (int64_t)t * ldy + rb;
+    if (rb + 3 < R && ((((uintptr_t)o) & 15) == 0)) {
+      *(float4*)o = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (rb + i < R) o[i] = acc[g][i];
+    }
+  }
+}
+
+// y[t][r] = sum_s P[s][t][r] in split order
+__global__ __launch_bounds__(256) void k_gemm_packed_sum(const float* __restrict__ P, int ns,
+                                                         int T, int R, int64_t ldp,
+                                                         float* __restrict__ y, int64_t ldy) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)T * R) return;
+  const int t = (int)(idx / R), r = (int)(idx % R);
+  float v = 0.f;
+  for (int s = 0; s < ns; ++s) v += P[((int64_t)s * T + t) * ldp + r];
+  y[(int64_t)t * ldy + r] = v;
+}
+
+// Split of the block range: about 512 workgroups (two per CU of an
+// MI355X; a function of the shapes only, so the workspace size is known
+// without a device), at least 8 blocks per split.
+constexpr int GM_TARGET_WG = 512;
+static inline int gemm_packed_splits(int64_t R, int64_t C, int64_t T, int* bps) {
+  const int64_t nblk = (C + PB - 1) / PB;
+  const int64_t tt = gemm_packed_tt(T);
+  const int64_t tiles = ((R + GM_ROWS - 1) / GM_ROWS) * ((T + tt - 1) / tt);
+  int64_t ns = (GM_TARGET_WG + tiles - 1) / tiles;
+  ns = std::max<int64_t>(1, std::min<int64_t>(ns, nblk / 8));
+  const int64_t per = (nblk + ns - 1) / ns;
+  *bps = (int)per;
+  return (int)((nblk + per - 1) / per);
+}
+
 }  // namespace crbq
 
 extern "C" int crbq_pack(const void* Q, int dtype, int64_t R, int64_t C, int64_t ldq,
@@ -326,5 +464,56 @@ extern "C" int crbq_gemv_packed(const uint8_t* codes, int64_t ldc, const void* l
         codes, ldc, (const uint16_t*)lut, sal, (int)R, (int)C, (int)nblk, (const uint16_t*)x,
         ldx, nvec, y, ldy);
   CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}
+
+extern "C" size_t crbq_gemm_packed_workspace_size(int64_t R, int64_t C, int64_t ntok) {
+  if (R <= 0 || C <= 0 || ntok <= 0) return 0;
+  int bps = 0;
+  const int ns = crbq::gemm_packed_splits(R, C, ntok, &bps);
+  return ns > 1 ? (size_t)ns * (size_t)ntok * (size_t)R * sizeof(float) : 0;
+}
+
+extern "C" int crbq_gemm_packed(const uint8_t* codes, int64_t ldc, const void* lut,
+                                const uint8_t* sal, int dtype, int64_t R, int64_t C,
+                                const void* x, int64_t ldx, int64_t ntok, float* y, int64_t ldy,
+                                void* ws, size_t ws_bytes, void* stream) {
+  if (!codes || !lut || !sal || !x || !y) return CRBQ_ERR_ARG;
+  if (dtype != CRBQ_F16 && dtype != CRBQ_BF16) return CRBQ_ERR_ARG;
+  if (R <= 0 || C <= 0 || ntok <= 0 || R > 0x7fffffff || C > 0x7fffffff || ntok > 0x7fffffff ||
+      ldx < C || ldy < R)
+    return CRBQ_ERR_ARG;
+  const int64_t nblk = (C + crbq::PB - 1) / crbq::PB;
+  if (ldc < nblk * 32 || (ldc & 7) || (ldx & 7) || (((uintptr_t)x) & 15) ||
+      (((uintptr_t)lut) & 15) || (((uintptr_t)codes) & 7) || (((uintptr_t)sal) & 3))
+    return CRBQ_ERR_ARG;
+  int bps = 0;
+  const int ns = crbq::gemm_packed_splits(R, C, ntok, &bps);
+  const size_t need = ns > 1 ? (size_t)ns * (size_t)ntok * (size_t)R * sizeof(float) : 0;
+  if (need && (!ws || ws_bytes < need)) return CRBQ_ERR_WORKSPACE;
+  float* out = ns > 1 ? (float*)ws : y;
+  const int64_t ldo = ns > 1 ? R : ldy;
+  const int tt = crbq::gemm_packed_tt(ntok);
+  dim3 grid((unsigned)((R + crbq::GM_ROWS - 1) / crbq::GM_ROWS),
+            (unsigned)((ntok + tt - 1) / tt), (unsigned)ns);
+  if (grid.y > 65535) return CRBQ_ERR_ARG;
+  hipStream_t s = (hipStream_t)stream;
+#define CRBQ_GM_LAUNCH(T8, TT)                                                                  \
+  crbq::k_gemm_packed<T8, TT><<<grid, 64 * crbq::GM_WAVES, 0, s>>>(                             \
+      codes, ldc, (const uint16_t*)lut, sal, (int)R, (int)C, (int)nblk, (const uint16_t*)x,     \
+      ldx, (int)ntok, bps, out, ldo)
+  if (dtype == CRBQ_BF16) {
+    if (tt == 128) CRBQ_GM_LAUNCH(b8_t, 128); else CRBQ_GM_LAUNCH(b8_t, 64);
+  } else {
+    if (tt == 128) CRBQ_GM_LAUNCH(h8_t, 128); else CRBQ_GM_LAUNCH(h8_t, 64);
+  }
+#undef CRBQ_GM_LAUNCH
+  CRBQ_LAUNCH_CHECK();
+  if (ns > 1) {
+    const int64_t n = ntok * R;
+    crbq::k_gemm_packed_sum<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+        out, ns, (int)ntok, (int)R, R, y, ldy);
+    CRBQ_LAUNCH_CHECK();
+  }
   return CRBQ_OK;
 }

@@ -300,3 +300,33 @@ def gemv_packed(codes: torch.Tensor, lut: torch.Tensor, sal: torch.Tensor, C: in
                                x.stride(0), nvec, y.data_ptr(), y.stride(0), stream_of(y)),
           "crbq_gemv_packed")
     return y
+
+
+def gemm_packed(codes: torch.Tensor, lut: torch.Tensor, sal: torch.Tensor, C: int,
+                x: torch.Tensor) -> torch.Tensor:
+    """Y [T, R] (fp32) = x [T, C] @ W^T for the packed W, any T >= 1."""
+    _dev_check(codes, lut, sal, x)
+    if x.dim() == 1:
+        x = x.unsqueeze(0)
+    if x.dtype != lut.dtype:
+        x = x.to(lut.dtype)
+    T = x.shape[0]
+    if T < 1 or x.shape[1] != C:
+        raise _lib.CrbqError("gemm_packed takes [T, C] activations of the weight's width")
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+        if C % 8:
+            xp = torch.zeros((T, (C + 7) // 8 * 8), dtype=x.dtype, device=x.device)
+            xp[:, :C] = x
+            x = xp
+    R = codes.shape[0]
+    y = torch.empty((T, R), dtype=torch.float32, device=x.device)
+    lib = _lib.ready(x.device)
+    nws = int(lib.crbq_gemm_packed_workspace_size(R, C, T))
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
+    check(lib.crbq_gemm_packed(codes.data_ptr(), codes.stride(0), lut.data_ptr(),
+                               sal.data_ptr(), _lib.DTYPES[lut.dtype], R, C, x.data_ptr(),
+                               x.stride(0), T, y.data_ptr(), y.stride(0), ws.data_ptr(), nws,
+                               stream_of(y)),
+          "crbq_gemm_packed")
+    return y

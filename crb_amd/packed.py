@@ -5,7 +5,11 @@ The reference stores a quantized layer as fake-quantized fp16/bf16 weights
 3 bits each (2-bit codes, an 8-entry value table per 128-column block
 row, one salient-column bitmap per block; the format is described in
 include/crbq.h) and multiplies with them directly: up to 16 tokens per call
-through the packed GEMV (MFMA on weights decoded in registers), more by unpacking into a temporary dense weight.
+through the packed GEMV (MFMA on weights decoded in registers), up to 768
+through the packed GEMM (each decoded fragment reused for 64 or 128 tokens),
+and larger batches, where the product is compute-bound, by unpacking into a
+temporary dense weight for the dense GEMM.  The limits are the measured
+crossovers on MI355X (4096 x 16384 and 16384 x 4096 fp16 layers).
 """
 from __future__ import annotations
 
@@ -16,6 +20,7 @@ import torch.nn.functional as F
 from . import kernels
 
 GEMV_MAX_TOKENS = 16
+GEMM_MAX_TOKENS = 768
 
 
 class PackedLinear(nn.Module):
@@ -44,8 +49,9 @@ class PackedLinear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shape = x.shape
         x2 = x.reshape(-1, self.in_features)
-        if x2.shape[0] <= GEMV_MAX_TOKENS:
-            y = kernels.gemv_packed(self.codes, self.lut, self.sal, self.in_features, x2)
+        if x2.shape[0] <= GEMM_MAX_TOKENS:
+            mm = kernels.gemv_packed if x2.shape[0] <= GEMV_MAX_TOKENS else kernels.gemm_packed
+            y = mm(self.codes, self.lut, self.sal, self.in_features, x2)
             y = y.to(x.dtype)
             if self.bias is not None:
                 y = y + self.bias

@@ -219,6 +219,19 @@ int crbq_gemv_packed(const uint8_t* codes, int64_t ldc, const void* lut,
                      const uint8_t* sal, int dtype, int64_t R, int64_t C,
                      const void* x, int64_t ldx, int nvec, float* y, int64_t ldy,
                      void* stream);
+/* crbq_gemm_packed: Y[t][r] = sum_c W[r][c] X[t][c] for ntok tokens (any
+ * count; meant for prefill batches above the GEMV's 16), X in the weights'
+ * dtype (ldx multiple of 8, 16-byte aligned), fp32 Y [ntok][ldy].  Each
+ * decoded weight fragment is reused for 64 tokens (128 above 64).  When the
+ * shapes give fewer than about 512 row x token tiles the column blocks are split over
+ * workgroups whose fp32 partials go to the workspace and are summed in
+ * split order (deterministic); crbq_gemm_packed_workspace_size(R, C, ntok)
+ * bytes (0 when there is no split) depend on the shapes only. */
+size_t crbq_gemm_packed_workspace_size(int64_t R, int64_t C, int64_t ntok);
+int crbq_gemm_packed(const uint8_t* codes, int64_t ldc, const void* lut,
+                     const uint8_t* sal, int dtype, int64_t R, int64_t C,
+                     const void* x, int64_t ldx, int64_t ntok, float* y, int64_t ldy,
+                     void* ws, size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

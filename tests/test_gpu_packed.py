@@ -109,6 +109,57 @@ def test_gemv_against_float64(R, C, dtype, nvec):
     assert (err <= 1e-5 * scale + 1e-30).all(), float((err / scale.clamp_min(1e-30)).max())
 
 
+@pytest.mark.parametrize("R,C,T,dtype", [(37, 300, 17, torch.float16),      # ragged everything
+                                          (256, 1024, 64, torch.bfloat16),
+                                          (130, 640, 100, torch.float16),
+                                          (1000, 4096, 33, torch.bfloat16),   # split K
+                                          (300, 2048, 250, torch.float16),
+                                          (64, 128, 1, torch.float16)])
+def test_gemm_against_float64(R, C, T, dtype):
+    """crbq_gemm_packed against float64 products of the unpacked weights,
+    same bar as the GEMV; the split-K and single-pass launches are both
+    covered (the split depends on R x T tiles)."""
+    print(f"gemm {R}x{C} T={T} {dtype}", flush=True)
+    from crb_amd import _lib
+    q, masks = structured(R, C, seed=5 * R + C)
+    if dtype == torch.bfloat16:
+        Q = torch.from_numpy(q.view(np.uint16).astype(np.int16)).view(torch.bfloat16).to(DEV)
+    else:
+        Q = torch.from_numpy(q).to(DEV)
+    codes, lut, sal = _k().pack(Q, torch.from_numpy(masks).to(DEV))
+    g = torch.Generator().manual_seed(T)
+    x = torch.randn(T, C + 40, generator=g).to(dtype).to(DEV)[:, :C]
+    y = _k().gemm_packed(codes, lut, sal, C, x)
+    torch.cuda.synchronize()
+    W64 = Q.double().cpu()
+    x64 = x.double().cpu()
+    ref = x64 @ W64.t()
+    scale = x64.abs() @ W64.abs().t()
+    err = (y.double().cpu() - ref).abs()
+    assert (err <= 1e-5 * scale + 1e-30).all(), float((err / scale.clamp_min(1e-30)).max())
+    # the header's rule: split when ~512 workgroups need it and >= 8 blocks per split
+    tiles = -(-R // 128) * -(-T // (128 if T > 64 else 64))
+    split = min(-(-512 // tiles), -(-C // 128) // 8) > 1
+    lib = _lib.load()
+    assert (lib.crbq_gemm_packed_workspace_size(R, C, T) > 0) == split
+
+
+def test_gemm_deterministic_and_matches_gemv():
+    """Split-K partials are summed in a fixed order: repeated calls are
+    bitwise equal; the first 16 tokens agree with the GEMV to the same bar."""
+    print("gemm determinism", flush=True)
+    q, masks = structured(1000, 4096, seed=9)
+    Q = torch.from_numpy(q).to(DEV)
+    codes, lut, sal = _k().pack(Q, torch.from_numpy(masks).to(DEV))
+    x = torch.randn(40, 4096, generator=torch.Generator().manual_seed(2)).half().to(DEV)
+    y1 = _k().gemm_packed(codes, lut, sal, 4096, x)
+    y2 = _k().gemm_packed(codes, lut, sal, 4096, x)
+    assert torch.equal(y1, y2)
+    yv = _k().gemv_packed(codes, lut, sal, 4096, x[:16])
+    scale = x[:16].double().abs() @ Q.double().abs().t()
+    assert ((y1[:16].double() - yv.double()).abs() <= 2e-5 * scale + 1e-30).all()
+
+
 def test_packed_linear_forward():
     print("packed linear", flush=True)
     from crb_amd.packed import PackedLinear
@@ -119,7 +170,7 @@ def test_packed_linear_forward():
     assert torch.equal(pl.weight(), lin.weight.data)
     assert pl.packed_bytes() * 8 / (192 * 512) < 3.1
     g = torch.Generator().manual_seed(0)
-    for ntok in (1, 8, 40):                # 2 and 16 tokens: GEMV; 80: unpack
+    for ntok in (1, 8, 40, 400):           # 2, 16: GEMV; 80: GEMM; 800: unpack + dense
         x = torch.randn(2, ntok, 512, generator=g).half().to(DEV)
         with torch.no_grad():
             got = pl(x).float()
