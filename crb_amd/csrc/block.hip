@@ -47,6 +47,13 @@ constexpr int H1_BITS = 12, H2_BITS = 10, H3_BITS = 10;   // 12 + 10 + 10 = 32
 constexpr int H1 = 1 << H1_BITS, H2 = 1 << H2_BITS, H3 = 1 << H3_BITS;
 constexpr int SH1 = H2_BITS + H3_BITS, SH2 = H3_BITS;     // key = b1<<SH1 | b2<<SH2 | b3
 constexpr int NONE = 0x7fffffff;
+// The level-2 histogram of the radix select, the one most elements reach,
+// is kept once per XCD: a workgroup adds into the copy of the XCD it runs
+// on (hardware register XCC_ID) with workgroup-scope atomics, which
+// complete in that XCD's L2 instead of travelling to memory as device-scope
+// atomics do; the level-2 scan sums the copies.  Kernel boundaries write
+// the L2s back, so the next launch sees every copy.
+constexpr int NXCD = 8;
 
 // torch.linspace(0.10, 0.90, 81) on the CPU (utils/autosearch.py:65), float32.
 __constant__ float c_q[NQ];
@@ -79,7 +86,7 @@ struct SearchWs {
   int* slot1map;     // [H1]
   Tgt* tgt;          // [NT]
   float* gam;        // [NQ]
-  uint32_t* hist2;   // [NT][H2]
+  uint32_t* hist2;   // [NXCD][NT][H2]
   int* slot2map;     // [NT][H2]
   uint32_t* hist3;   // [NT][H3]
   float* tval;       // [NT]
@@ -98,11 +105,17 @@ static void carve_search(WsCarver& c, int64_t R, SearchWs& s) {
   s.slot1map = c.take<int>(H1);
   s.tgt = c.take<Tgt>(NT);
   s.gam = c.take<float>(NQ);
-  s.hist2 = c.take<uint32_t>((size_t)NT * H2);
+  s.hist2 = c.take<uint32_t>((size_t)NXCD * NT * H2);
   s.slot2map = c.take<int>((size_t)NT * H2);
   s.hist3 = c.take<uint32_t>((size_t)NT * H3);
   s.tval = c.take<float>(NT);
   s.pvals = c.take<float>(NQ);
+}
+
+__device__ __forceinline__ int xcd_id() {
+  int x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x & (NXCD - 1);
 }
 
 // Salient-search target T (utils/structure.py:9-12).
@@ -192,10 +205,8 @@ __global__ __launch_bounds__(CS_THREADS) void k_colscore(
   part[ph][col] = acc;
   // zero the histograms used later by this block (grid-stride)
   const size_t gsz = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)NT * H2; i += gsz) {
-    s.hist2[i] = 0u;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)NT * H3; i += gsz)
     s.hist3[i] = 0u;
-  }
   for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)H1; i += gsz) s.hist1[i] = 0u;
   __syncthreads();
   if (ph == 0) {
@@ -461,6 +472,13 @@ __global__ __launch_bounds__(256) void k_qpass1(
     const float v = fabsf(target_of(W[(int64_t)r * ldw + c], d2s[c], metric));
     atomicAdd(&lh[__float_as_uint(v) >> SH1], 1u);
   }
+  // zero the level-2 copies for k_qpass2 (16-byte stores, grid-stride)
+  {
+    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+    uint4* h2 = (uint4*)s.hist2;
+    const size_t n4 = (size_t)NXCD * NT * H2 / 4, gsz = (size_t)gridDim.x * 256;
+    for (size_t i = (size_t)blockIdx.x * 256 + tid; i < n4; i += gsz) h2[i] = z;
+  }
   __syncthreads();
   for (int i = tid; i < H1; i += 256)
     if (lh[i]) atomicAdd(&s.hist1[i], lh[i]);
@@ -472,15 +490,22 @@ __global__ __launch_bounds__(256) void k_qpass1(
 }
 
 // Block-wide exclusive scan of H (multiple of 256) counters in LDS.
-template <int H>
+// The counters are the sums of NC copies `cstride` apart.
+template <int H, int NC = 1>
 __device__ void block_scan(const uint32_t* __restrict__ src, uint32_t* cum,
-                           uint32_t* tmp /* 256 */) {
+                           uint32_t* tmp /* 256 */, size_t cstride = 0) {
   constexpr int PER = H / 256;
   const int tid = threadIdx.x;
   uint32_t loc[PER];
   uint32_t sum = 0;
 #pragma unroll
-  for (int k = 0; k < PER; ++k) { loc[k] = src[tid * PER + k]; sum += loc[k]; }
+  for (int k = 0; k < PER; ++k) loc[k] = src[tid * PER + k];
+#pragma unroll
+  for (int x = 1; x < NC; ++x)
+#pragma unroll
+    for (int k = 0; k < PER; ++k) loc[k] += src[x * cstride + tid * PER + k];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) sum += loc[k];
   tmp[tid] = sum;
   __syncthreads();
   for (int o = 1; o < 256; o <<= 1) {
@@ -561,6 +586,7 @@ __global__ __launch_bounds__(256) void k_qpass2(
   for (size_t i = (size_t)blockIdx.x * 256 + tid; i < (size_t)NT * H2; i += gsz)
     s.slot2map[i] = NONE;
   __syncthreads();
+  uint32_t* h2 = s.hist2 + (size_t)xcd_id() * NT * H2;
   const int r0 = blockIdx.x * Q_RPW, r1 = min(R, r0 + Q_RPW);
   for (int i = tid; i < (r1 - r0) * nc; i += 256) {
     const int r = r0 + i / nc, c = i % nc;
@@ -568,12 +594,16 @@ __global__ __launch_bounds__(256) void k_qpass2(
     const float v = fabsf(target_of(W[(int64_t)r * ldw + c], d2s[c], metric));
     const uint32_t key = __float_as_uint(v);
     const int sl = sm[key >> SH1];
-    if (sl >= 0) atomicAdd(&s.hist2[(size_t)sl * H2 + ((key >> SH2) & (H2 - 1))], 1u);
+    if (sl >= 0)
+      __hip_atomic_fetch_add(&h2[(size_t)sl * H2 + ((key >> SH2) & (H2 - 1))], 1u,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   if (blockIdx.x == 0 && tid == 0 && sm[0] >= 0) {
     int nsal = 0;
     for (int c = 0; c < nc; ++c) nsal += rk[c] < istar;
-    if (nsal) atomicAdd(&s.hist2[(size_t)sm[0] * H2], (uint32_t)R * (uint32_t)nsal);
+    if (nsal)
+      __hip_atomic_fetch_add(&h2[(size_t)sm[0] * H2], (uint32_t)R * (uint32_t)nsal,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 }
 
@@ -583,7 +613,7 @@ __global__ __launch_bounds__(256) void k_qscan2(SearchWs s) {
   __shared__ uint32_t tmp[256];
   const int t = blockIdx.x;
   const int sl = s.tgt[t].slot1;
-  block_scan<H2>(s.hist2 + (size_t)sl * H2, cum, tmp);
+  block_scan<H2, NXCD>(s.hist2 + (size_t)sl * H2, cum, tmp, (size_t)NT * H2);
   if (threadIdx.x == 0) {
     Tgt& g = s.tgt[t];
     const int b = find_bin<H2>(cum, (uint32_t)g.r1);
