@@ -84,13 +84,14 @@ _SIGS = {
     "crbq_sgemm": (c_i32, [c_i32, c_i32, c_i64, c_i64, c_i64, ctypes.c_float, c_vp, c_i64,
                            c_vp, c_i64, ctypes.c_float, c_vp, c_i64, c_vp]),
     "crbq_pack": (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,
-                          c_vp, c_vp, c_vp]),
-    "crbq_unpack": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64, c_vp]),
-    "crbq_gemv_packed": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64,
-                                 c_i32, c_vp, c_i64, c_vp]),
+                          c_vp, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp]),
+    "crbq_unpack": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i64, c_i64,
+                            c_vp, c_i64, c_vp]),
+    "crbq_gemv_packed": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i64,
+                                 c_i64, c_vp, c_i64, c_i32, c_vp, c_i64, c_vp]),
     "crbq_gemm_packed_workspace_size": (c_size, [c_i64, c_i64, c_i64]),
-    "crbq_gemm_packed": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_i32, c_i64, c_i64, c_vp, c_i64,
-                                 c_i64, c_vp, c_i64, c_vp, c_size, c_vp]),
+    "crbq_gemm_packed": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i64,
+                                 c_i64, c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_size, c_vp]),
 }
 
 _lock = threading.Lock()

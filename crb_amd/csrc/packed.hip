@@ -43,15 +43,34 @@ __device__ __forceinline__ int wave_or_i(int v) {
   return v;
 }
 
-__global__ void k_zero_status(int* status) { *status = 0; }
+__global__ void k_zero_status(int* status, int* ex_count) {
+  *status = 0;
+  *ex_count = 0;
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t u, bool bf16) {
+  return bf16 ? __uint_as_float(u << 16)
+              : (float)__builtin_bit_cast(_Float16, (unsigned short)(u & 0xffffu));
+}
+
+constexpr int NDV = 8;    // distinct values a group's table is chosen from
 
 // One wavefront per (row, block); lane l holds elements l and 64 + l.
+// Per group (mask 1 and 2: 2 table entries, mask 3: 4) the table keeps the
+// most frequent values among the group's NDV smallest distinct values (ties
+// to the smaller key), in ascending order; every other element is an
+// exception: code = the group's first entry, and (flat index r * C + c, raw
+// value, value - first entry in fp32) appended to the exception list.
 __global__ __launch_bounds__(256) void k_pack(const uint16_t* __restrict__ Q, int64_t ldq,
                                               const uint8_t* __restrict__ M, int64_t ldm,
-                                              int R, int C, int nblk,
+                                              int R, int C, int nblk, bool bf16,
                                               uint8_t* __restrict__ codes, int64_t ldc,
                                               uint16_t* __restrict__ lut,
-                                              uint8_t* __restrict__ sal, int* status) {
+                                              uint8_t* __restrict__ sal,
+                                              int64_t* __restrict__ ex_idx,
+                                              uint16_t* __restrict__ ex_val,
+                                              float* __restrict__ ex_delta, int ex_cap,
+                                              int* ex_count, int* status) {
   const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w >= (int64_t)R * nblk) return;   // whole wavefronts
   const int r = (int)(w / nblk), b = (int)(w % nblk), lane = threadIdx.x & 63;
@@ -72,37 +91,72 @@ __global__ __launch_bounds__(256) void k_pack(const uint16_t* __restrict__ Q, in
   for (int s = 0; s < 2; ++s)
     if (inside[s] && (grp[s] < 1 || grp[s] > 3)) err |= 4;
   int code[2] = {0, 0};
+  bool exc[2] = {false, false};
   uint32_t lv[8];
 #pragma unroll
   for (int G = 1; G <= 3; ++G) {
     const int cap = G == 3 ? 4 : 2, base = G == 1 ? 0 : (G == 2 ? 2 : 4);
-    int keys[4], found = 0, prev = -1;
+    // the group's NDV smallest distinct keys and their counts (uniform)
+    int cand[NDV], cnt[NDV], nd = 0, prev = -1;
 #pragma unroll
-    for (int k = 0; k < cap; ++k) {
-      int cand = 0x10000;
+    for (int k = 0; k < NDV; ++k) {
+      int m = 0x10000;
 #pragma unroll
       for (int s = 0; s < 2; ++s)
-        if (grp[s] == G && key[s] > prev) cand = min(cand, key[s]);
-      cand = wave_min_i(cand);
-      keys[k] = cand;
-      if (cand < 0x10000) {
-        found = k + 1;
-        prev = cand;
+        if (grp[s] == G && key[s] > prev) m = min(m, key[s]);
+      m = wave_min_i(m);
+      cand[k] = m;
+      cnt[k] = 0;
+      if (m < 0x10000) {
+        cnt[k] = __popcll(__ballot(grp[0] == G && key[0] == m)) +
+                 __popcll(__ballot(grp[1] == G && key[1] == m));
+        nd = k + 1;
+        prev = m;
       }
     }
+    // keep the cap most frequent (ties: smaller key), in ascending key order
+    bool keep[NDV];
+#pragma unroll
+    for (int k = 0; k < NDV; ++k) {
+      int better = 0;
+#pragma unroll
+      for (int q = 0; q < NDV; ++q)
+        better += (q < nd && (cnt[q] > cnt[k] || (cnt[q] == cnt[k] && q < k))) ? 1 : 0;
+      keep[k] = k < nd && better < cap;
+    }
+    int keys[4], found = 0;
+#pragma unroll
+    for (int k = 0; k < NDV; ++k)
+      if (keep[k] && found < 4) keys[found++] = cand[k];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       if (grp[s] != G) continue;
       int rk = -1;
 #pragma unroll
-      for (int k = 0; k < cap; ++k)
+      for (int k = 0; k < 4; ++k)
         if (k < found && keys[k] == key[s]) rk = k;
-      if (rk < 0) err |= 1;                      // more distinct values than codes
-      else code[s] = (G == 2 ? 2 : 0) + rk;
+      exc[s] = rk < 0;
+      code[s] = (G == 2 ? 2 : 0) + (rk < 0 ? 0 : rk);
     }
 #pragma unroll
     for (int k = 0; k < cap; ++k)
       lv[base + k] = found ? unkey16(keys[k < found ? k : found - 1]) : 0u;
+  }
+  // exceptions (rare): append to the list
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (!exc[s]) continue;
+    const int c = b * PB + s * 64 + lane;
+    const uint32_t v = unkey16(key[s]);
+    const uint32_t t = lv[(grp[s] == 3 ? 4 : 0) + code[s]];
+    const int e = atomicAdd(ex_count, 1);
+    if (e < ex_cap) {
+      ex_idx[e] = (int64_t)r * C + c;
+      ex_val[e] = (uint16_t)v;
+      ex_delta[e] = half_bits_to_float(v, bf16) - half_bits_to_float(t, bf16);
+    } else {
+      err |= 1;
+    }
   }
   err = wave_or_i(err);
   if (lane == 0 && err) atomicOr(status, err);
@@ -146,6 +200,36 @@ __global__ __launch_bounds__(256) void k_unpack(const uint8_t* __restrict__ code
   for (int i = 0; i < 4; ++i) {
     const int c = b * PB + 4 * t + i;
     if (c < C) Q[(int64_t)r * ldq + c] = L[4 * ((sb >> i) & 1) + ((cb >> (2 * i)) & 3)];
+  }
+}
+
+// Exceptions of the packed form: the exact values over the unpacked ones.
+__global__ __launch_bounds__(256) void k_unpack_ex(const int64_t* __restrict__ ex_idx,
+                                                   const uint16_t* __restrict__ ex_val,
+                                                   int64_t n_ex, int C, int64_t n,
+                                                   uint16_t* __restrict__ Q, int64_t ldq) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= n_ex) return;
+  const int64_t i = ex_idx[e];
+  if (i < 0 || i >= n) return;           // indices outside R x C are ignored
+  Q[(i / C) * ldq + i % C] = ex_val[e];
+}
+
+// y[t][r] += delta_e * x[t][c] for every exception e = (r, c), one thread
+// per token, exceptions in list order (deterministic for a given list).
+__global__ __launch_bounds__(256) void k_apply_ex(const int64_t* __restrict__ ex_idx,
+                                                  const float* __restrict__ ex_delta,
+                                                  int64_t n_ex, int C, int64_t n,
+                                                  const uint16_t* __restrict__ x, int64_t ldx,
+                                                  bool bf16, int T, float* __restrict__ y,
+                                                  int64_t ldy) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= T) return;
+  for (int64_t e = 0; e < n_ex; ++e) {
+    const int64_t i = ex_idx[e];
+    if (i < 0 || i >= n) continue;       // indices outside R x C are ignored
+    const int r = (int)(i / C), c = (int)(i % C);
+    y[(int64_t)t * ldy + r] += ex_delta[e] * half_bits_to_float(x[(int64_t)t * ldx + c], bf16);
   }
 }
 
@@ -407,8 +491,11 @@ static inline int gemm_packed_splits(int64_t R, int64_t C, int64_t T, int* bps) 
 
 extern "C" int crbq_pack(const void* Q, int dtype, int64_t R, int64_t C, int64_t ldq,
                          const uint8_t* masks, int64_t ldm, uint8_t* codes, int64_t ldc,
-                         void* lut, uint8_t* sal, int* status, void* stream) {
-  if (!Q || !masks || !codes || !lut || !sal || !status) return CRBQ_ERR_ARG;
+                         void* lut, uint8_t* sal, int64_t* ex_idx, void* ex_val,
+                         float* ex_delta, int ex_cap, int* ex_count, int* status,
+                         void* stream) {
+  if (!Q || !masks || !codes || !lut || !sal || !status || !ex_count) return CRBQ_ERR_ARG;
+  if (ex_cap < 0 || (ex_cap > 0 && (!ex_idx || !ex_val || !ex_delta))) return CRBQ_ERR_ARG;
   if (dtype != CRBQ_F16 && dtype != CRBQ_BF16) return CRBQ_ERR_ARG;
   if (R <= 0 || C <= 0 || R > 0x7fffffff || C > 0x7fffffff || ldq < C || ldm < C)
     return CRBQ_ERR_ARG;
@@ -417,35 +504,56 @@ extern "C" int crbq_pack(const void* Q, int dtype, int64_t R, int64_t C, int64_t
       (((uintptr_t)codes) & 7))
     return CRBQ_ERR_ARG;
   hipStream_t s = (hipStream_t)stream;
-  crbq::k_zero_status<<<1, 1, 0, s>>>(status);
+  crbq::k_zero_status<<<1, 1, 0, s>>>(status, ex_count);
   CRBQ_LAUNCH_CHECK();
   const int64_t waves = R * nblk;
   crbq::k_pack<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(
-      (const uint16_t*)Q, ldq, masks, ldm, (int)R, (int)C, (int)nblk, codes, ldc,
-      (uint16_t*)lut, sal, status);
+      (const uint16_t*)Q, ldq, masks, ldm, (int)R, (int)C, (int)nblk, dtype == CRBQ_BF16, codes,
+      ldc, (uint16_t*)lut, sal, ex_idx, (uint16_t*)ex_val, ex_delta, ex_cap, ex_count, status);
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }
 
 extern "C" int crbq_unpack(const uint8_t* codes, int64_t ldc, const void* lut, const uint8_t* sal,
-                           int dtype, int64_t R, int64_t C, void* Q, int64_t ldq, void* stream) {
+                           const int64_t* ex_idx, const void* ex_val, int64_t n_ex, int dtype,
+                           int64_t R, int64_t C, void* Q, int64_t ldq, void* stream) {
   if (!codes || !lut || !sal || !Q) return CRBQ_ERR_ARG;
+  if (n_ex < 0 || (n_ex > 0 && (!ex_idx || !ex_val))) return CRBQ_ERR_ARG;
   if (dtype != CRBQ_F16 && dtype != CRBQ_BF16) return CRBQ_ERR_ARG;
   if (R <= 0 || C <= 0 || R > 0x7fffffff || C > 0x7fffffff || ldq < C) return CRBQ_ERR_ARG;
   const int64_t nblk = (C + crbq::PB - 1) / crbq::PB;
   if (ldc < nblk * 32) return CRBQ_ERR_ARG;
   const int64_t n = R * nblk * 32;
-  crbq::k_unpack<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+  hipStream_t s = (hipStream_t)stream;
+  crbq::k_unpack<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
       codes, ldc, (const uint16_t*)lut, sal, (int)R, (int)C, (int)nblk, (uint16_t*)Q, ldq);
+  CRBQ_LAUNCH_CHECK();
+  if (n_ex > 0) {
+    crbq::k_unpack_ex<<<(unsigned)((n_ex + 255) / 256), 256, 0, s>>>(
+        ex_idx, (const uint16_t*)ex_val, n_ex, (int)C, R * C, (uint16_t*)Q, ldq);
+    CRBQ_LAUNCH_CHECK();
+  }
+  return CRBQ_OK;
+}
+
+static int apply_ex(const int64_t* ex_idx, const float* ex_delta, int64_t n_ex, int64_t R,
+                    int64_t C, const void* x, int64_t ldx, int dtype, int64_t T, float* y,
+                    int64_t ldy, hipStream_t s) {
+  if (n_ex <= 0) return CRBQ_OK;
+  crbq::k_apply_ex<<<(unsigned)((T + 255) / 256), 256, 0, s>>>(
+      ex_idx, ex_delta, n_ex, (int)C, R * C, (const uint16_t*)x, ldx, dtype == CRBQ_BF16,
+      (int)T, y, ldy);
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }
 
 extern "C" int crbq_gemv_packed(const uint8_t* codes, int64_t ldc, const void* lut,
-                                const uint8_t* sal, int dtype, int64_t R, int64_t C,
-                                const void* x, int64_t ldx, int nvec, float* y, int64_t ldy,
-                                void* stream) {
+                                const uint8_t* sal, const int64_t* ex_idx,
+                                const float* ex_delta, int64_t n_ex, int dtype, int64_t R,
+                                int64_t C, const void* x, int64_t ldx, int nvec, float* y,
+                                int64_t ldy, void* stream) {
   if (!codes || !lut || !sal || !x || !y) return CRBQ_ERR_ARG;
+  if (n_ex < 0 || (n_ex > 0 && (!ex_idx || !ex_delta))) return CRBQ_ERR_ARG;
   if (dtype != CRBQ_F16 && dtype != CRBQ_BF16) return CRBQ_ERR_ARG;
   if (R <= 0 || C <= 0 || R > 0x7fffffff || C > 0x7fffffff) return CRBQ_ERR_ARG;
   if (nvec < 1 || nvec > crbq::GV_MAXVEC || ldx < C || ldy < R) return CRBQ_ERR_ARG;
@@ -464,7 +572,7 @@ extern "C" int crbq_gemv_packed(const uint8_t* codes, int64_t ldc, const void* l
         codes, ldc, (const uint16_t*)lut, sal, (int)R, (int)C, (int)nblk, (const uint16_t*)x,
         ldx, nvec, y, ldy);
   CRBQ_LAUNCH_CHECK();
-  return CRBQ_OK;
+  return apply_ex(ex_idx, ex_delta, n_ex, R, C, x, ldx, dtype, nvec, y, ldy, s);
 }
 
 extern "C" size_t crbq_gemm_packed_workspace_size(int64_t R, int64_t C, int64_t ntok) {
@@ -475,10 +583,12 @@ extern "C" size_t crbq_gemm_packed_workspace_size(int64_t R, int64_t C, int64_t 
 }
 
 extern "C" int crbq_gemm_packed(const uint8_t* codes, int64_t ldc, const void* lut,
-                                const uint8_t* sal, int dtype, int64_t R, int64_t C,
-                                const void* x, int64_t ldx, int64_t ntok, float* y, int64_t ldy,
-                                void* ws, size_t ws_bytes, void* stream) {
+                                const uint8_t* sal, const int64_t* ex_idx,
+                                const float* ex_delta, int64_t n_ex, int dtype, int64_t R,
+                                int64_t C, const void* x, int64_t ldx, int64_t ntok, float* y,
+                                int64_t ldy, void* ws, size_t ws_bytes, void* stream) {
   if (!codes || !lut || !sal || !x || !y) return CRBQ_ERR_ARG;
+  if (n_ex < 0 || (n_ex > 0 && (!ex_idx || !ex_delta))) return CRBQ_ERR_ARG;
   if (dtype != CRBQ_F16 && dtype != CRBQ_BF16) return CRBQ_ERR_ARG;
   if (R <= 0 || C <= 0 || ntok <= 0 || R > 0x7fffffff || C > 0x7fffffff || ntok > 0x7fffffff ||
       ldx < C || ldy < R)
@@ -515,5 +625,5 @@ extern "C" int crbq_gemm_packed(const uint8_t* codes, int64_t ldc, const void* l
         out, ns, (int)ntok, (int)R, R, y, ldy);
     CRBQ_LAUNCH_CHECK();
   }
-  return CRBQ_OK;
+  return apply_ex(ex_idx, ex_delta, n_ex, R, C, x, ldx, dtype, ntok, y, ldy, s);
 }

@@ -8,6 +8,8 @@ from __future__ import annotations
 
 import ctypes
 
+from typing import NamedTuple
+
 import torch
 
 from . import _lib
@@ -230,16 +232,31 @@ def sgemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, alpha: float = 1.0,
 
 # -- packed low-bit storage ---------------------------------------------------
 PACK_BLOCK = 128
-PACK_ERRORS = {1: "a group has more distinct values than its codes (blocksize not a "
-                  "multiple of 128, or weights not from the binarizer)",
+PACK_ERRORS = {1: "more out-of-table values than the exception list holds (weights not "
+                  "from the binarizer, or blocksize not a multiple of 128)",
                2: "salient columns differ between rows",
                4: "mask code outside 1..3"}
 
 
-def pack(Q: torch.Tensor, masks: torch.Tensor):
-    """Packed form (codes, lut, sal) of quantized fp16/bf16 weights Q [R, C]
-    with their mask codes (uint8 1/2/3).  Raises CrbqError if Q does not
-    have the per-block structure the format stores exactly."""
+class PackedEx(NamedTuple):
+    """Exceptions of a packed layer, sorted by flat index r * C + c."""
+    idx: torch.Tensor      # int64 [n]
+    val: torch.Tensor      # [n] in the weight dtype: the exact values
+    delta: torch.Tensor    # fp32 [n]: value - the table entry their code decodes to
+
+
+def _ex_args(ex, device, dtype):
+    if ex is None or ex.idx.numel() == 0:
+        return 0, 0, 0, 0
+    _dev_check(ex.idx, ex.val, ex.delta)
+    return ex.idx.data_ptr(), ex.val.data_ptr(), ex.delta.data_ptr(), int(ex.idx.numel())
+
+
+def pack(Q: torch.Tensor, masks: torch.Tensor, ex_cap: int | None = None):
+    """Packed form (codes, lut, sal, ex) of quantized fp16/bf16 weights
+    Q [R, C] with their mask codes (uint8 1/2/3).  Raises CrbqError if Q
+    does not have the per-block structure the format stores (beyond
+    ex_cap exceptions, by default one per 8 row-blocks and at least 1024)."""
     _dev_check(Q, masks)
     if Q.dtype not in (torch.float16, torch.bfloat16) or Q.dim() != 2 or Q.stride(1) != 1:
         raise _lib.CrbqError("pack takes a row-major fp16/bf16 [R, C] weight")
@@ -247,86 +264,97 @@ def pack(Q: torch.Tensor, masks: torch.Tensor):
         raise _lib.CrbqError("pack takes uint8 mask codes shaped like the weight")
     R, C = Q.shape
     nblk = (C + PACK_BLOCK - 1) // PACK_BLOCK
-    codes = torch.empty((R, nblk * 32), dtype=torch.uint8, device=Q.device)
-    lut = torch.empty((R, nblk, 8), dtype=Q.dtype, device=Q.device)
-    sal = torch.empty((nblk, 16), dtype=torch.uint8, device=Q.device)
-    status = torch.empty(1, dtype=torch.int32, device=Q.device)
-    lib = _lib.ready(Q.device)
+    cap = int(ex_cap) if ex_cap is not None else max(1024, R * nblk // 8)
+    dev = Q.device
+    codes = torch.empty((R, nblk * 32), dtype=torch.uint8, device=dev)
+    lut = torch.empty((R, nblk, 8), dtype=Q.dtype, device=dev)
+    sal = torch.empty((nblk, 16), dtype=torch.uint8, device=dev)
+    ex_idx = torch.empty(max(cap, 1), dtype=torch.int64, device=dev)
+    ex_val = torch.empty(max(cap, 1), dtype=Q.dtype, device=dev)
+    ex_delta = torch.empty(max(cap, 1), dtype=torch.float32, device=dev)
+    counters = torch.empty(2, dtype=torch.int32, device=dev)     # status, ex_count
+    lib = _lib.ready(dev)
     check(lib.crbq_pack(Q.data_ptr(), _lib.DTYPES[Q.dtype], R, C, Q.stride(0),
                         masks.data_ptr(), masks.stride(0), codes.data_ptr(), codes.stride(0),
-                        lut.data_ptr(), sal.data_ptr(), status.data_ptr(), stream_of(Q)),
+                        lut.data_ptr(), sal.data_ptr(), ex_idx.data_ptr(), ex_val.data_ptr(),
+                        ex_delta.data_ptr(), cap, counters[1:].data_ptr(),
+                        counters[:1].data_ptr(), stream_of(Q)),
           "crbq_pack")
-    st = int(status.item())
+    st, n = (int(v) for v in counters.tolist())
     if st:
         why = "; ".join(v for k, v in PACK_ERRORS.items() if st & k)
         raise _lib.CrbqError(f"crbq_pack: {why}")
-    return codes, lut, sal
+    order = torch.argsort(ex_idx[:n])
+    ex = PackedEx(ex_idx[:n][order].contiguous(), ex_val[:n][order].contiguous(),
+                  ex_delta[:n][order].contiguous())
+    return codes, lut, sal, ex
 
 
-def unpack(codes: torch.Tensor, lut: torch.Tensor, sal: torch.Tensor, C: int) -> torch.Tensor:
-    """The weights [R, C] (lut's dtype) a packed triple encodes."""
+def unpack(codes: torch.Tensor, lut: torch.Tensor, sal: torch.Tensor, C: int,
+           ex: PackedEx | None = None) -> torch.Tensor:
+    """The weights [R, C] (lut's dtype) a packed layer encodes."""
     _dev_check(codes, lut, sal)
     R = codes.shape[0]
     Q = torch.empty((R, C), dtype=lut.dtype, device=codes.device)
     lib = _lib.ready(codes.device)
+    ei, ev, _, n = _ex_args(ex, codes.device, lut.dtype)
     check(lib.crbq_unpack(codes.data_ptr(), codes.stride(0), lut.data_ptr(), sal.data_ptr(),
-                          _lib.DTYPES[lut.dtype], R, C, Q.data_ptr(), Q.stride(0),
+                          ei, ev, n, _lib.DTYPES[lut.dtype], R, C, Q.data_ptr(), Q.stride(0),
                           stream_of(Q)), "crbq_unpack")
     return Q
 
 
-def gemv_packed(codes: torch.Tensor, lut: torch.Tensor, sal: torch.Tensor, C: int,
-                x: torch.Tensor) -> torch.Tensor:
-    """y [nvec, R] (fp32) = x [nvec, C] @ W^T for the packed W, nvec <= 16."""
-    _dev_check(codes, lut, sal, x)
+def _packed_x(x, lut, C, what):
     if x.dim() == 1:
         x = x.unsqueeze(0)
     if x.dtype != lut.dtype:
         x = x.to(lut.dtype)
-    nvec = x.shape[0]
-    if not 1 <= nvec <= 16 or x.shape[1] != C:
-        raise _lib.CrbqError("gemv_packed takes 1..16 vectors of the weight's width")
+    if x.shape[0] < 1 or x.shape[1] != C:
+        raise _lib.CrbqError(f"{what} takes [T, C] activations of the weight's width")
     if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
         x = x.contiguous()
         if C % 8:
-            xp = torch.zeros((nvec, (C + 7) // 8 * 8), dtype=x.dtype, device=x.device)
+            xp = torch.zeros((x.shape[0], (C + 7) // 8 * 8), dtype=x.dtype, device=x.device)
             xp[:, :C] = x
             x = xp
+    return x
+
+
+def gemv_packed(codes: torch.Tensor, lut: torch.Tensor, sal: torch.Tensor, C: int,
+                x: torch.Tensor, ex: PackedEx | None = None) -> torch.Tensor:
+    """y [nvec, R] (fp32) = x [nvec, C] @ W^T for the packed W, nvec <= 16."""
+    _dev_check(codes, lut, sal, x)
+    x = _packed_x(x, lut, C, "gemv_packed")
+    nvec = x.shape[0]
+    if nvec > 16:
+        raise _lib.CrbqError("gemv_packed takes 1..16 vectors")
     R = codes.shape[0]
     y = torch.empty((nvec, R), dtype=torch.float32, device=x.device)
     lib = _lib.ready(x.device)
+    ei, _, ed, n = _ex_args(ex, x.device, lut.dtype)
     check(lib.crbq_gemv_packed(codes.data_ptr(), codes.stride(0), lut.data_ptr(),
-                               sal.data_ptr(), _lib.DTYPES[lut.dtype], R, C, x.data_ptr(),
-                               x.stride(0), nvec, y.data_ptr(), y.stride(0), stream_of(y)),
+                               sal.data_ptr(), ei, ed, n, _lib.DTYPES[lut.dtype], R, C,
+                               x.data_ptr(), x.stride(0), nvec, y.data_ptr(), y.stride(0),
+                               stream_of(y)),
           "crbq_gemv_packed")
     return y
 
 
 def gemm_packed(codes: torch.Tensor, lut: torch.Tensor, sal: torch.Tensor, C: int,
-                x: torch.Tensor) -> torch.Tensor:
+                x: torch.Tensor, ex: PackedEx | None = None) -> torch.Tensor:
     """Y [T, R] (fp32) = x [T, C] @ W^T for the packed W, any T >= 1."""
     _dev_check(codes, lut, sal, x)
-    if x.dim() == 1:
-        x = x.unsqueeze(0)
-    if x.dtype != lut.dtype:
-        x = x.to(lut.dtype)
+    x = _packed_x(x, lut, C, "gemm_packed")
     T = x.shape[0]
-    if T < 1 or x.shape[1] != C:
-        raise _lib.CrbqError("gemm_packed takes [T, C] activations of the weight's width")
-    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
-        x = x.contiguous()
-        if C % 8:
-            xp = torch.zeros((T, (C + 7) // 8 * 8), dtype=x.dtype, device=x.device)
-            xp[:, :C] = x
-            x = xp
     R = codes.shape[0]
     y = torch.empty((T, R), dtype=torch.float32, device=x.device)
     lib = _lib.ready(x.device)
     nws = int(lib.crbq_gemm_packed_workspace_size(R, C, T))
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=x.device)
+    ei, _, ed, n = _ex_args(ex, x.device, lut.dtype)
     check(lib.crbq_gemm_packed(codes.data_ptr(), codes.stride(0), lut.data_ptr(),
-                               sal.data_ptr(), _lib.DTYPES[lut.dtype], R, C, x.data_ptr(),
-                               x.stride(0), T, y.data_ptr(), y.stride(0), ws.data_ptr(), nws,
-                               stream_of(y)),
+                               sal.data_ptr(), ei, ed, n, _lib.DTYPES[lut.dtype], R, C,
+                               x.data_ptr(), x.stride(0), T, y.data_ptr(), y.stride(0),
+                               ws.data_ptr(), nws, stream_of(y)),
           "crbq_gemm_packed")
     return y

@@ -187,51 +187,63 @@ int crbq_sgemm(int transa, int transb, int64_t M, int64_t N, int64_t K,
                float alpha, const float* A, int64_t lda, const float* B,
                int64_t ldb, float beta, float* C, int64_t ldc, void* stream);
 
-/* ---- packed low-bit storage and GEMV -------------------------------------
+/* ---- packed low-bit storage, GEMV and GEMM --------------------------------
  * No counterpart in the reference, which keeps fake-quantized fp16/bf16
  * weights (bigptq.py:278-280); for inference callers that want the
- * quantized layer in 3 bits per weight.  Within a 128-column block of a
- * row the quantized weights take <= 2 values per non-salient group
- * (mask 1, mask 2, order 1) and <= 4 on the salient columns (mask 3, order
- * 2), and the salient columns are the same for every row.  With
- * nblk = ceil(C / 128):
+ * quantized layer in about 3 bits per weight.  Within a 128-column block
+ * of a row the quantized weights take 2 values per non-salient group
+ * (mask 1, mask 2, order 1) and 4 on the salient columns (mask 3, order 2),
+ * and the salient columns are the same for every row, except where a
+ * binarizer's sign is exactly 0 (torch.sign of an element equal to its
+ * group's mean gives the mean itself): such rare elements are kept as
+ * exceptions.  With nblk = ceil(C / 128):
  *   codes [R][ldc] bytes, ldc >= nblk * 32 (multiple of 8, 8-byte aligned): 2 bits per
  *     weight, column j of block b at byte b * 32 + j / 4, bits 2 (j % 4);
- *   lut [R][nblk][8] in the weight dtype (16-byte aligned): mask1 lo, hi,
- *     mask2 lo, hi, mask3 4 values, ascending (-0 below +0);
+ *   lut [R][nblk][8] in the weight dtype (16-byte aligned): mask1 two values,
+ *     mask2 two, mask3 four, each group's ascending (-0 below +0); a group
+ *     keeps its most frequent values (ties to the smaller), chosen among
+ *     its 8 smallest distinct values;
  *   sal [nblk][16] bytes (8-byte aligned): bit j % 8 of byte j / 8 marks salient column j;
- *   weight = lut[r][b][4 * salient + code].
+ *   weight = lut[r][b][4 * salient + code];
+ *   exceptions: the other elements, code = their group's first entry, with
+ *     ex_idx = r * C + c (int64), ex_val = the exact 16-bit value and
+ *     ex_delta = value - lut entry (fp32); list order unspecified.
  * crbq_pack reads the quantized weights Q (fp16/bf16) and the mask codes
- * (1/2/3, as crbq_fasterquant writes them) and sets the device int *status
- * to 0, or to an OR of 1 (a group with more distinct values than codes),
- * 2 (salient columns differ between rows), 4 (mask code outside 1..3);
- * the caller reads it after the stream.  Blocksizes that are multiples of
- * 128 satisfy the structure.  crbq_unpack writes the weights back bit for
- * bit.  crbq_gemv_packed: y[v][r] = sum_c W[r][c] x[v][c] for nvec <= 16
- * vectors x in the weights' dtype (ldx multiple of 8, 16-byte aligned),
- * fp32 y. */
+ * (1/2/3, as crbq_fasterquant writes them), fills up to ex_cap exceptions,
+ * sets the device int *ex_count to their number and *status to 0, or to
+ * an OR of 1 (more than ex_cap exceptions), 2 (salient columns differ
+ * between rows), 4 (mask code outside 1..3); the caller reads both after
+ * the stream.  crbq_unpack writes the weights back bit for bit.
+ * crbq_gemv_packed: y[v][r] = sum_c W[r][c] x[v][c] for nvec <= 16 vectors
+ * x in the weights' dtype (ldx multiple of 8, 16-byte aligned), fp32 y;
+ * the n_ex exceptions are added as delta * x in list order after the
+ * packed product. */
 int crbq_pack(const void* Q, int dtype, int64_t R, int64_t C, int64_t ldq,
               const uint8_t* masks, int64_t ldm, uint8_t* codes, int64_t ldc,
-              void* lut, uint8_t* sal, int* status, void* stream);
+              void* lut, uint8_t* sal, int64_t* ex_idx, void* ex_val, float* ex_delta,
+              int ex_cap, int* ex_count, int* status, void* stream);
 int crbq_unpack(const uint8_t* codes, int64_t ldc, const void* lut, const uint8_t* sal,
-                int dtype, int64_t R, int64_t C, void* Q, int64_t ldq, void* stream);
+                const int64_t* ex_idx, const void* ex_val, int64_t n_ex, int dtype,
+                int64_t R, int64_t C, void* Q, int64_t ldq, void* stream);
 int crbq_gemv_packed(const uint8_t* codes, int64_t ldc, const void* lut,
-                     const uint8_t* sal, int dtype, int64_t R, int64_t C,
-                     const void* x, int64_t ldx, int nvec, float* y, int64_t ldy,
-                     void* stream);
+                     const uint8_t* sal, const int64_t* ex_idx, const float* ex_delta,
+                     int64_t n_ex, int dtype, int64_t R, int64_t C, const void* x,
+                     int64_t ldx, int nvec, float* y, int64_t ldy, void* stream);
 /* crbq_gemm_packed: Y[t][r] = sum_c W[r][c] X[t][c] for ntok tokens (any
  * count; meant for prefill batches above the GEMV's 16), X in the weights'
- * dtype (ldx multiple of 8, 16-byte aligned), fp32 Y [ntok][ldy].  Each
- * decoded weight fragment is reused for 64 tokens (128 above 64).  When the
- * shapes give fewer than about 512 row x token tiles the column blocks are split over
- * workgroups whose fp32 partials go to the workspace and are summed in
- * split order (deterministic); crbq_gemm_packed_workspace_size(R, C, ntok)
- * bytes (0 when there is no split) depend on the shapes only. */
+ * dtype (ldx multiple of 8, 16-byte aligned), fp32 Y [ntok][ldy], the
+ * exceptions added as in the GEMV.  Each decoded weight fragment is reused
+ * for 64 tokens (128 above 64).  When the shapes give fewer than about 512
+ * row x token tiles the column blocks are split over workgroups whose fp32
+ * partials go to the workspace and are summed in split order
+ * (deterministic); crbq_gemm_packed_workspace_size(R, C, ntok) bytes (0
+ * when there is no split) depend on the shapes only. */
 size_t crbq_gemm_packed_workspace_size(int64_t R, int64_t C, int64_t ntok);
 int crbq_gemm_packed(const uint8_t* codes, int64_t ldc, const void* lut,
-                     const uint8_t* sal, int dtype, int64_t R, int64_t C,
-                     const void* x, int64_t ldx, int64_t ntok, float* y, int64_t ldy,
-                     void* ws, size_t ws_bytes, void* stream);
+                     const uint8_t* sal, const int64_t* ex_idx, const float* ex_delta,
+                     int64_t n_ex, int dtype, int64_t R, int64_t C, const void* x,
+                     int64_t ldx, int64_t ntok, float* y, int64_t ldy, void* ws,
+                     size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

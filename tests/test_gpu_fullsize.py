@@ -1,0 +1,139 @@
+"""Size-independent properties at the BASELINE configs' full sizes
+(configs[1] OPT-1.3B layer crb vs braq, configs[3] OPT-66B fc2 with a
+36864^2 Hessian, configs[4] Llama-3-8B layer in bf16 with 1 % outlier
+columns, crb with 5 refinement rounds and crbog), where the CPU oracle is
+too slow to run:
+
+* Hessian: 256 sampled entries against float64 dot products over all
+  128 x 2048 tokens (relative to sqrt(H_ii H_jj)).
+* GPTQ identity: the block loop makes W0 - Q = E U with E the per-column
+  errors (w - q) / U_jj and U the upper Cholesky factor of H_d^-1 (H_d the
+  damped Hessian), so U H_d U^T = I gives, per row,
+  sum_j e_j^2 / 2 = (W0 - Q) H_d (W0 - Q)^T / 2, which is the loss the
+  loop accumulates (bigptq.py:240-262).  It holds whatever the quantizer
+  and ties the Hessian, the factor, the block loop and every trailing
+  update together.
+* Binarization structure: all rows share the salient columns (crbq_pack
+  accepts the layer), the quantized values of each group fit the packed
+  table apart from rare exceptions (an element equal to its group's mean
+  binarizes to the mean itself), and the packed layer unpacks bit-exactly.
+"""
+import pytest
+import torch
+
+from crb_amd import synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+NTOK = 128 * 2048
+
+
+def _k():
+    from crb_amd import kernels
+    return kernels
+
+
+def _acts(C, seed):
+    """[NTOK, C] fp16 activations with Student-t(4) channel scales."""
+    s = synth.channel_scales(C, seed, kind="student_t4", device=DEV)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    x = torch.empty(NTOK, C, dtype=torch.float16, device=DEV)
+    for t0 in range(0, NTOK, 8192):
+        x[t0:t0 + 8192] = (torch.randn(8192, C, generator=g, device=DEV) * s).half()
+    return x
+
+
+def _hessian(X, nseq=128):
+    C = X.shape[1]
+    S = torch.zeros(C, C, device=DEV)
+    _k().hessian_accum(X, S)
+    H = _k().hessian_finalize(S, 2.0 / nseq, S)
+    # sampled entries against float64 sums over every token
+    g = torch.Generator().manual_seed(C)
+    i = torch.randint(0, C, (256,), generator=g).to(DEV)
+    j = torch.randint(0, C, (256,), generator=g).to(DEV)
+    want = torch.zeros(256, dtype=torch.float64, device=DEV)
+    for t0 in range(0, X.shape[0], 32768):
+        xa = X[t0:t0 + 32768, i].double()
+        xb = X[t0:t0 + 32768, j].double()
+        want += (xa * xb).sum(0)
+    want *= 2.0 / nseq
+    d = torch.diagonal(H).double()
+    rel = (H[i, j].double() - want).abs() / torch.sqrt(d[i] * d[j])
+    assert float(rel.max()) < 1e-5, float(rel.max())
+    return H
+
+
+def _quantize_check(name, W16, H, method, refine_iters=1):
+    """One sublayer through the factor and the block loop; checks the GPTQ
+    identity and the binarization structure.  Returns the layer error."""
+    Hd = H.clone()
+    W = W16.float().contiguous()
+    U, retries, fb = _k().hinv_upper(Hd, W, 0.01)          # Hd is now the damped H
+    assert retries == 0 and not fb
+    W0 = W.clone()
+    L = torch.zeros(W.shape[0], device=DEV)
+    from crb_amd import _lib
+    p = _lib.params(method, refine_iters=refine_iters)
+    masks, _ = _k().fasterquant_blocks(W, U, p, L, want_masks=True)
+    D = W0 - W
+    quad = ((D @ Hd) * D).sum(1) / 2
+    rel = (quad.double() - L.double()).abs() / L.double().clamp_min(1e-30)
+    tot = abs(float(quad.double().sum()) - float(L.double().sum())) / float(L.double().sum())
+    print(f"  {name} {method}: error {float(L.sum()):.5g}  identity rel total {tot:.2e} "
+          f"row max {float(rel.max()):.2e}", flush=True)
+    assert tot < 1e-3, tot
+    assert float(rel.max()) < 1e-2, float(rel.max())
+    Wq = W.to(W16.dtype).contiguous()
+    codes, lut, sal, ex = _k().pack(Wq, masks)               # raises on a structure violation
+    n_ex = int(ex.idx.numel())
+    print(f"  {name} {method}: packed, {n_ex} exceptions", flush=True)
+    assert n_ex * 10000 <= Wq.numel(), n_ex                 # rare: ties at a group mean
+    back = _k().unpack(codes, lut, sal, W.shape[1], ex)
+    assert torch.equal(back.view(torch.int16), Wq.view(torch.int16))
+    return float(L.sum())
+
+
+def test_cfg1_opt13b_layer_crb_and_braq():
+    print("cfg1 OPT-1.3B layer", flush=True)
+    subs = synth.opt_sublayers("opt-1.3b")
+    groups = {}
+    for j, (name, r, c, grp) in enumerate(subs):
+        if grp not in groups:
+            groups[grp] = _hessian(_acts(c, 100 + j))
+    errs = {}
+    for method in ("crb", "braq"):
+        tot = 0.0
+        for j, (name, r, c, grp) in enumerate(subs):
+            W = (torch.randn(r, c, generator=torch.Generator(device=DEV).manual_seed(j),
+                             device=DEV) * 0.02).half()
+            tot += _quantize_check(name, W, groups[grp], method)
+        errs[method] = tot
+    print(f"  layer error crb {errs['crb']:.5g} braq {errs['braq']:.5g}", flush=True)
+
+
+def test_cfg3_opt66b_fc2_max_shape():
+    print("cfg3 OPT-66B fc2 (C = 36864)", flush=True)
+    H = _hessian(_acts(36864, 7))
+    W = (torch.randn(9216, 36864, generator=torch.Generator(device=DEV).manual_seed(3),
+                     device=DEV) * 0.02).half()
+    _quantize_check("fc2", W, H, "crb")
+
+
+def test_cfg4_llama3_8b_layer_bf16():
+    print("cfg4 Llama-3-8B layer bf16", flush=True)
+    subs = synth.llama3_8b_sublayers()
+    groups = {}
+    for j, (name, r, c, grp) in enumerate(subs):
+        if grp not in groups:
+            groups[grp] = _hessian(_acts(c, 200 + j))
+    errs = {}
+    for method, it in (("crb", 5), ("crbog", 1)):
+        tot = 0.0
+        for j, (name, r, c, grp) in enumerate(subs):
+            W = synth.weight(r, c, 300 + j, outlier_frac=0.01, outlier_scale=10.0,
+                             dtype=torch.bfloat16, device=DEV)
+            tot += _quantize_check(name, W, groups[grp], method, refine_iters=it)
+        errs[method] = tot
+    print(f"  layer error crb(refine 5) {errs['crb']:.5g} crbog {errs['crbog']:.5g}", flush=True)

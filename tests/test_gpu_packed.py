@@ -1,8 +1,8 @@
 """Packed low-bit storage on the GPU: crbq_pack / crbq_unpack byte-for-byte
-against the NumPy statement of the format (tests/packed_ref.py) and bit-exact
-round trips of layers quantized by the block loop; crbq_gemv_packed against
-float64 products of the unpacked weights; PackedLinear and the stack
-driver's pack option.
+against the NumPy statement of the format (tests/packed_ref.py), exception
+lists included, and bit-exact round trips of layers quantized by the block
+loop; crbq_gemv_packed / crbq_gemm_packed against float64 products of the
+unpacked weights; PackedLinear and the stack driver's pack option.
 
 GEMV bar: |y - y64| <= 1e-5 * sum_c |w_c x_c| per output (fp32 sums of
 exact 16-bit products)."""
@@ -21,24 +21,33 @@ def _k():
     return kernels
 
 
-@pytest.mark.parametrize("R,C,dtype", [(37, 300, torch.float16), (64, 512, torch.bfloat16),
-                                       (5, 128, torch.float16), (200, 1000, torch.bfloat16)])
-def test_pack_matches_format_statement(R, C, dtype):
-    print(f"pack structured {R}x{C} {dtype}", flush=True)
-    q, masks = structured(R, C, seed=R + C, dtype=np.float16)
+def _q16(q, dtype):
     bits = q.view(np.uint16)
     if dtype == torch.bfloat16:          # reinterpret the same bit patterns as bf16
-        Q = torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16).to(DEV)
-    else:
-        Q = torch.from_numpy(q).to(DEV)
+        return torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16).to(DEV)
+    return torch.from_numpy(q).to(DEV)
+
+
+@pytest.mark.parametrize("R,C,dtype,n_odd", [(37, 300, torch.float16, 0),
+                                             (64, 512, torch.bfloat16, 0),
+                                             (5, 128, torch.float16, 3),
+                                             (200, 1000, torch.bfloat16, 40)])
+def test_pack_matches_format_statement(R, C, dtype, n_odd):
+    print(f"pack structured {R}x{C} {dtype} odd={n_odd}", flush=True)
+    q, masks = structured(R, C, seed=R + C, dtype=np.float16, n_odd=n_odd)
+    bits = q.view(np.uint16)
+    Q = _q16(q, dtype)
     M = torch.from_numpy(masks).to(DEV)
-    codes, lut, sal = _k().pack(Q, M)
-    rc, rl, rs, st = pack_ref(bits, masks)
-    assert st == 0
+    codes, lut, sal, ex = _k().pack(Q, M)
+    rc, rl, rs, rex, st = pack_ref(bits, masks, bf16=dtype == torch.bfloat16)
+    assert st == 0 and (len(rex[0]) > 0) == (n_odd > 0)
     assert np.array_equal(codes.cpu().numpy(), rc)
     assert np.array_equal(lut.cpu().view(torch.int16).numpy().view(np.uint16), rl)
     assert np.array_equal(sal.cpu().numpy(), rs)
-    back = _k().unpack(codes, lut, sal, C)
+    assert np.array_equal(ex.idx.cpu().numpy(), rex[0])
+    assert np.array_equal(ex.val.cpu().view(torch.int16).numpy().view(np.uint16), rex[1])
+    assert np.array_equal(ex.delta.cpu().numpy(), rex[2])
+    back = _k().unpack(codes, lut, sal, C, ex)
     assert torch.equal(back.view(torch.int16).cpu(), Q.view(torch.int16).cpu())
 
 
@@ -48,9 +57,11 @@ def test_pack_reports_structure_errors():
     q, masks = structured(8, 256, seed=3)
     col = int(np.nonzero(masks[2, :128] == 1)[0][0])
     bad = q.copy()
-    bad[2, col] = np.float16(0.123)
-    with pytest.raises(CrbqError, match="more distinct values"):
-        _k().pack(torch.from_numpy(bad).to(DEV), torch.from_numpy(masks).to(DEV))
+    bad[2, col] = np.float16(0.123)            # one out-of-table value: an exception
+    codes, lut, sal, ex = _k().pack(torch.from_numpy(bad).to(DEV), torch.from_numpy(masks).to(DEV))
+    assert ex.idx.tolist() == [2 * 256 + col]
+    with pytest.raises(CrbqError, match="exception list"):
+        _k().pack(torch.from_numpy(bad).to(DEV), torch.from_numpy(masks).to(DEV), ex_cap=0)
     m2 = masks.copy()
     m2[5, int(np.nonzero(masks[0, :128] == 3)[0][0])] = 1
     with pytest.raises(CrbqError, match="salient columns differ"):
@@ -74,11 +85,12 @@ def test_quantized_layer_round_trip(method, dtype, R, C):
     lq = LayerQuantizer([Sublayer("w", W, "x")], method=method, keep_masks=True)
     lq.add_batch("x", X.to(DEV))
     lq.quantize()
-    codes, lut, sal = _k().pack(W, lq.masks["w"])
-    assert torch.equal(_k().unpack(codes, lut, sal, C).view(torch.int16), W.view(torch.int16))
-    rc, rl, rs, st = pack_ref(W.view(torch.int16).cpu().numpy().view(np.uint16),
-                              lq.masks["w"].cpu().numpy())
+    codes, lut, sal, ex = _k().pack(W, lq.masks["w"])
+    assert torch.equal(_k().unpack(codes, lut, sal, C, ex).view(torch.int16), W.view(torch.int16))
+    rc, rl, rs, rex, st = pack_ref(W.view(torch.int16).cpu().numpy().view(np.uint16),
+                                   lq.masks["w"].cpu().numpy(), bf16=dtype == torch.bfloat16)
     assert st == 0 and np.array_equal(codes.cpu().numpy(), rc)
+    assert np.array_equal(ex.idx.cpu().numpy(), rex[0])
 
 
 @pytest.mark.parametrize("R,C,dtype,nvec", [(37, 300, torch.float16, 1),
@@ -90,16 +102,13 @@ def test_quantized_layer_round_trip(method, dtype, R, C):
                                             (17, 136, torch.bfloat16, 11)])
 def test_gemv_against_float64(R, C, dtype, nvec):
     print(f"gemv {R}x{C} {dtype} nvec={nvec}", flush=True)
-    q, masks = structured(R, C, seed=7 * R + C)
-    if dtype == torch.bfloat16:
-        Q = torch.from_numpy(q.view(np.uint16).astype(np.int16)).view(torch.bfloat16).to(DEV)
-    else:
-        Q = torch.from_numpy(q).to(DEV)
-    codes, lut, sal = _k().pack(Q, torch.from_numpy(masks).to(DEV))
+    q, masks = structured(R, C, seed=7 * R + C, n_odd=R // 8)
+    Q = _q16(q, dtype)
+    codes, lut, sal, ex = _k().pack(Q, torch.from_numpy(masks).to(DEV))
     g = torch.Generator().manual_seed(C)
     xf = torch.randn(nvec, C + 24, generator=g)
     x = xf.to(dtype).to(DEV)[:, :C]        # rows strided by C + 24
-    y = _k().gemv_packed(codes, lut, sal, C, x)
+    y = _k().gemv_packed(codes, lut, sal, C, x, ex)
     torch.cuda.synchronize()
     W64 = Q.double().cpu()
     x64 = x.double().cpu()
@@ -121,15 +130,12 @@ def test_gemm_against_float64(R, C, T, dtype):
     covered (the split depends on R x T tiles)."""
     print(f"gemm {R}x{C} T={T} {dtype}", flush=True)
     from crb_amd import _lib
-    q, masks = structured(R, C, seed=5 * R + C)
-    if dtype == torch.bfloat16:
-        Q = torch.from_numpy(q.view(np.uint16).astype(np.int16)).view(torch.bfloat16).to(DEV)
-    else:
-        Q = torch.from_numpy(q).to(DEV)
-    codes, lut, sal = _k().pack(Q, torch.from_numpy(masks).to(DEV))
+    q, masks = structured(R, C, seed=5 * R + C, n_odd=R // 8)
+    Q = _q16(q, dtype)
+    codes, lut, sal, ex = _k().pack(Q, torch.from_numpy(masks).to(DEV))
     g = torch.Generator().manual_seed(T)
     x = torch.randn(T, C + 40, generator=g).to(dtype).to(DEV)[:, :C]
-    y = _k().gemm_packed(codes, lut, sal, C, x)
+    y = _k().gemm_packed(codes, lut, sal, C, x, ex)
     torch.cuda.synchronize()
     W64 = Q.double().cpu()
     x64 = x.double().cpu()
@@ -148,14 +154,14 @@ def test_gemm_deterministic_and_matches_gemv():
     """Split-K partials are summed in a fixed order: repeated calls are
     bitwise equal; the first 16 tokens agree with the GEMV to the same bar."""
     print("gemm determinism", flush=True)
-    q, masks = structured(1000, 4096, seed=9)
+    q, masks = structured(1000, 4096, seed=9, n_odd=100)
     Q = torch.from_numpy(q).to(DEV)
-    codes, lut, sal = _k().pack(Q, torch.from_numpy(masks).to(DEV))
+    codes, lut, sal, ex = _k().pack(Q, torch.from_numpy(masks).to(DEV))
     x = torch.randn(40, 4096, generator=torch.Generator().manual_seed(2)).half().to(DEV)
-    y1 = _k().gemm_packed(codes, lut, sal, 4096, x)
-    y2 = _k().gemm_packed(codes, lut, sal, 4096, x)
+    y1 = _k().gemm_packed(codes, lut, sal, 4096, x, ex)
+    y2 = _k().gemm_packed(codes, lut, sal, 4096, x, ex)
     assert torch.equal(y1, y2)
-    yv = _k().gemv_packed(codes, lut, sal, 4096, x[:16])
+    yv = _k().gemv_packed(codes, lut, sal, 4096, x[:16], ex)
     scale = x[:16].double().abs() @ Q.double().abs().t()
     assert ((y1[:16].double() - yv.double()).abs() <= 2e-5 * scale + 1e-30).all()
 
@@ -163,7 +169,7 @@ def test_gemm_deterministic_and_matches_gemv():
 def test_packed_linear_forward():
     print("packed linear", flush=True)
     from crb_amd.packed import PackedLinear
-    q, masks = structured(192, 512, seed=11)
+    q, masks = structured(192, 512, seed=11, n_odd=12)
     lin = torch.nn.Linear(512, 192).to(DEV).half()
     lin.weight.data = torch.from_numpy(q).to(DEV)
     pl = PackedLinear.from_linear(lin, torch.from_numpy(masks).to(DEV))
