@@ -72,13 +72,22 @@ __global__ __launch_bounds__(1024) void k_damp(float* H, int64_t ldh, int C, flo
 
 __global__ void k_set_int(int* p, int v) { *p = v; }
 
-// A[i][j] = H[C-1-i][C-1-j] in the lower triangle, 0 above it
+// Grid of the row-wise copies below: x = row, y = 1024-column chunk.
+static inline dim3 rows_grid(int64_t C) {
+  return dim3((unsigned)C, (unsigned)((C + 1023) / 1024));
+}
+
+// A[i][j] = H[C-1-i][C-1-j] in the lower triangle, 0 above it (rows_grid)
 __global__ __launch_bounds__(256) void k_reverse_lower(const float* __restrict__ H, int64_t ldh,
                                                        int C, float* A, int64_t lda) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int i = (int)(idx / C), j = (int)(idx % C);
-  if (i >= C) return;
-  A[(int64_t)i * lda + j] = j <= i ? H[(int64_t)(C - 1 - i) * ldh + (C - 1 - j)] : 0.f;
+  const int i = blockIdx.x;
+  const float* h = H + (int64_t)(C - 1 - i) * ldh + (C - 1);
+  float* a = A + (int64_t)i * lda;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int j = blockIdx.y * 1024 + k * 256 + threadIdx.x;
+    if (j < C) a[j] = j <= i ? h[-j] : 0.f;
+  }
 }
 
 // Y[r][c] = X[r][c] for an M x N block (row strides ldx, ldy)
@@ -92,13 +101,17 @@ __global__ __launch_bounds__(256) void k_copy2d(const float* __restrict__ X, int
   Y[(int64_t)r * ldy + c] = X[(int64_t)r * ldx + c];
 }
 
-// U[i][j] = X[C-1-i][C-1-j] for j >= i, 0 below the diagonal
+// U[i][j] = X[C-1-i][C-1-j] for j >= i, 0 below the diagonal (rows_grid)
 __global__ __launch_bounds__(256) void k_reverse_to_u(const float* __restrict__ X, int64_t ldx,
                                                       int C, float* U, int64_t ldu) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int i = (int)(idx / C), j = (int)(idx % C);
-  if (i >= C) return;
-  U[(int64_t)i * ldu + j] = j >= i ? X[(int64_t)(C - 1 - i) * ldx + (C - 1 - j)] : 0.f;
+  const int i = blockIdx.x;
+  const float* x = X + (int64_t)(C - 1 - i) * ldx + (C - 1);
+  float* u = U + (int64_t)i * ldu;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int j = blockIdx.y * 1024 + k * 256 + threadIdx.x;
+    if (j < C) u[j] = j >= i ? x[-j] : 0.f;
+  }
 }
 
 // Last resort (bigptq.py:124-128): L = diag(sqrt(clamp(diag H, 1e-8))),
@@ -550,11 +563,11 @@ extern "C" int crbq_hinv_upper_async(float* H, int64_t ldh, int64_t C, float* W,
   k_damp<<<1, 1024, 0, s>>>(H, ldh, Ci, percdamp, 0, w.scal);      // bigptq.py:109-111
   CRBQ_LAUNCH_CHECK();
   k_set_int<<<1, 1, 0, s>>>(w.info, 0);
-  k_reverse_lower<<<nblocks(C * C), 256, 0, s>>>(H, ldh, Ci, w.A, C);
+  k_reverse_lower<<<rows_grid(C), 256, 0, s>>>(H, ldh, Ci, w.A, C);
   CRBQ_LAUNCH_CHECK();
   st = chol_inv_sweep(w.A, C, Ci, w, s);
   if (st) return st;
-  k_reverse_to_u<<<nblocks(C * C), 256, 0, s>>>(w.A, C, Ci, U, ldu);
+  k_reverse_to_u<<<rows_grid(C), 256, 0, s>>>(w.A, C, Ci, U, ldu);
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }
@@ -584,7 +597,7 @@ extern "C" int crbq_hinv_upper_finish(float* H, int64_t ldh, int64_t C, float* U
     CRBQ_LAUNCH_CHECK();
     if (attempt == 10) break;                                       // 10 attempts in all
     k_set_int<<<1, 1, 0, s>>>(w.info, 0);
-    k_reverse_lower<<<nblocks(C * C), 256, 0, s>>>(H, ldh, Ci, w.A, C);
+    k_reverse_lower<<<rows_grid(C), 256, 0, s>>>(H, ldh, Ci, w.A, C);
     CRBQ_LAUNCH_CHECK();
     st = chol_inv_sweep(w.A, C, Ci, w, s);
     if (st) return st;
@@ -592,7 +605,7 @@ extern "C" int crbq_hinv_upper_finish(float* H, int64_t ldh, int64_t C, float* U
     CRBQ_HIP(hipStreamSynchronize(s));
     ok = hinfo == 0;
     if (ok) {
-      k_reverse_to_u<<<nblocks(C * C), 256, 0, s>>>(w.A, C, Ci, U, ldu);
+      k_reverse_to_u<<<rows_grid(C), 256, 0, s>>>(w.A, C, Ci, U, ldu);
       CRBQ_LAUNCH_CHECK();
     }
   }

@@ -50,7 +50,8 @@ __device__ __forceinline__ f4_t mfma16<b8_t>(b8_t a, b8_t b, f4_t c) {
 // 16-bit inputs (T8 = h8_t or b8_t; storage is 2 bytes per element):
 // 256 x 256 output tile per workgroup (k_syrk16p below).
 // Split-K: workgroup (tile, s) sums tokens [s*span, (s+1)*span) and, when
-// the grid is split, writes its partial tile to P[s] for k_sum_splits.
+// the grid is split, split 0 adds into S and split s > 0 writes its
+// partial tile to P[s - 1] for k_sum_splits.
 constexpr int ST = 256;                 // output tile (channels)
 
 // FAST: C and ldx are multiples of 8 and X is 16-byte aligned, so every
@@ -248,7 +249,10 @@ __global__ __launch_bounds__(SYRKP_THREADS) void k_syrk16p(const uint16_t* __res
     sync_lds();
   }
   const int c16 = lane & 15, r4 = (lane >> 4) * 4;
-  float* out = P ? P + (size_t)blockIdx.y * (size_t)C * lds : S;
+  // split 0 adds into S, split s > 0 writes P[s - 1]; k_sum_splits then
+  // adds P[0..] in split order, so S + acc_0 + acc_1 + ... either way
+  const bool part = P && blockIdx.y > 0;
+  float* out = part ? P + (size_t)(blockIdx.y - 1) * (size_t)C * lds : S;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -259,7 +263,7 @@ __global__ __launch_bounds__(SYRKP_THREADS) void k_syrk16p(const uint16_t* __res
         const int gj = tj * ST + wn + j * 16 + c16;
         if (gi < C && gj < C && gi <= gj) {
           float* q = out + (int64_t)gi * lds + gj;
-          *q = P ? acc[i][j][r] : *q + acc[i][j][r];
+          *q = part ? acc[i][j][r] : *q + acc[i][j][r];
         }
       }
 }
@@ -427,7 +431,10 @@ __global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __res
     sync_lds();
   }
   const int c16 = lane & 15, r4 = (lane >> 4) * 4;
-  float* out = P ? P + (size_t)blockIdx.y * (size_t)C * lds : S;
+  // split 0 adds into S, split s > 0 writes P[s - 1]; k_sum_splits then
+  // adds P[0..] in split order, so S + acc_0 + acc_1 + ... either way
+  const bool part = P && blockIdx.y > 0;
+  float* out = part ? P + (size_t)(blockIdx.y - 1) * (size_t)C * lds : S;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -438,20 +445,29 @@ __global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __res
         const int gj = tj * ST + wn + j * 16 + c16;
         if (gi < C && gj < C && gi <= gj) {
           float* q = out + (int64_t)gi * lds + gj;
-          *q = P ? acc[i][j][r] : *q + acc[i][j][r];
+          *q = part ? acc[i][j][r] : *q + acc[i][j][r];
         }
       }
 }
 
-// S[i][j] += sum_s P[s][i][j] in split order, upper triangle
+// S[i][j] += sum_s P[s][i][j] in split order, upper triangle.  Grid: x =
+// row, y = 1024-column chunk; 256 threads, 4 columns each.
 __global__ __launch_bounds__(256) void k_sum_splits(const float* __restrict__ P, int nsplit,
                                                     int C, float* S, int64_t lds) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int i = (int)(idx / C), j = (int)(idx % C);
-  if (i >= C || j < i) return;
-  float v = S[(int64_t)i * lds + j];
-  for (int s = 0; s < nsplit; ++s) v = v + P[(size_t)s * C * lds + (int64_t)i * lds + j];
-  S[(int64_t)i * lds + j] = v;
+  const int i = blockIdx.x;
+  const int j0 = blockIdx.y * 1024;
+  if (j0 + 1023 < i) return;
+  const float* pi = P + (int64_t)i * lds;
+  float* si = S + (int64_t)i * lds;
+  const size_t pstride = (size_t)C * lds;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int j = j0 + k * 256 + threadIdx.x;
+    if (j < i || j >= C) continue;
+    float v = si[j];
+    for (int sp = 0; sp < nsplit; ++sp) v = v + pi[sp * pstride + j];
+    si[j] = v;
+  }
 }
 
 // fp32 inputs: LDS in natural token-major layout, A[i][k] = X[k][i].
@@ -513,15 +529,46 @@ __global__ __launch_bounds__(256) void k_syrk32(const float* __restrict__ X, int
       }
 }
 
+// H = scale * sym(S) from the upper triangle of S, in 64 x 64 tiles: the
+// workgroup of upper tile (ti, tj) stages it in LDS and writes it and its
+// mirror (tj, ti) with row-contiguous stores.  Grid: x = tj, y = ti;
+// workgroups below the diagonal exit.  H may alias S: a workgroup reads
+// only its own upper tile, and lower tiles are never read.
+constexpr int FT = 64;
 __global__ __launch_bounds__(256) void k_finalize(const float* S, int64_t lds, int C,
                                                   float scale, float* H, int64_t ldh) {
-  // H may alias S: each thread owns the pair (i, j), (j, i) with i <= j.
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int i = (int)(idx / C), j = (int)(idx % C);
-  if (i >= C || j < i) return;
-  const float v = scale * S[(int64_t)i * lds + j];
-  H[(int64_t)i * ldh + j] = v;
-  H[(int64_t)j * ldh + i] = v;
+  const int tj = blockIdx.x, ti = blockIdx.y;
+  if (ti > tj) return;
+  __shared__ float T[FT][FT + 1];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int r0 = ti * FT, c0 = tj * FT;
+#pragma unroll
+  for (int k = 0; k < FT; k += 4) {
+    const int r = r0 + ty + k, c = c0 + tx;
+    float v = 0.f;
+    if (r < C && c < C && r <= c) v = scale * S[(int64_t)r * lds + c];
+    T[ty + k][tx] = v;
+  }
+  __syncthreads();
+  if (ti == tj) {
+#pragma unroll
+    for (int k = 0; k < FT; k += 4) {
+      const int r = ty + k, c = tx;
+      if (r0 + r < C && c0 + c < C)
+        H[(int64_t)(r0 + r) * ldh + c0 + c] = r <= c ? T[r][c] : T[c][r];
+    }
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < FT; k += 4) {
+    const int r = r0 + ty + k, c = c0 + tx;
+    if (r < C && c < C) H[(int64_t)r * ldh + c] = T[ty + k][tx];
+  }
+#pragma unroll
+  for (int k = 0; k < FT; k += 4) {
+    const int r = c0 + ty + k, c = r0 + tx;
+    if (r < C && c < C) H[(int64_t)r * ldh + c] = T[tx][ty + k];
+  }
 }
 
 }  // namespace crbq
@@ -688,8 +735,8 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
       CRBQ_LAUNCH_CHECK();
       tm.stop(s);
       if (P) {
-        crbq::k_sum_splits<<<(unsigned)((C * C + 255) / 256), 256, 0, s>>>(P, ns, (int)C, S,
-                                                                           lds);
+        crbq::k_sum_splits<<<dim3((unsigned)C, (unsigned)((C + 1023) / 1024)), 256, 0, s>>>(
+            P, ns - 1, (int)C, S, lds);
         CRBQ_LAUNCH_CHECK();
       }
     }
@@ -717,7 +764,8 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
   CRBQ_LAUNCH_CHECK();
   tm.stop(s);
   if (P) {
-    crbq::k_sum_splits<<<(unsigned)((C * C + 255) / 256), 256, 0, s>>>(P, ns, (int)C, S, lds);
+    crbq::k_sum_splits<<<dim3((unsigned)C, (unsigned)((C + 1023) / 1024)), 256, 0, s>>>(
+        P, ns - 1, (int)C, S, lds);
     CRBQ_LAUNCH_CHECK();
   }
   return CRBQ_OK;
@@ -755,10 +803,10 @@ extern "C" int crbq_syrk_timing_collect(float* ms, int64_t* C, int max, int* n) 
 
 extern "C" int crbq_hessian_finalize(const float* S, int64_t lds, int64_t C, float scale,
                                      float* H, int64_t ldh, void* stream) {
-  if (!S || !H || C <= 0 || lds < C || ldh < C) return CRBQ_ERR_ARG;
-  const int64_t n = C * C;
-  crbq::k_finalize<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(
-      S, lds, (int)C, scale, H, ldh);
+  if (!S || !H || C <= 0 || C > (1 << 20) || lds < C || ldh < C) return CRBQ_ERR_ARG;
+  const unsigned nt = (unsigned)((C + crbq::FT - 1) / crbq::FT);
+  crbq::k_finalize<<<dim3(nt, nt), 256, 0, (hipStream_t)stream>>>(S, lds, (int)C, scale, H,
+                                                                    ldh);
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }

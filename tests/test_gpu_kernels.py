@@ -89,6 +89,29 @@ def test_hessian_accum(dtype, T, C):
     assert torch.equal(H.cpu(), H.cpu().t())
 
 
+@pytest.mark.parametrize("C,pad", [(1, 0), (63, 1), (64, 0), (130, 6), (300, 0)])
+def test_hessian_finalize_tiles(C, pad):
+    """H = scale * sym(upper(S)) in place and into another buffer, with
+    padded row strides; the lower triangle of S is never read."""
+    print(f"finalize C={C} pad={pad}", flush=True)
+    g = torch.Generator().manual_seed(C)
+    up = torch.randn(C, C, generator=g)
+    junk = torch.full((C, C), float("nan"))
+    S0 = torch.where(torch.ones(C, C, dtype=torch.bool).triu(), up, junk)
+    want = 0.25 * (torch.triu(up) + torch.triu(up, 1).t())
+    buf = torch.full((C, C + pad), float("nan"), device=DEV)
+    S = buf[:, :C]
+    S.copy_(S0.to(DEV))
+    Hbuf = torch.full((C, C + pad + 3), float("nan"), device=DEV)
+    H = Hbuf[:, :C]
+    _k().hessian_finalize(S, 0.25, H)
+    _k().hessian_finalize(S, 0.25, S)                  # in place
+    torch.cuda.synchronize()
+    assert torch.equal(H.cpu(), want)
+    assert torch.equal(S.cpu(), want)
+    assert torch.isnan(Hbuf[:, C:].cpu()).all()        # nothing written past C
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("T,C", [(8192, 520), (16384, 256)])
 def test_hessian_accum_split_k(dtype, T, C):
