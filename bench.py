@@ -100,6 +100,23 @@ def load_traffic(name):
     return vals.get("t")
 
 
+def load_profile_values(name):
+    """`key: value` lines of a summary in profiles/ (None if it is absent)."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    with open(path) as f:
+        for line in f:
+            k, sep, v = line.partition(":")
+            if sep and k.strip().replace("_", "").isalnum() and " " not in k.strip():
+                try:
+                    vals[k.strip()] = float(v)
+                except ValueError:
+                    pass
+    return vals
+
+
 def stack_run(dev, nlayers, ntok, chunk=8, seed=0):
     """The model-level driver (crb_amd/stack.py) on an OPT-6.7B-shaped decoder
     stack of nlayers random-init layers, calibration 128 x 2048 uniform token
@@ -187,6 +204,95 @@ def packed_gemv(dev, R=4096, C=16384, reps=20):
         td = graph_us(lambda: torch.nn.functional.linear(x, W))
         out["gemm_per_ntok"][ntok] = {"packed_us": round(tp, 2), "dense_fp16_us": round(td, 2),
                                       "packed_TFLOP_s": round(2 * R * C * ntok / tp / 1e6, 1)}
+    return out
+
+
+def _ev_ms(fn, reps):
+    """Average ms of fn() over reps back-to-back calls, events recorded on
+    the current stream (the one the wrappers launch on)."""
+    fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def kernel_rooflines(dev, R=4096, C=16384, reps=20):
+    """The block loop's kernels launched alone at the fc2 sublayer's shapes
+    (R x C = 4096 x 16384, 128-column blocks, 1024-column super-blocks),
+    each against its roofline:
+    * trailing update W[:, sb1:] -= Err @ U[sb0:sb1, sb1:] (k_sgemm, fp32
+      MFMA), K = 1024, N = 8192 remaining columns: 2 M N K flop;
+    * binarization (k_binarize_g, crb order 2) over 65536 rows x 128 columns
+      in one launch, 9 bytes per element (fp32 in, mask byte, fp32 out)
+      against HBM;
+    * one block step (salient/split search + binarize + in-block error
+      feedback, crbq_fasterquant on a 4096 x 128 block): its algorithmic
+      bytes (W block in, U block in, Q, Err and masks out) against HBM;
+    * the whole fc2 block loop alone (128 blocks, with trailing updates)."""
+    from crb_amd import _lib, kernels
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    out = {}
+    # trailing update
+    K, N = 1024, 8192
+    Wbig = torch.randn(R, C, device=dev, generator=g) * 0.02
+    Ubig = torch.randn(K, C, device=dev, generator=g) * 0.01
+    E = torch.randn(R, K, device=dev, generator=g) * 0.01
+    ms = _ev_ms(lambda: kernels.sgemm(E, Ubig[:, C - N:], Wbig[:, C - N:], alpha=-1.0,
+                                      beta=1.0), reps)
+    fl = 2.0 * R * N * K
+    out["trailing_update_gemm"] = {
+        "kernel": "k_sgemm<128> (fp32 MFMA)", "shape": [R, N, K], "ms": round(ms, 4),
+        "achieved": round(fl / ms / 1e9, 1), "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
+        "frac": round(fl / ms / 1e9 / (PEAK_F32 / 1e12), 3)}
+    # binarization, streaming shape
+    nb = 65536
+    x = torch.randn(nb, 128, device=dev, generator=g) * 0.02
+    m = torch.rand(nb, 128, device=dev, generator=g) < 0.9
+    ob = torch.empty_like(x)
+    ms = _ev_ms(lambda: kernels.binarize(x, m, 2, "crb", out=ob), reps)
+    by = nb * 128 * 9
+    out["binarize"] = {
+        "kernel": "k_binarize_g<16> (crb, order 2)", "shape": [nb, 128], "ms": round(ms, 4),
+        "achieved": round(by / ms / 1e6, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+        "frac": round(by / ms / 1e6 / (PEAK_HBM / 1e9), 3)}
+    # one block step and the whole loop
+    p = _lib.params("crb")
+    U = torch.triu(torch.randn(C, C, device=dev, generator=g) * 1e-3)
+    U.diagonal().add_(1.0)
+    L = torch.zeros(R, device=dev)
+    Wb = torch.empty(R, 128, device=dev)
+    W0b = Wbig[:, :128].contiguous()
+
+    def step():
+        Wb.copy_(W0b)
+        kernels.fasterquant_blocks(Wb, U[:128, :128], p, L, want_masks=False)
+
+    ms_copy = _ev_ms(lambda: Wb.copy_(W0b), reps)
+    ms = _ev_ms(step, reps) - ms_copy
+    by = R * 128 * 4 * 3 + 128 * 128 * 4 + R * 128
+    out["block_step"] = {
+        "kernels": "colscore, phase_a, qpass1-3, qscan1-3, phase_c, quantize",
+        "shape": [R, 128], "ms": round(ms, 4), "achieved": round(by / ms / 1e6, 1),
+        "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(by / ms / 1e6 / (PEAK_HBM / 1e9), 4),
+        "note": "2 MB working set per block, resident in L2/MALL; bound by the search's "
+                "dependent passes, not by HBM"}
+    del Ubig, E, x, m, ob
+    W = Wbig.clone()
+
+    def loop():
+        W.copy_(Wbig)
+        kernels.fasterquant_blocks(W, U, p, L, want_masks=False)
+
+    ms = _ev_ms(loop, 2)
+    out["block_loop_fc2_alone_ms"] = round(ms, 3)
+    del W, Wbig, U
+    torch.cuda.empty_cache()
     return out
 
 
@@ -339,6 +445,14 @@ def main():
                      "algorithmic_flop": flops,
                      "traffic": load_traffic("syrk_fc2_opt67b_traffic.md")},
     }
+    pv = load_profile_values("mfma_busy_layer.md") or {}
+    if "syrk_fc2_mfma_busy_per_simd" in pv:
+        # rocprofv3 counters of the same kernel: matrix-unit busy fraction
+        # and the engine clock it ran at (quoted peaks assume 2.4 GHz)
+        out["roofline"]["mfma_busy_per_simd"] = pv["syrk_fc2_mfma_busy_per_simd"]
+        out["roofline"]["clock_ghz_under_load"] = pv.get("syrk_fc2_clock_ghz")
+    out["kernels"] = kernel_rooflines(dev)
+    print(f"[bench] kernels: {out['kernels']}", file=sys.stderr, flush=True)
     if args.stack_layers > 0:
         del X
         torch.cuda.empty_cache()

@@ -1,5 +1,6 @@
-// Per-row binarizers of the three in-scope techniques, one wavefront per
-// row, EPL elements per lane.  Elementwise arithmetic is fp32 in the
+// Per-row binarizers of the three in-scope techniques: a row is held by an
+// aligned group of LPR lanes (64: one wavefront per row; 16: four rows per
+// wavefront), EPL elements per lane.  Elementwise arithmetic is fp32 in the
 // reference's operation order (compiled with -ffp-contract=off so nothing is
 // fused); every row reduction is summed exactly enough in fp64 and rounded
 // to fp32, the value the reference's fp32 torch.sum approximates.
@@ -16,45 +17,45 @@ struct CrbConsts {
   int iters;    // refinement rounds (reference: 1)
 };
 
-template <int EPL>
+template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rsum(const float (&v)[EPL], const bool (&m)[EPL]) {
   double s = 0.0;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) s += m[e] ? (double)v[e] : 0.0;
-  return (float)wave_sum(s);
+  return (float)group_sum<LPR>(s);
 }
 
-template <int EPL>
+template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rsum_abs(const float (&v)[EPL], const bool (&m)[EPL]) {
   double s = 0.0;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) s += m[e] ? (double)fabsf(v[e]) : 0.0;
-  return (float)wave_sum(s);
+  return (float)group_sum<LPR>(s);
 }
 
-template <int EPL>
+template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rcount(const bool (&m)[EPL]) {
   float c = 0.f;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) c += m[e] ? 1.f : 0.f;
-  return wave_sum_f(c);  // integer-valued, exact
+  return group_sum_f<LPR>(c);  // integer-valued, exact
 }
 
 // high_order_residual, binary.py:18-39.
-template <int EPL>
+template <int EPL, int LPR = 64>
 __device__ void hor_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
                         float (&acc)[EPL]) {
-  const float cnt = rcount(m);
+  const float cnt = rcount<EPL, LPR>(m);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
   for (int od = 0; od < order; ++od) {
     float c[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) c[e] = x[e] - acc[e];            // residual
-    const float mu = cnt > 0.f ? rsum(c, m) / cnt : 0.f;           // nanmean, NaN->0
+    const float mu = cnt > 0.f ? rsum<EPL, LPR>(c, m) / cnt : 0.f;           // nanmean, NaN->0
 #pragma unroll
     for (int e = 0; e < EPL; ++e) c[e] = c[e] - mu;
-    const float alpha = cnt > 0.f ? rsum_abs(c, m) / cnt : 0.f;
+    const float alpha = cnt > 0.f ? rsum_abs<EPL, LPR>(c, m) / cnt : 0.f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
       float b = tsign(c[e]) * alpha;
@@ -80,69 +81,69 @@ __device__ __forceinline__ void crb_solve(float d, float c12, float c1w, float c
 }
 
 // coupled_residual_binarization_stable_v7, binary.py:1544-1638.
-template <int EPL>
+template <int EPL, int LPR = 64>
 __device__ void crb_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
                         const CrbConsts& k, float (&out)[EPL],
                         float* scales = nullptr) {
-  const float d = rcount(m);
+  const float d = rcount<EPL, LPR>(m);
   const float ds = fmaxf(d, 1.f);
-  const float mean = rsum(x, m) / ds;
+  const float mean = rsum<EPL, LPR>(x, m) / ds;
   float cen[EPL], B1[EPL], B2[EPL], t[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) cen[e] = m[e] ? x[e] - mean : 0.f;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) B1[e] = m[e] ? tsign(cen[e]) : 0.f;
   if (order == 1) {                                                 // :1570-1576
-    const float a1 = rsum_abs(cen, m) / ds;
+    const float a1 = rsum_abs<EPL, LPR>(cen, m) / ds;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) out[e] = m[e] ? mean + a1 * B1[e] : 0.f;
     if (scales) { scales[0] = mean; scales[1] = 0.f; scales[2] = a1; scales[3] = 0.f; }
     return;
   }
-  const float a10 = rsum_abs(cen, m) / ds;                          // step 2
+  const float a10 = rsum_abs<EPL, LPR>(cen, m) / ds;                          // step 2
 #pragma unroll
   for (int e = 0; e < EPL; ++e) t[e] = m[e] ? cen[e] - a10 * B1[e] : 0.f;   // step 3
-  const float rmean = rsum(t, m) / ds;
+  const float rmean = rsum<EPL, LPR>(t, m) / ds;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) B2[e] = m[e] ? tsign(t[e] - rmean) : 0.f;
   float c12, c1w, c2w, a1, a2;
   {                                                                 // step 4
 #pragma unroll
     for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
-    c12 = rsum(t, m);
+    c12 = rsum<EPL, LPR>(t, m);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B1[e];
-    c1w = rsum(t, m);
+    c1w = rsum<EPL, LPR>(t, m);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B2[e];
-    c2w = rsum(t, m);
+    c2w = rsum<EPL, LPR>(t, m);
   }
   crb_solve(d, c12, c1w, c2w, k, a1, a2);
   if (!k.skip) {
     for (int it = 0; it < k.iters; ++it) {
 #pragma unroll
       for (int e = 0; e < EPL; ++e) t[e] = m[e] ? cen[e] - a1 * B1[e] : 0.f;  // step 5
-      const float t5m = rsum(t, m) / ds;
+      const float t5m = rsum<EPL, LPR>(t, m) / ds;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) B2[e] = m[e] ? tsign(t[e] - t5m) : 0.f;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B2[e];
-      c2w = rsum(t, m);
+      c2w = rsum<EPL, LPR>(t, m);
 #pragma unroll
       for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
-      c12 = rsum(t, m);
+      c12 = rsum<EPL, LPR>(t, m);
       crb_solve(d, c12, c1w, c2w, k, a1, a2);
 #pragma unroll
       for (int e = 0; e < EPL; ++e) t[e] = m[e] ? cen[e] - a2 * B2[e] : 0.f;  // step 6
-      const float t6m = rsum(t, m) / ds;
+      const float t6m = rsum<EPL, LPR>(t, m) / ds;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) B1[e] = m[e] ? tsign(t[e] - t6m) : 0.f;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B1[e];
-      c1w = rsum(t, m);
+      c1w = rsum<EPL, LPR>(t, m);
 #pragma unroll
       for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
-      c12 = rsum(t, m);
+      c12 = rsum<EPL, LPR>(t, m);
       crb_solve(d, c12, c1w, c2w, k, a1, a2);
     }
   }
@@ -151,7 +152,7 @@ __device__ void crb_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
     const float ap = a1 * B1[e] + a2 * B2[e];
     t[e] = m[e] ? cen[e] - ap : 0.f;
   }
-  const float muc = rsum(t, m) / ds;
+  const float muc = rsum<EPL, LPR>(t, m) / ds;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     float v = mean + muc;
@@ -163,31 +164,31 @@ __device__ void crb_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
 }
 
 // coupled_residual_binarization (CRBOG), binary.py:577-687.
-template <int EPL>
+template <int EPL, int LPR = 64>
 __device__ void crbog_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
                           float (&out)[EPL]) {
-  if (order == 1) { hor_row(x, m, 1, out); return; }               // :595-630
-  const float n = rcount(m);
+  if (order == 1) { hor_row<EPL, LPR>(x, m, 1, out); return; }               // :595-630
+  const float n = rcount<EPL, LPR>(m);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) out[e] = 0.f;
   if (n == 0.f) return;                                             // :647-649
-  const float mean = rsum(x, m) / n;
+  const float mean = rsum<EPL, LPR>(x, m) / n;
   float cen[EPL], B1[EPL], B2[EPL], t[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) { cen[e] = x[e] - mean; B1[e] = tsign(cen[e]); }
-  float a1 = rsum_abs(cen, m) / n;
+  float a1 = rsum_abs<EPL, LPR>(cen, m) / n;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) { t[e] = cen[e] - a1 * B1[e]; B2[e] = tsign(t[e]); }
-  float a2 = rsum_abs(t, m) / n;
+  float a2 = rsum_abs<EPL, LPR>(t, m) / n;
 #pragma unroll
   for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
-  const double c12 = (double)rsum(t, m);
+  const double c12 = (double)rsum<EPL, LPR>(t, m);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B1[e];
-  const double c1w = (double)rsum(t, m);
+  const double c1w = (double)rsum<EPL, LPR>(t, m);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B2[e];
-  const double c2w = (double)rsum(t, m);
+  const double c2w = (double)rsum<EPL, LPR>(t, m);
   const double dn = (double)n;
   const double det = dn * dn - c12 * c12;
   if (fabs(det) > 1e-12) {
@@ -205,18 +206,18 @@ __device__ void crbog_row(const float (&x)[EPL], const bool (&m)[EPL], int order
 }
 
 // Binarization.quantize dispatch, binary.py:2874-2890.
-template <int EPL>
+template <int EPL, int LPR = 64>
 __device__ __forceinline__ void binarize_row(int method, const float (&x)[EPL],
                                              const bool (&m)[EPL], int order,
                                              const CrbConsts& base, float (&out)[EPL]) {
   switch (method) {
-    case CRBQ_BRAQ: hor_row(x, m, order, out); break;
-    case CRBQ_CRBOG: crbog_row(x, m, order, out); break;
+    case CRBQ_BRAQ: hor_row<EPL, LPR>(x, m, order, out); break;
+    case CRBQ_CRBOG: crbog_row<EPL, LPR>(x, m, order, out); break;
     default: {
       CrbConsts k = base;
       k.skip = (method == CRBQ_CRB_NOREFINE || method == CRBQ_CRB_SYMDAMP_NOREFINE);
       k.sym = (method == CRBQ_CRB_SYMDAMP || method == CRBQ_CRB_SYMDAMP_NOREFINE);
-      crb_row(x, m, order, k, out);
+      crb_row<EPL, LPR>(x, m, order, k, out);
     }
   }
 }

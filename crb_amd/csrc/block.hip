@@ -1204,6 +1204,56 @@ __global__ __launch_bounds__(256) void k_binarize(const float* x, int R, int nc,
     if (c < nc) out[(int64_t)row * ldo + c] = o[e];
   }
 }
+// Rows of at most 4 * LPR columns, LPR lanes per row (256 / LPR rows per
+// workgroup), 8 elements per lane: lane r of a row holds columns
+// 4r .. 4r+3 and 4 LPR + 4r .. 4 LPR + 4r+3, moved with 16-byte accesses
+// (x, out and their row strides 16-byte aligned, mask rows 4-byte aligned;
+// the host checks).  Row reductions stay inside the row's lane group.
+template <int LPR>
+__global__ __launch_bounds__(256) void k_binarize_g(const float* x, int R, int nc, int64_t ldx,
+                                                    const uint8_t* __restrict__ mask, int64_t ldm,
+                                                    int order, int method, CrbConsts k,
+                                                    float* out, int64_t ldo) {
+  constexpr int EPL = 8;
+  const int r = threadIdx.x % LPR;
+  const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
+  if (row >= R) return;                      // whole lane groups leave together
+  float v[EPL], o[EPL];
+  bool m[EPL];
+  const float* xr = x + (int64_t)row * ldx;
+  const uint8_t* mr = mask + (int64_t)row * ldm;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c0 = h * 4 * LPR + r * 4;
+    if (c0 + 3 < nc) {
+      const float4 q = *(const float4*)(xr + c0);
+      const unsigned mb = *(const unsigned*)(mr + c0);
+      v[4 * h] = q.x; v[4 * h + 1] = q.y; v[4 * h + 2] = q.z; v[4 * h + 3] = q.w;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) m[4 * h + j] = ((mb >> (8 * j)) & 0xFF) != 0;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = c0 + j < nc;
+        v[4 * h + j] = ok ? xr[c0 + j] : 0.f;
+        m[4 * h + j] = ok && mr[c0 + j] != 0;
+      }
+    }
+  }
+  binarize_row<EPL, LPR>(method, v, m, order, k, o);
+  float* orow = out + (int64_t)row * ldo;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c0 = h * 4 * LPR + r * 4;
+    if (c0 + 3 < nc) {
+      *(float4*)(orow + c0) = make_float4(o[4 * h], o[4 * h + 1], o[4 * h + 2], o[4 * h + 3]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (c0 + j < nc) orow[c0 + j] = o[4 * h + j];
+    }
+  }
+}
 }  // namespace crbq
 
 extern "C" int crbq_binarize(const float* x, int64_t R, int32_t ncols, int64_t ldx,
@@ -1221,8 +1271,22 @@ extern "C" int crbq_binarize(const float* x, int64_t R, int32_t ncols, int64_t l
   k.skip = false;
   k.iters = refine_iters;
   hipStream_t hs = (hipStream_t)stream;
-  const unsigned g = (unsigned)cdiv(R, 4);
   const int r = (int)R;
+  const bool vec = ((uintptr_t)x % 16 == 0) && ((uintptr_t)out % 16 == 0) && ldx % 4 == 0 &&
+                   ldo % 4 == 0 && ((uintptr_t)mask % 4 == 0) && ldm % 4 == 0;
+  if (vec && ncols <= 128) {
+    k_binarize_g<16><<<(unsigned)cdiv(R, 16), 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order,
+                                                          method, k, out, ldo);
+    CRBQ_LAUNCH_CHECK();
+    return CRBQ_OK;
+  }
+  if (vec && ncols <= 256) {
+    k_binarize_g<32><<<(unsigned)cdiv(R, 8), 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order,
+                                                         method, k, out, ldo);
+    CRBQ_LAUNCH_CHECK();
+    return CRBQ_OK;
+  }
+  const unsigned g = (unsigned)cdiv(R, 4);
   if (ncols <= 128) k_binarize<2><<<g, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, out, ldo);
   else if (ncols <= 256) k_binarize<4><<<g, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, out, ldo);
   else if (ncols <= 512) k_binarize<8><<<g, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, out, ldo);

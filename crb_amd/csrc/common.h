@@ -29,18 +29,86 @@ __device__ __forceinline__ float tsign(float x) {
 // torch.clamp(x, min=0): NaN propagates.
 __device__ __forceinline__ float clamp0(float x) { return x < 0.f ? 0.f : x; }
 
-// Butterfly sum over the 64 lanes of a wavefront.  Every lane ends with the
-// bitwise-same value (each level adds two commuted operands).
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, CRBQ_WAVE);
-  return v;
+// Sum over the 64 lanes of a wavefront without the LDS crossbar: DPP
+// quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror and row_mirror
+// within each 16-lane row, then v_permlane16_swap (rows 0<->1, 2<->3) and
+// v_permlane32_swap (lanes 0-31 <-> 32-63).  Every lane ends with the
+// bitwise-same value: a DPP level adds commuted operand pairs (lane i adds
+// v_j, lane j adds v_i, with all lanes of the partner group already equal),
+// and a swap level returns (lower-group value, upper-group value) in the
+// same order to both lanes of a pair.
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp_u32(unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
 }
-__device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, CRBQ_WAVE);
-  return v;
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+typedef unsigned u2_t __attribute__((ext_vector_type(2)));
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const unsigned lo = dpp_u32<CTRL>((unsigned)b), hi = dpp_u32<CTRL>((unsigned)(b >> 32));
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
 }
+// (value of the lower lane group, value of the upper group) of a pair
+__device__ __forceinline__ void swap16_f64(double v, double& a, double& b) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  const u2_t lo = __builtin_amdgcn_permlane16_swap((unsigned)u, (unsigned)u, false, false);
+  const u2_t hi =
+      __builtin_amdgcn_permlane16_swap((unsigned)(u >> 32), (unsigned)(u >> 32), false, false);
+  a = __builtin_bit_cast(double, ((unsigned long long)hi.x << 32) | lo.x);
+  b = __builtin_bit_cast(double, ((unsigned long long)hi.y << 32) | lo.y);
+}
+__device__ __forceinline__ void swap32_f64(double v, double& a, double& b) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  const u2_t lo = __builtin_amdgcn_permlane32_swap((unsigned)u, (unsigned)u, false, false);
+  const u2_t hi =
+      __builtin_amdgcn_permlane32_swap((unsigned)(u >> 32), (unsigned)(u >> 32), false, false);
+  a = __builtin_bit_cast(double, ((unsigned long long)hi.x << 32) | lo.x);
+  b = __builtin_bit_cast(double, ((unsigned long long)hi.y << 32) | lo.y);
+}
+
+// Sum over aligned groups of LPR lanes (2, 4, 8, 16, 32 or 64): the first
+// log2(LPR) levels of the sequence above.
+template <int LPR>
+__device__ __forceinline__ double group_sum(double v) {
+  static_assert(LPR == 2 || LPR == 4 || LPR == 8 || LPR == 16 || LPR == 32 || LPR == 64, "LPR");
+  v = v + dpp_f64<DPP_XOR1>(v);
+  if (LPR == 2) return v;
+  v = v + dpp_f64<DPP_XOR2>(v);
+  if (LPR == 4) return v;
+  v = v + dpp_f64<DPP_HALF_MIRROR>(v);
+  if (LPR == 8) return v;
+  v = v + dpp_f64<DPP_MIRROR>(v);
+  if (LPR == 16) return v;
+  double a, b;
+  swap16_f64(v, a, b);
+  v = a + b;
+  if (LPR == 32) return v;
+  swap32_f64(v, a, b);
+  return a + b;
+}
+template <int LPR>
+__device__ __forceinline__ float group_sum_f(float v) {
+  static_assert(LPR == 2 || LPR == 4 || LPR == 8 || LPR == 16 || LPR == 32 || LPR == 64, "LPR");
+  auto f = [](unsigned u) { return __builtin_bit_cast(float, u); };
+  auto u = [](float x) { return __builtin_bit_cast(unsigned, x); };
+  v = v + f(dpp_u32<DPP_XOR1>(u(v)));
+  if (LPR == 2) return v;
+  v = v + f(dpp_u32<DPP_XOR2>(u(v)));
+  if (LPR == 4) return v;
+  v = v + f(dpp_u32<DPP_HALF_MIRROR>(u(v)));
+  if (LPR == 8) return v;
+  v = v + f(dpp_u32<DPP_MIRROR>(u(v)));
+  if (LPR == 16) return v;
+  u2_t s = __builtin_amdgcn_permlane16_swap(u(v), u(v), false, false);
+  v = f(s.x) + f(s.y);
+  if (LPR == 32) return v;
+  s = __builtin_amdgcn_permlane32_swap(u(v), u(v), false, false);
+  return f(s.x) + f(s.y);
+}
+__device__ __forceinline__ double wave_sum(double v) { return group_sum<64>(v); }
+__device__ __forceinline__ float wave_sum_f(float v) { return group_sum_f<64>(v); }
 
 // Align a workspace carve-out to 256 bytes.
 struct WsCarver {

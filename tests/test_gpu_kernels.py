@@ -347,6 +347,26 @@ def test_binarize_random_vs_oracle(method):
             assert float(bad.float().mean()) <= 2e-3, (R, nc, order)
 
 
+@pytest.mark.parametrize("method", BIN_METHODS)
+def test_binarize_lane_groups_vs_oracle(method):
+    """The 16- and 32-lane-per-row kernel (rows of <= 256 columns with
+    16-byte aligned rows): full, ragged (100, 200 columns) and strided rows,
+    row counts that leave part of the last workgroup empty."""
+    print(f"binarize lane groups {method}", flush=True)
+    g = torch.Generator().manual_seed(23)
+    for R, nc, ld in [(33, 100, 100), (17, 200, 200), (5, 128, 128), (70, 256, 256),
+                      (50, 128, 384), (9, 64, 64)]:
+        big = torch.randn(R, ld, generator=g) * 0.02
+        x = big[:, ld - nc:] if ld > nc else big       # 16-byte aligned column offset
+        m = torch.rand(R, nc, generator=g) < 0.7
+        for order in (1, 2):
+            want = O.binarize(method, x, m, order)
+            got = _k().binarize(big.to(DEV)[:, ld - nc:], m.to(DEV), order, method).cpu()
+            tol = 1e-5 * float(x.abs().max())
+            bad = (got - want).abs() > tol
+            assert float(bad.float().mean()) <= 2e-3, (R, nc, ld, order)
+
+
 # ---------------------------------------------------------------------------
 def test_block_search_matches_reference_golden(golden):
     """structural_searching on the reference-written blocks: T is passed as W
