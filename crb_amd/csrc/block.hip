@@ -256,6 +256,7 @@ __global__ __launch_bounds__(CS_THREADS) void k_colscore(
 #define CRBQ_PA_WAVES 16
 #endif
 constexpr int PA_WAVES = CRBQ_PA_WAVES;
+constexpr int PA2_WAVES = 8;    // wavefronts per workgroup of the two-rows-per-wavefront form
 
 struct GroupA {         // per-lane accumulators of one group
   double ad, e1, e2;
@@ -362,44 +363,59 @@ __device__ __forceinline__ void pass_res(const float* xs, int c0, int c1, int i,
   Cg.e2 += (double)p2C;
 }
 
-__global__ __launch_bounds__(64 * PA_WAVES) void k_phase_a(
+// One wavefront per row (TWO = false: lane i-1 evaluates candidate i, up to
+// 64 candidates) or per two rows (TWO = true, at most 32 candidates: lanes
+// 0-31 and 32-63 each hold one row's candidates, so no lane idles on the
+// reference's default up_lim = 30).  NW wavefronts per workgroup.
+template <int NW, bool TWO>
+__global__ __launch_bounds__(64 * NW) void k_phase_a(
     const float* __restrict__ W, int64_t ldw, int R, int nc,
     const float* __restrict__ U, int64_t ldu, int metric, int ncand, int up_lim, SearchWs s,
     crbq_block_trace* tr) {
-  __shared__ float xs[PA_WAVES][NCMAX];
-  __shared__ double errs[PA_WAVES][64];
-  __shared__ double red[PA_WAVES][UPMAX];
+  constexpr int RPW = TWO ? 2 : 1;               // rows per wavefront
+  constexpr int XS = NCMAX + 4;                  // row stride: 16-byte aligned, rows 4 banks apart
+  constexpr int GL = 64 / RPW;                   // lanes per row group
+  __shared__ __attribute__((aligned(16))) float xs[NW * RPW][XS];
+  __shared__ double errs[NW][64];
+  __shared__ double red[NW][UPMAX];
   __shared__ double e[UPMAX];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int h = TWO ? lane >> 5 : 0, gl = lane & (GL - 1);
   const int c0 = lane, c1 = lane + 64;
   const int rk0 = c0 < nc ? s.rank[c0] : -1, rk1 = c1 < nc ? s.rank[c1] : -1;
   float d20 = 1.f, d21 = 1.f;
   if (c0 < nc) { const float dg = U[(int64_t)c0 * ldu + c0]; d20 = dg * dg; }
   if (c1 < nc) { const float dg = U[(int64_t)c1 * ldu + c1]; d21 = dg * dg; }
-  const int i = lane + 1;                        // candidate (salient columns)
+  const int i = gl + 1;                          // candidate (salient columns)
   const float nS = (float)i, nC = (float)(nc - i);
   const int mix_end = min(nc, ncand);            // ranks >= ncand are never salient
   double acc = 0.0;
-  for (int r0 = blockIdx.x * PA_WAVES; r0 < R; r0 += gridDim.x * PA_WAVES) {
-    const int row = r0 + wv;
-    float* x = xs[wv];
-    __syncthreads();                             // previous row's readers are done
-    if (row < R) {
-      if (rk0 >= 0) x[rk0] = target_of(W[(int64_t)row * ldw + c0], d20, metric);
-      if (rk1 >= 0) x[rk1] = target_of(W[(int64_t)row * ldw + c1], d21, metric);
+  for (int r0 = blockIdx.x * NW * RPW; r0 < R; r0 += gridDim.x * NW * RPW) {
+    __syncthreads();                             // previous rows' readers are done
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+      const int rq = r0 + wv * RPW + q;
+      float* xq = xs[wv * RPW + q];
+      if (rq < R) {
+        if (rk0 >= 0) xq[rk0] = target_of(W[(int64_t)rq * ldw + c0], d20, metric);
+        if (rk1 >= 0) xq[rk1] = target_of(W[(int64_t)rq * ldw + c1], d21, metric);
+      }
     }
     __syncthreads();
+    const int row = r0 + wv * RPW + h;
+    const float* x = xs[wv * RPW + h];
     if (row < R) {
       // prefix sums in rank order: candidate i's salient group is ranks [0, i)
-      const double y0 = lane < nc ? (double)x[lane] : 0.0;
-      const double y1 = lane + 64 < nc ? (double)x[lane + 64] : 0.0;
-      double ps = y0;
+      double ps = gl < nc ? (double)x[gl] : 0.0;
+      double rest = 0.0;
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
+      for (int k = 1; k < 128 / GL; ++k) rest += gl + k * GL < nc ? (double)x[gl + k * GL] : 0.0;
+      const double tot = group_sum<GL>(ps + rest);
+#pragma unroll
+      for (int o = 1; o < GL; o <<= 1) {
         const double t = __shfl_up(ps, o, CRBQ_WAVE);
-        if (lane >= o) ps += t;
+        if (gl >= o) ps += t;
       }
-      const double tot = wave_sum(y0 + y1);
       const float m1S = (float)ps / nS;
       const float m1C = nC > 0.f ? (float)(tot - ps) / nC : 0.f;
       GroupA S = {0.0, 0.0, 0.0, 0, 0, 0}, Cg = {0.0, 0.0, 0.0, 0, 0, 0};
@@ -430,11 +446,14 @@ __global__ __launch_bounds__(64 * PA_WAVES) void k_phase_a(
   if (tid < ncand) {
     double v = 0.0;
 #pragma unroll
-    for (int w = 0; w < PA_WAVES; ++w) v += errs[w][tid];
+    for (int w = 0; w < NW; ++w) {
+      v += errs[w][tid];
+      if (TWO) v += errs[w][tid + 32];
+    }
     s.parta[(size_t)blockIdx.x * UPMAX + tid] = v;
   }
   if (!last_block(&s.ctrl->cnt[CNT_A])) return;
-  reduce_partials<UPMAX, PA_WAVES>(s.parta, UPMAX, gridDim.x, ncand, red, e);
+  reduce_partials<UPMAX, NW>(s.parta, UPMAX, gridDim.x, ncand, red, e);
   if (tid == 0) {
     double best = INFINITY;
     int istar = max(1, up_lim / 3);                                  // :43
@@ -971,11 +990,16 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
   const int ncand = up_lim - 1;
   const int nwg_cs = (int)std::min<int64_t>(cdiv(R, CS_PH), CS_MAXWG);
   const int nwg_q = (int)cdiv(R, Q_RPW);
-  const int nwg_a = (int)std::min<int64_t>(cdiv(R, PA_WAVES), PX_MAXWG);
+  const bool two = ncand <= 32;
+  const int nwg_a = (int)std::min<int64_t>(cdiv(R, two ? 2 * PA2_WAVES : PA_WAVES), PX_MAXWG);
   const int nwg_c = (int)std::min<int64_t>(cdiv(R, PC_WAVES), PX_MAXWG);
   k_colscore<<<nwg_cs, CS_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  k_phase_a<<<nwg_a, 64 * PA_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric, ncand, up_lim, s,
-                                              tr);
+  if (two)
+    k_phase_a<PA2_WAVES, true><<<nwg_a, 64 * PA2_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric,
+                                                                 ncand, up_lim, s, tr);
+  else
+    k_phase_a<PA_WAVES, false><<<nwg_a, 64 * PA_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric,
+                                                                ncand, up_lim, s, tr);
   k_qpass1<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_qscan1<<<1, 256, 0, st>>>((int64_t)R * nc, s);
   k_qpass2<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);

@@ -398,3 +398,24 @@ def test_block_search_matches_reference_golden(golden):
         assert float(gt["split"]).hex() == c["split_hex"] or \
             abs(gt["split"] - c["split"]) <= 1e-6 * abs(c["split"])
         np.testing.assert_array_equal((masks.cpu() == 3).numpy(), A[f"search{i}_m3"])
+
+
+@pytest.mark.parametrize("R,up_lim", [(64, 30), (37, 30), (1, 30), (300, 33), (130, 12)])
+def test_block_search_two_rows_per_wave_vs_oracle(R, up_lim):
+    """Salient-count candidates of two rows per wavefront (up_lim - 1 <= 32,
+    the reference's default up_lim = 30): per-candidate errors, i* and the
+    salient columns against the oracle, with row counts that leave half a
+    wavefront empty."""
+    print(f"search two rows R={R} up_lim={up_lim}", flush=True)
+    g = torch.Generator().manual_seed(R + up_lim)
+    T = torch.randn(R, 128, generator=g) * torch.exp(torch.randn(128, generator=g))
+    tr = O.SearchTrace()
+    _, m3_o = O.structural_searching(T, up_lim, trace=tr)
+    U = torch.eye(128, device=DEV)
+    masks, gt = _k().block_search(T.to(DEV), U, metric="magnitude", up_lim=up_lim)
+    torch.cuda.synchronize()
+    ea = np.asarray(gt["errs_a"][1:up_lim]) / T.numel()
+    eo = np.asarray(tr.errs_a)
+    assert np.max(np.abs(ea - eo) / np.abs(eo)) < 1e-4
+    assert gt["i_star"] == tr.i_star
+    np.testing.assert_array_equal((masks.cpu() == 3).numpy(), m3_o.numpy())
