@@ -780,31 +780,90 @@ __device__ double group_err1(const SortedRow& r, int l1, int h1, int l2, int h2)
   return err;
 }
 
+// Partner value of a xor-j exchange inside the wavefront, without the LDS
+// crossbar.  For j = 16, 32 the permlane swap returns {own, partner} in some
+// order, which is all a compare-exchange needs (min and max of the pair).
+template <int J>
+__device__ __forceinline__ void xchg_pair(float x, float& a, float& b) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const int lane = threadIdx.x & 63;
+  if (J == 1) {
+    a = x; b = __builtin_bit_cast(float, dpp_u32<DPP_XOR1>(u));
+  } else if (J == 2) {
+    a = x; b = __builtin_bit_cast(float, dpp_u32<DPP_XOR2>(u));
+  } else if (J == 4 || J == 8) {
+    // row_shl:J brings lane + J, row_shr:J lane - J (rows of 16 lanes)
+    const float up = __builtin_bit_cast(float, dpp_u32<0x100 + J>(u));
+    const float dn = __builtin_bit_cast(float, dpp_u32<0x110 + J>(u));
+    a = x; b = (lane & J) ? dn : up;
+  } else {
+    unsigned p = u, q = u;
+    if (J == 16) permlane16_swap(p, q);
+    else permlane32_swap(p, q);
+    a = __builtin_bit_cast(float, p); b = __builtin_bit_cast(float, q);
+  }
+}
+
+template <int J>
+__device__ __forceinline__ void bitonic_step(float& x0, float& x1, int k) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int slot = 0; slot < 2; ++slot) {
+    float& x = slot ? x1 : x0;
+    const int pos = lane + 64 * slot;
+    float a, b;
+    xchg_pair<J>(x, a, b);
+    const bool up = ((pos & k) == 0);
+    const bool lower = (pos & J) == 0;
+    x = (lower == up) ? fminf(a, b) : fmaxf(a, b);
+  }
+}
+
 // bitonic sort of 128 values held 2 per lane (position lane + 64*slot)
 __device__ __forceinline__ void wave_sort128(float& x0, float& x1) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int k = 2; k <= 128; k <<= 1) {
-#pragma unroll
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      if (j == 64) {                       // partner is the other slot of this lane
-        const bool up = ((lane & k) == 0);  // k == 128: always ascending
-        const float a = fminf(x0, x1), b = fmaxf(x0, x1);
-        x0 = up ? a : b;
-        x1 = up ? b : a;
-      } else {
-#pragma unroll
-        for (int slot = 0; slot < 2; ++slot) {
-          float& x = slot ? x1 : x0;
-          const int pos = lane + 64 * slot;
-          const float y = __shfl_xor(x, j, CRBQ_WAVE);
-          const bool up = ((pos & k) == 0);
-          const bool lower = (pos & j) == 0;
-          x = (lower == up) ? fminf(x, y) : fmaxf(x, y);
-        }
-      }
+    if (k >= 128) {                          // partner is the other slot of this lane
+      const float a = fminf(x0, x1), b = fmaxf(x0, x1);
+      x0 = a;
+      x1 = b;
     }
+    if (k >= 64) bitonic_step<32>(x0, x1, k);
+    if (k >= 32) bitonic_step<16>(x0, x1, k);
+    if (k >= 16) bitonic_step<8>(x0, x1, k);
+    if (k >= 8) bitonic_step<4>(x0, x1, k);
+    if (k >= 4) bitonic_step<2>(x0, x1, k);
+    bitonic_step<1>(x0, x1, k);
   }
+  (void)lane;
+}
+
+// inclusive fp64 scan over the 64 lanes: row_shr 1, 2, 4, 8 inside rows of
+// 16 (zero fill), then row_bcast15 / row_bcast31 carry the row totals
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_f64_rows(double v) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, ROWS, 0xF,
+                                                            true);
+  const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL,
+                                                            ROWS, 0xF, true);
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ double wave_scan_f64(double v) {
+  v = v + dpp_f64_rows<0x111, 0xF>(v);       // row_shr:1
+  v = v + dpp_f64_rows<0x112, 0xF>(v);       // row_shr:2
+  v = v + dpp_f64_rows<0x114, 0xF>(v);       // row_shr:4
+  v = v + dpp_f64_rows<0x118, 0xF>(v);       // row_shr:8
+  v = v + dpp_f64_rows<0x142, 0xA>(v);       // row_bcast:15 into rows 1, 3
+  v = v + dpp_f64_rows<0x143, 0xC>(v);       // row_bcast:31 into rows 2, 3
+  return v;
+}
+__device__ __forceinline__ double lane63_f64(double v) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const unsigned lo = __builtin_amdgcn_readlane((unsigned)b, 63);
+  const unsigned hi = __builtin_amdgcn_readlane((unsigned)(b >> 32), 63);
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
 }
 
 // exclusive fp64 prefix sums of the sorted row into r.S / r.Q
@@ -812,13 +871,11 @@ __device__ __forceinline__ void wave_prefix(SortedRow& r, float x0, float x1, in
   const int lane = threadIdx.x & 63;
   double s0 = lane < n ? (double)x0 : 0.0, s1 = lane + 64 < n ? (double)x1 : 0.0;
   double q0 = s0 * s0, q1 = s1 * s1;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {       // inclusive scans within each slot
-    const double a = __shfl_up(s0, o, CRBQ_WAVE), b = __shfl_up(s1, o, CRBQ_WAVE);
-    const double c = __shfl_up(q0, o, CRBQ_WAVE), d = __shfl_up(q1, o, CRBQ_WAVE);
-    if (lane >= o) { s0 += a; s1 += b; q0 += c; q1 += d; }
-  }
-  const double tS = __shfl(s0, 63, CRBQ_WAVE), tQ = __shfl(q0, 63, CRBQ_WAVE);
+  s0 = wave_scan_f64(s0);
+  s1 = wave_scan_f64(s1);
+  q0 = wave_scan_f64(q0);
+  q1 = wave_scan_f64(q1);
+  const double tS = lane63_f64(s0), tQ = lane63_f64(q0);
   s1 += tS;
   q1 += tQ;
   r.S[lane + 1] = s0;

@@ -42,7 +42,21 @@ __device__ __forceinline__ unsigned dpp_u32(unsigned v) {
   return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
 }
 constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
-typedef unsigned u2_t __attribute__((ext_vector_type(2)));
+
+// v_permlane16_swap_b32 / v_permlane32_swap_b32 on the pair (a, b) (a is
+// VDST, b is SRC0): after the swap, with a = b = v on entry, every lane holds
+// in a the value of the lower lane group of its pair (rows 0/2 for 16, lanes
+// 0-31 for 32) and in b the value of the upper group.  Issued as inline
+// assembly: the compiler's optimizer folds the builtins' second result into
+// the first when they are used as floats, which is wrong across lanes.  The
+// s_nop guards cover the VALU-write -> permlane-read hazard and a DPP read
+// of the results, which the hazard recognizer does not see inside asm.
+__device__ __forceinline__ void permlane16_swap(unsigned& a, unsigned& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane32_swap(unsigned& a, unsigned& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
 
 template <int CTRL>
 __device__ __forceinline__ double dpp_f64(double v) {
@@ -51,21 +65,20 @@ __device__ __forceinline__ double dpp_f64(double v) {
   return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
 }
 // (value of the lower lane group, value of the upper group) of a pair
-__device__ __forceinline__ void swap16_f64(double v, double& a, double& b) {
+template <bool W32>
+__device__ __forceinline__ void swap_f64(double v, double& a, double& b) {
   const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
-  const u2_t lo = __builtin_amdgcn_permlane16_swap((unsigned)u, (unsigned)u, false, false);
-  const u2_t hi =
-      __builtin_amdgcn_permlane16_swap((unsigned)(u >> 32), (unsigned)(u >> 32), false, false);
-  a = __builtin_bit_cast(double, ((unsigned long long)hi.x << 32) | lo.x);
-  b = __builtin_bit_cast(double, ((unsigned long long)hi.y << 32) | lo.y);
+  unsigned la = (unsigned)u, lb = (unsigned)u, ha = (unsigned)(u >> 32), hb = ha;
+  if (W32) { permlane32_swap(la, lb); permlane32_swap(ha, hb); }
+  else { permlane16_swap(la, lb); permlane16_swap(ha, hb); }
+  a = __builtin_bit_cast(double, ((unsigned long long)ha << 32) | la);
+  b = __builtin_bit_cast(double, ((unsigned long long)hb << 32) | lb);
+}
+__device__ __forceinline__ void swap16_f64(double v, double& a, double& b) {
+  swap_f64<false>(v, a, b);
 }
 __device__ __forceinline__ void swap32_f64(double v, double& a, double& b) {
-  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
-  const u2_t lo = __builtin_amdgcn_permlane32_swap((unsigned)u, (unsigned)u, false, false);
-  const u2_t hi =
-      __builtin_amdgcn_permlane32_swap((unsigned)(u >> 32), (unsigned)(u >> 32), false, false);
-  a = __builtin_bit_cast(double, ((unsigned long long)hi.x << 32) | lo.x);
-  b = __builtin_bit_cast(double, ((unsigned long long)hi.y << 32) | lo.y);
+  swap_f64<true>(v, a, b);
 }
 
 // Sum over aligned groups of LPR lanes (2, 4, 8, 16, 32 or 64): the first
@@ -101,11 +114,14 @@ __device__ __forceinline__ float group_sum_f(float v) {
   if (LPR == 8) return v;
   v = v + f(dpp_u32<DPP_MIRROR>(u(v)));
   if (LPR == 16) return v;
-  u2_t s = __builtin_amdgcn_permlane16_swap(u(v), u(v), false, false);
-  v = f(s.x) + f(s.y);
+  unsigned a = u(v), b = a;
+  permlane16_swap(a, b);
+  v = f(a) + f(b);
   if (LPR == 32) return v;
-  s = __builtin_amdgcn_permlane32_swap(u(v), u(v), false, false);
-  return f(s.x) + f(s.y);
+  a = u(v);
+  b = a;
+  permlane32_swap(a, b);
+  return f(a) + f(b);
 }
 __device__ __forceinline__ double wave_sum(double v) { return group_sum<64>(v); }
 __device__ __forceinline__ float wave_sum_f(float v) { return group_sum_f<64>(v); }
