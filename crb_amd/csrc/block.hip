@@ -1033,6 +1033,107 @@ __global__ __launch_bounds__(256) void k_quantize(QuantArgs a, SearchWs s) {
   }
 }
 
+// k_quantize for blocks of at most 128 columns with 16 lanes per row (16
+// rows per workgroup), 8 elements per lane at columns 4r .. 4r+3 and
+// 64 + 4r .. 64 + 4r+3, 16-byte loads and stores (W, err and their row
+// strides 16-byte aligned, masks 4-byte aligned; the host checks).
+__global__ __launch_bounds__(256) void k_quantize_g(QuantArgs a, SearchWs s) {
+  constexpr int EPL = 8, LPR = 16;
+  const int r = threadIdx.x % LPR;
+  const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
+  if (row >= a.R) return;                    // whole lane groups leave together
+  const int istar = a.partition == 3 ? s.ctrl->istar : 0;
+  const float split = a.partition == 3 ? s.ctrl->split : 0.f;
+  float x[EPL], dd[EPL];
+  int grp[EPL];
+  bool valid[EPL];
+  float* wr = a.W + (int64_t)row * a.ldw;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c0 = h * 64 + r * 4;
+    if (c0 + 3 < a.nc) {
+      const float4 q = *(const float4*)(wr + c0);
+      x[4 * h] = q.x; x[4 * h + 1] = q.y; x[4 * h + 2] = q.z; x[4 * h + 3] = q.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[4 * h + j] = c0 + j < a.nc ? wr[c0 + j] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int c = (e >> 2) * 64 + r * 4 + (e & 3);
+    valid[e] = c < a.nc;
+    dd[e] = valid[e] ? a.U[(int64_t)c * a.ldu + c] : 1.f;
+    int g = -1;
+    if (valid[e]) {
+      if (a.partition != 3) g = 0;
+      else if (s.rank[c] < istar) g = 2;
+      else {
+        const float t = fabsf(target_of(x[e], dd[e] * dd[e], a.metric));
+        g = t >= split ? 1 : 0;
+      }
+    }
+    grp[e] = g;
+  }
+  float q[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) q[e] = 0.f;
+  const int ngroups = a.partition == 3 ? 3 : 1;
+  for (int g = 0; g < ngroups; ++g) {
+    bool m[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) m[e] = grp[e] == g;
+    float out[EPL];
+    binarize_row<EPL, LPR>(a.method, x, m, a.orders[g], a.k, out);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) if (m[e]) q[e] = out[e];
+  }
+  double lsum = 0.0;
+  float ev[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    ev[e] = 0.f;
+    if (!valid[e]) continue;
+    const float w = x[e], d = dd[e];
+    const float df = w - q[e];
+    if (a.gptq) {
+      const float d2 = d * d;
+      const float l = (df * df) / d2;
+      lsum += (double)l;
+      ev[e] = df / d;
+    }
+  }
+  float* er = a.err + (int64_t)row * a.lde;
+  uint8_t* mr = a.masks ? a.masks + (int64_t)row * a.ldm : nullptr;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c0 = h * 64 + r * 4;
+    if (c0 + 3 < a.nc) {
+      *(float4*)(wr + c0) = make_float4(q[4 * h], q[4 * h + 1], q[4 * h + 2], q[4 * h + 3]);
+      if (a.gptq)
+        *(float4*)(er + c0) = make_float4(ev[4 * h], ev[4 * h + 1], ev[4 * h + 2], ev[4 * h + 3]);
+      if (mr) {
+        unsigned mb = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mb |= (unsigned)(grp[4 * h + j] + 1) << (8 * j);
+        *(unsigned*)(mr + c0) = mb;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (c0 + j >= a.nc) continue;
+        wr[c0 + j] = q[4 * h + j];
+        if (a.gptq) er[c0 + j] = ev[4 * h + j];
+        if (mr) mr[c0 + j] = (uint8_t)(grp[4 * h + j] + 1);
+      }
+    }
+  }
+  if (a.gptq) {
+    const float tot = (float)group_sum<LPR>(lsum);
+    if (r == 0) a.losses[row] = a.losses[row] + tot / 2.f;
+  }
+}
+
 // clears the arrival counters of the last-workgroup reductions
 __global__ void k_init_ctrl(SearchWs s) {
   if (threadIdx.x < 4) s.ctrl->cnt[threadIdx.x] = 0u;
@@ -1239,7 +1340,13 @@ extern "C" int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw, con
       a.err = err + (st0 - sb0); a.lde = SB;
       a.losses = losses;
       a.masks = masks ? masks + st0 : nullptr; a.ldm = ldm;
-      k_quantize<2><<<(unsigned)cdiv(R, 4), 256, 0, hs>>>(a, s);
+      const bool vec = ((uintptr_t)Wb % 16 == 0) && ldw % 4 == 0 &&
+                       ((uintptr_t)a.err % 16 == 0) && a.lde % 4 == 0 &&
+                       (!a.masks || (((uintptr_t)a.masks % 4 == 0) && ldm % 4 == 0));
+      if (vec && nc <= 128)
+        k_quantize_g<<<(unsigned)cdiv(R, 16), 256, 0, hs>>>(a, s);
+      else
+        k_quantize<2><<<(unsigned)cdiv(R, 4), 256, 0, hs>>>(a, s);
       CRBQ_LAUNCH_CHECK();
       const int64_t ed = st0 + nc;
       if (gptq && ed < sb1) {            // rest of this super-block
