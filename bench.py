@@ -233,7 +233,8 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
     * one block step (salient/split search + binarize + in-block error
       feedback, crbq_fasterquant on a 4096 x 128 block): its algorithmic
       bytes (W block in, U block in, Q, Err and masks out) against HBM;
-    * the whole fc2 block loop alone (128 blocks, with trailing updates)."""
+    * the whole fc2 block loop alone (128 blocks, with trailing updates),
+      and fc1's (16384 x 4096, 32 blocks)."""
     from crb_amd import _lib, kernels
     g = torch.Generator(device=dev)
     g.manual_seed(11)
@@ -292,6 +293,20 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
     ms = _ev_ms(loop, 2)
     out["block_loop_fc2_alone_ms"] = round(ms, 3)
     del W, Wbig, U
+    # fc1's shape: 16384 rows x 4096 columns, 32 blocks
+    R1, C1 = 4 * R, C // 4
+    W1 = torch.randn(R1, C1, device=dev, generator=g) * 0.02
+    U1 = torch.triu(torch.randn(C1, C1, device=dev, generator=g) * 1e-3)
+    U1.diagonal().add_(1.0)
+    L1 = torch.zeros(R1, device=dev)
+    Wq = W1.clone()
+
+    def loop1():
+        Wq.copy_(W1)
+        kernels.fasterquant_blocks(Wq, U1, p, L1, want_masks=False)
+
+    out["block_loop_fc1_alone_ms"] = round(_ev_ms(loop1, 2), 3)
+    del W1, U1, Wq
     torch.cuda.empty_cache()
     return out
 
