@@ -887,6 +887,105 @@ __device__ __forceinline__ void wave_prefix(SortedRow& r, float x0, float x1, in
   r.v[lane + 64] = x1;
 }
 
+// Salient-count candidates as (row, candidate) pairs when 32 < ncand <= 64:
+// PF_RB rows per workgroup iteration, thread f evaluates row f / ncand with
+// candidate f % ncand + 1, so only the tail of the last wavefront idles
+// (the reference's up_lim = 50: 784 pairs on 13 wavefronts instead of 16
+// wavefronts with 15 idle lanes each).  Same per-pair arithmetic as
+// k_phase_a, with the rank-order prefix sums of each row staged in LDS.
+constexpr int PF_RB = 16;
+__global__ __launch_bounds__(1024) void k_phase_a_pairs(
+    const float* __restrict__ W, int64_t ldw, int R, int nc,
+    const float* __restrict__ U, int64_t ldu, int metric, int ncand, int up_lim, SearchWs s,
+    crbq_block_trace* tr) {
+  constexpr int XS = NCMAX + 4;
+  __shared__ __attribute__((aligned(16))) float xs[PF_RB][XS];
+  __shared__ double pre[PF_RB][NCMAX + 1];   // pre[q][k]: sum of ranks [0, k) of row q
+  __shared__ double errs[1024];
+  __shared__ double red[8][UPMAX];
+  __shared__ double e[UPMAX];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
+  const bool act = tid < PF_RB * ncand;
+  const int q = act ? tid / ncand : 0;
+  const int i = act ? tid % ncand + 1 : 1;   // candidate (salient columns)
+  const int c0 = lane, c1 = lane + 64;
+  const int rk0 = c0 < nc ? s.rank[c0] : -1, rk1 = c1 < nc ? s.rank[c1] : -1;
+  float d20 = 1.f, d21 = 1.f;
+  if (c0 < nc) { const float dg = U[(int64_t)c0 * ldu + c0]; d20 = dg * dg; }
+  if (c1 < nc) { const float dg = U[(int64_t)c1 * ldu + c1]; d21 = dg * dg; }
+  const float nS = (float)i, nC = (float)(nc - i);
+  const int mix_end = min(nc, ncand);
+  double acc = 0.0;
+  for (int r0 = blockIdx.x * PF_RB; r0 < R; r0 += gridDim.x * PF_RB) {
+    __syncthreads();                             // previous rows' readers are done
+    for (int qq = wv; qq < PF_RB; qq += nw) {    // rows in rank order, one wavefront each
+      const int rq = r0 + qq;
+      if (rq < R) {
+        if (rk0 >= 0) xs[qq][rk0] = target_of(W[(int64_t)rq * ldw + c0], d20, metric);
+        if (rk1 >= 0) xs[qq][rk1] = target_of(W[(int64_t)rq * ldw + c1], d21, metric);
+      }
+    }
+    __syncthreads();
+    for (int qq = wv; qq < PF_RB; qq += nw) {    // exclusive prefix sums in rank order
+      if (r0 + qq < R) {
+        const double y0 = lane < nc ? (double)xs[qq][lane] : 0.0;
+        const double y1 = lane + 64 < nc ? (double)xs[qq][lane + 64] : 0.0;
+        const double p0 = wave_scan_f64(y0);
+        const double p1 = wave_scan_f64(y1) + lane63_f64(p0);
+        pre[qq][lane + 1] = p0;
+        pre[qq][lane + 65] = p1;
+        if (lane == 0) pre[qq][0] = 0.0;
+      }
+    }
+    __syncthreads();
+    const int row = r0 + q;
+    if (act && row < R) {
+      const float* x = xs[q];
+      const double ps = pre[q][i], tot = pre[q][nc];
+      const float m1S = (float)ps / nS;
+      const float m1C = nC > 0.f ? (float)(tot - ps) / nC : 0.f;
+      GroupA S = {0.0, 0.0, 0.0, 0, 0, 0}, Cg = {0.0, 0.0, 0.0, 0, 0, 0};
+      pass_abs<true>(x, 0, mix_end, i, m1S, m1C, S, Cg);
+      pass_abs<false>(x, mix_end, nc, i, m1S, m1C, S, Cg);
+      const float a1S = (float)S.ad / nS;
+      const float a1C = nC > 0.f ? (float)Cg.ad / nC : 0.f;
+      float hiS = a1S + m1S, loS = -a1S + m1S, hiC = a1C + m1C, loC = -a1C + m1C;
+      const double s1S = S.npos * (double)hiS + S.nneg * (double)loS +
+                         ((double)nS - S.npos - S.nneg) * (double)m1S;
+      const double s1C = Cg.npos * (double)hiC + Cg.nneg * (double)loC +
+                         ((double)nC - Cg.npos - Cg.nneg) * (double)m1C;
+      const float m2S = (float)(ps - s1S) / nS;
+      const float m2C = nC > 0.f ? (float)((tot - ps) - s1C) / nC : 0.f;
+      const ParA PS = {m1S, hiS, loS, m2S}, PC = {m1C, hiC, loC, m2C};
+      pass_res<true>(x, 0, mix_end, i, PS, PC, S, Cg);
+      pass_res<false>(x, mix_end, nc, i, PS, PC, S, Cg);
+      const double a2S = (double)((float)S.e1 / nS);
+      const double a2C = nC > 0.f ? (double)((float)Cg.e1 / nC) : 0.0;
+      const double eS = S.e2 - 2.0 * a2S * S.e1 + a2S * a2S * (double)S.nz;
+      const double eC = Cg.e2 - 2.0 * a2C * Cg.e1 + a2C * a2C * (double)Cg.nz;
+      acc += eS + eC;
+    }
+  }
+  errs[tid] = acc;
+  __syncthreads();
+  if (tid < ncand) {
+    double v = 0.0;
+    for (int qq = 0; qq < PF_RB; ++qq) v += errs[qq * ncand + tid];
+    s.parta[(size_t)blockIdx.x * UPMAX + tid] = v;
+  }
+  if (!last_block(&s.ctrl->cnt[CNT_A])) return;
+  reduce_partials<UPMAX, 8>(s.parta, UPMAX, gridDim.x, ncand, red, e);
+  if (tid == 0) {
+    double best = INFINITY;
+    int istar = max(1, up_lim / 3);                                  // :43
+    for (int k = 0; k < ncand; ++k)
+      if (e[k] < best) { best = e[k]; istar = k + 1; }
+    s.ctrl->istar = istar;
+    if (tr) tr->i_star = istar;
+  }
+  if (tr && tid < UPMAX) tr->errs_a[tid] = (tid >= 1 && tid <= ncand) ? e[tid - 1] : 0.0;
+}
+
 __global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
     const float* __restrict__ W, int64_t ldw, int R, int nc,
     const float* __restrict__ U, int64_t ldu, int metric, SearchWs s, crbq_block_trace* tr) {
@@ -1149,12 +1248,17 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
   const int nwg_cs = (int)std::min<int64_t>(cdiv(R, CS_PH), CS_MAXWG);
   const int nwg_q = (int)cdiv(R, Q_RPW);
   const bool two = ncand <= 32;
-  const int nwg_a = (int)std::min<int64_t>(cdiv(R, two ? 2 * PA2_WAVES : PA_WAVES), PX_MAXWG);
+  const bool pairs = !two && ncand <= 64;
+  const int nwg_a = (int)std::min<int64_t>(
+      cdiv(R, two ? 2 * PA2_WAVES : (pairs ? PF_RB : PA_WAVES)), PX_MAXWG);
   const int nwg_c = (int)std::min<int64_t>(cdiv(R, PC_WAVES), PX_MAXWG);
   k_colscore<<<nwg_cs, CS_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   if (two)
     k_phase_a<PA2_WAVES, true><<<nwg_a, 64 * PA2_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric,
                                                                  ncand, up_lim, s, tr);
+  else if (pairs)   // wavefronts for PF_RB * ncand pairs (>= 9: reduce_partials uses 512)
+    k_phase_a_pairs<<<nwg_a, 64 * (int)cdiv(PF_RB * ncand, 64), 0, st>>>(
+        W, ldw, R, nc, U, ldu, metric, ncand, up_lim, s, tr);
   else
     k_phase_a<PA_WAVES, false><<<nwg_a, 64 * PA_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric,
                                                                 ncand, up_lim, s, tr);

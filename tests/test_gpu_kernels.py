@@ -400,12 +400,15 @@ def test_block_search_matches_reference_golden(golden):
         np.testing.assert_array_equal((masks.cpu() == 3).numpy(), A[f"search{i}_m3"])
 
 
-@pytest.mark.parametrize("R,up_lim", [(64, 30), (37, 30), (1, 30), (300, 33), (130, 12)])
-def test_block_search_two_rows_per_wave_vs_oracle(R, up_lim):
-    """Salient-count candidates of two rows per wavefront (up_lim - 1 <= 32,
-    the reference's default up_lim = 30): per-candidate errors, i* and the
-    salient columns against the oracle, with row counts that leave half a
-    wavefront empty."""
+@pytest.mark.parametrize("R,up_lim", [(64, 30), (37, 30), (1, 30), (300, 33), (130, 12),
+                                     (37, 50), (1, 50), (300, 64), (1000, 50)])
+def test_block_search_candidate_layouts_vs_oracle(R, up_lim):
+    """Salient-count candidates in both packed layouts: two rows per
+    wavefront (up_lim - 1 <= 32, structural_searching's default up_lim = 30)
+    and (row, candidate) pairs over a workgroup (32 < up_lim - 1 <= 63,
+    bigptq.py's up_lim = 50): per-candidate errors, i* and the salient
+    columns against the oracle, with row counts that leave part of a
+    wavefront or workgroup empty."""
     print(f"search two rows R={R} up_lim={up_lim}", flush=True)
     g = torch.Generator().manual_seed(R + up_lim)
     T = torch.randn(R, 128, generator=g) * torch.exp(torch.randn(128, generator=g))
