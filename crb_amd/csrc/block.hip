@@ -6,10 +6,12 @@
 // -> utils/mask.py:7-18), all on the device with no host round trip:
 //   k_colscore   column scores sum_r |T| (fp64 per-workgroup partials);
 //                the last workgroup ranks the columns (torch.topk order)
-//   k_phase_a    one wavefront per row, one lane per salient candidate i:
-//                order-2 residual binarization error of {top i cols} +
-//                complement (prefix scan + two passes, closed-form error)
-//                the last workgroup takes i* = first strict minimum
+//   k_phase_a    one lane per (row, salient candidate i) -- k_phase_a_pairs
+//                for 33-63 candidates, two rows per wavefront up to 32, one
+//                row per wavefront otherwise: order-2 residual binarization
+//                error of {top i cols} + complement (prefix sums + two
+//                passes, closed-form error); the last workgroup takes
+//                i* = first strict minimum
 //   k_qpass/k_qscan (x3)
 //                exact np.quantile of |T * ~M3| at the 81 float32
 //                percentiles: 3-level MSD radix select (12/10/10 bits of the
