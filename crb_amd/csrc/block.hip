@@ -201,6 +201,7 @@ __global__ __launch_bounds__(CS_THREADS) void k_colscore(
   if (col < nc) {
     const float dg = U[(int64_t)col * ldu + col];
     const float d2 = dg * dg;
+#pragma unroll 4
     for (int r = CS_PH * blockIdx.x + ph; r < R; r += CS_PH * gridDim.x)
       acc += (double)fabsf(target_of(W[(int64_t)r * ldw + col], d2, metric));
   }
