@@ -256,8 +256,10 @@ static int sgemm_go(bool ta, bool tb, bool lower, int64_t M, int64_t N, int64_t 
 }
 
 // Products that give fewer 128 x 128 tiles than the GPU has CUs run on
-// 64 x 64 tiles (4x the workgroups, a quarter of the work each), which
-// shortens the small products of the factorization's lower levels.
+// 64 x 64 tiles (4x the workgroups, a quarter of the work each), and those
+// with fewer than 64 such tiles on 32 x 32 tiles, which shortens the small
+// products of the factorization's lower levels (latency chains of a few
+// workgroups each).
 int sgemm_launch(bool ta, bool tb, bool lower, int64_t M, int64_t N, int64_t K,
                  float alpha, const float* A, int64_t lda, const float* B,
                  int64_t ldb, float beta, float* C, int64_t ldc,
@@ -265,6 +267,10 @@ int sgemm_launch(bool ta, bool tb, bool lower, int64_t M, int64_t N, int64_t K,
   if (M <= 0 || N <= 0) return CRBQ_OK;
   if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30) || K < 0) return CRBQ_ERR_ARG;
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  const int64_t t64 = ((M + 63) / 64) * ((N + 63) / 64);
+  if (t64 < 128)
+    return sgemm_go<32>(ta, tb, lower, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stop, s,
+                        tri);
   if (t128 < 256)
     return sgemm_go<64>(ta, tb, lower, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stop, s,
                         tri);
