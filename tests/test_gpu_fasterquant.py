@@ -152,3 +152,22 @@ def test_fasterquant_multi_superblock():
     assert m["err_rel"] < 1e-3
     assert m["recon_rel"] < 1e-3
     assert m["agree"] >= 0.999
+
+
+@pytest.mark.parametrize("R,C", [(40, 178), (33, 180)])
+def test_fasterquant_ragged_shapes(R, C):
+    """Row strides that are not 16-byte aligned (178 columns: the
+    one-row-per-wavefront binarization kernel) and a ragged last block with
+    a row count that leaves part of a workgroup empty (33 x 180: the
+    16-lane kernel), against the oracle.  The last block is at least
+    up_lim = 50 columns wide, as torch.topk requires."""
+    W = synth.weight(R, C, 11, outlier_frac=0.02)
+    X = synth.calibration(4, 256, C, 12, kind="lognormal")
+    print(f"fasterquant {R}x{C} crb", flush=True)
+    Wg, eg = run_gpu(W, X, "crb")
+    Wr, er, _ = oracle_ref(W, X, "crb")
+    m = compare(W, X, Wg, eg, Wr, er)
+    print("  ", m)
+    assert m["err_rel"] < 1e-3
+    assert m["recon_rel"] < 1e-3
+    assert m["agree"] >= 0.999
