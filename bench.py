@@ -311,13 +311,73 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
     return out
 
 
-def cpu_baseline(nseq=32, nblocks=48):
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cfg1_run(dev, method="crb"):
+    """BASELINE configs[0] in full: add_batch of 16 x 512 tokens (one call per
+    sequence) + fasterquant of the 768 x 768 fp32 layer, through the drop-in
+    BRAGPTQ on `dev` (the crbq kernels on a GPU, or the oracle's restatement
+    of the reference on the CPU).  Returns (seconds, error)."""
+    W, X = synth.cfg1(0)
+    if dev.type == "cpu":
+        from oracle import crb_oracle as O
+        t0 = time.time()
+        H = torch.zeros(768, 768)
+        n = 0
+        for s in range(X.shape[0]):
+            H, n = O.hessian_add_batch(H, n, X[s:s + 1])
+        err = O.fasterquant(W, H, method=method)[2]
+        return time.time() - t0, err
+    import contextlib
+    import io
+    from crb_amd import BRAGPTQ, Binarization
+    Xd = X.to(dev)
+    best = None
+    for _ in range(3):
+        layer = torch.nn.Linear(768, 768, bias=False).to(dev)
+        layer.weight.data = W.to(dev).clone()
+        torch.cuda.synchronize()
+        t0 = time.time()
+        bq = BRAGPTQ(layer, Binarization(layer.weight, method=method, groupsize=128), "hessian")
+        for s in range(Xd.shape[0]):
+            bq.add_batch(Xd[s:s + 1], None)
+        with contextlib.redirect_stdout(io.StringIO()):
+            err = bq.fasterquant(blocksize=128, percdamp=0.01, partition=3)["error"]
+        dt = time.time() - t0
+        best = dt if best is None else min(best, dt)
+    return best, err
+
+
+def reference_calibration():
+    """Oracle / genuine reference time ratio on configs[0], measured in the
+    build container (tests/golden/time_reference.py), or None."""
+    path = os.path.join(ROOT, "tests", "golden", "reference_timing.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        d = json.load(f)
+    return {"oracle_over_reference": round(d["oracle_over_reference"], 3),
+            "cpu": d["cpu"], "threads": d["threads"]}
+
+
+def cpu_baseline(nseq=32, nblocks=48, cfg1_gpu=None):
     """Time the test-only CPU oracle (torch-CPU restatement of the reference
     path) on a bounded sample of the workload (about 10-20 s on 16 cores)
-    and extrapolate to one OPT-6.7B layer."""
+    and extrapolate to one OPT-6.7B layer; also configs[0] in full."""
     from oracle import crb_oracle as O
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
+    cfg1_cpu_s, cfg1_err = cfg1_run(torch.device("cpu"))
     C = 4096
     g = torch.Generator().manual_seed(0)
     # Hessian: nseq sequences x 2048 tokens of a 4096-channel input, fed
@@ -363,7 +423,13 @@ def cpu_baseline(nseq=32, nblocks=48):
                    f"4096x4096 sublayer ({t_b:.2f}s); extrapolated to one OPT-6.7B layer by "
                    f"token count, C^3 and row-blocks"),
         "split_s": {"hessian": h_layer, "hinv": u_layer, "blocks": b_layer},
-        "cpu": platform.processor() or platform.machine(),
+        "cfg1_full": {"workload": "BASELINE configs[0] in full (768x768 fp32, 16x512 tokens, "
+                                  "crb)", "cpu_s": round(cfg1_cpu_s, 3),
+                      "cpu_error": cfg1_err,
+                      "gpu_s": None if cfg1_gpu is None else round(cfg1_gpu[0], 4),
+                      "gpu_error": None if cfg1_gpu is None else cfg1_gpu[1]},
+        "calibration": reference_calibration(),
+        "cpu": cpu_model(),
         "blas": torch.__config__.show().split("BLAS_INFO=")[-1].split(",")[0]
         if "BLAS_INFO=" in torch.__config__.show() else "unknown",
     }
@@ -479,7 +545,7 @@ def main():
         print(f"[bench] packed gemv: {out['packed_gemv']}", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline"] = cpu_baseline(cfg1_gpu=cfg1_run(dev))
     print(json.dumps(out))
 
 

@@ -49,7 +49,7 @@ class LayerQuantizer:
     def __init__(self, sublayers, method="crb", metric="hessian", blocksize=128,
                  percdamp=0.01, partition=3, orders=(1, 1, 2), refine_iters=1,
                  lam=1e-5, corr_damp=0.1, disable_gptq=False, nstreams=NSTREAMS,
-                 keep_masks=False):
+                 keep_masks=False, keep_factors=False):
         self.sublayers = list(sublayers)
         self.p = _lib.params(method, metric=metric, blocksize=blocksize, partition=partition,
                              orders=orders, up_lim=50, refine_iters=refine_iters,
@@ -59,6 +59,11 @@ class LayerQuantizer:
         self.nstreams = max(1, int(nstreams))
         self.keep_masks = bool(keep_masks)
         self.masks = {}            # keep_masks: name -> uint8 [R, C] mask codes 1/2/3
+        # keep_factors (for checks): group -> (damped H, U), name -> (fp32
+        # quantized weight before the cast to the layer dtype, per-row losses)
+        self.keep_factors = bool(keep_factors)
+        self.factors = {}
+        self.quantized = {}
         self.S = {}
         self.nsamples = {}
         self.ready = {}
@@ -173,9 +178,15 @@ class LayerQuantizer:
             self.info[g] = {"retries": retries, "fallback": fb}
             if retries or fb:
                 redo.add(g)
+                # the retries / fallback write U on the factor's stream and
+                # return without waiting: the redo below runs on `main`
+                main.wait_stream(jobs[g].stream)
         for s in order:
             if s.group in redo:
                 work[s.name] = self._blocks(s, U[s.group], dead[s.group])
+        if self.keep_factors:
+            self.factors = {g: (jobs[g].H, U[g]) for g in groups}
+            self.quantized = {s.name: (work[s.name][0], work[s.name][1]) for s in order}
         for s in order:
             W, losses, masks = work[s.name]
             if masks is not None:

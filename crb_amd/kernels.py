@@ -199,7 +199,15 @@ def binarize(x: torch.Tensor, mask: torch.Tensor, order: int, method: str, lam: 
     if method not in _lib.METHODS:
         raise NotImplementedError(method)
     xf = x if (x.dtype == torch.float32 and x.stride(-1) == 1) else x.float().contiguous()
-    m = mask.to(torch.uint8).contiguous()
+    if xf.dim() != 2:
+        raise _lib.CrbqError("binarize takes a [rows, cols] weight block")
+    try:
+        # the reference's elementwise ops broadcast the mask ([cols] or [1, cols])
+        m = mask.expand_as(xf)
+    except RuntimeError as e:
+        raise _lib.CrbqError(f"binarize: mask of shape {tuple(mask.shape)} does not "
+                             f"broadcast to {tuple(xf.shape)}") from e
+    m = m.to(torch.uint8).contiguous()
     R, nc = xf.shape
     if out is None:
         out = torch.empty((R, nc), dtype=torch.float32, device=x.device)
@@ -312,7 +320,9 @@ def _packed_x(x, lut, C, what):
     if x.shape[0] < 1 or x.shape[1] != C:
         raise _lib.CrbqError(f"{what} takes [T, C] activations of the weight's width")
     if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
-        x = x.contiguous()
+        # a fresh allocation: contiguous() would hand back a contiguous view
+        # at a misaligned storage offset unchanged
+        x = x.clone(memory_format=torch.contiguous_format)
         if C % 8:
             xp = torch.zeros((x.shape[0], (C + 7) // 8 * 8), dtype=x.dtype, device=x.device)
             xp[:, :C] = x

@@ -295,6 +295,18 @@ class StackQuantizer:
         outputs to outs (if given)."""
         layer = self.layers[i]
         clock = _Clock(inps.is_cuda)
+        if not any(self.name_filter(i, k) for k in find_linears(layer)):
+            # nothing selected in this layer (run.py:332-336): its output only
+            clock.mark()
+            clock.mark()
+            clock.mark()
+            if outs is not None:
+                self._forward(layer, inps, outs)
+            clock.mark()
+            stats = LayerStats(errors={}, groups={})
+            stats.capture_ms, stats.hessian_ms, stats.quantize_ms, stats.forward_ms = \
+                clock.spans()
+            return stats
         lq, groups, pending = self._capture_layer(i, layer, inps)
         clock.mark()
         for g, x in pending:

@@ -384,19 +384,26 @@ def fasterquant(W0: torch.Tensor, H0: torch.Tensor, method="crb", blocksize=128,
                 percdamp=0.01, partition=3, orders=(1, 1, 2),
                 salient_metric="hessian", lam=1e-5, corr_damp=0.1,
                 refine_iters=1, disable_gptq=False, up_lim=50,
-                max_blocks=None, trace: list | None = None):
+                max_blocks=None, trace: list | None = None, U0=None):
     """``BRAGPTQ.fasterquant`` legacy partitioned path, bigptq.py:56-291.
 
     W0: [R, C] weight (any float dtype); H0: [C, C] fp32 Hessian.
     Returns (Wq fp32 [R, C] before the dtype cast, Losses fp32 [R],
     error float = torch.sum(Losses).item(), HinvInfo, U).
-    ``max_blocks`` stops after that many column blocks (CPU baseline timing);
-    the unprocessed columns of Wq then hold the propagated, unquantized W.
+    ``max_blocks`` stops after that many column blocks (CPU baseline timing,
+    parity of the first blocks of full-size layers); the unprocessed columns
+    of Wq then hold the propagated, unquantized W.
+    ``U0`` (optional, fp32 [C, C] upper) is an inverse factor computed
+    elsewhere: the block loop (bigptq.py:131-264) then starts from it and
+    H0 is not used (no dead-column handling, which belongs to the factor).
     """
     W = W0.clone().float()
-    H = H0.clone().float()
     R, C = W.shape
-    U, hinfo = hinv_upper(H, W, percdamp)
+    if U0 is None:
+        H = H0.clone().float()
+        U, hinfo = hinv_upper(H, W, percdamp)
+    else:
+        U, hinfo = U0.float(), HinvInfo()
     losses = torch.zeros(R)
     for bi, st in enumerate(range(0, C, blocksize)):
         if max_blocks is not None and bi >= max_blocks:

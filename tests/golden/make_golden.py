@@ -9,7 +9,12 @@ What it pins (functions no closed form or library routine pins on its own):
   * BRAGPTQ.add_batch + fasterquant (bigptq.py:37-291) end to end for crb,
     braq and crbog: the quantized weight and the returned error.
   * the three binarizers (binary.py:18-39, 577-687, 1544-1638) on seeded
-    rows and masks, as a direct cross-check of the closed-form tests.
+    rows and masks, as a direct cross-check of the closed-form tests;
+  * the technique flags of fasterquant off the default path on one small
+    layer: RTN (disable_gptq, bigptq.py:149-162), partition=1 (one all-ones
+    mask, bigptq.py:138-140), the magnitude metric (utils/structure.py:11-12),
+    the crb_norefine / crb_symdamp / crb_symdamp_norefine methods
+    (binary.py:2885-2890), and bf16 weights and activations.
 
 Only inputs and outputs are written (tests/golden/*.npz, *.json); no
 reference source is copied.  ``torch.cuda.synchronize`` is replaced by a
@@ -72,6 +77,8 @@ def main(ref_root: str):
                     x, m, order=order, skip_refinement=True),
                 "crb_symdamp": binary.coupled_residual_binarization_stable_v7(
                     x, m, order=order, symmetric_damp=True),
+                "crb_symdamp_norefine": binary.coupled_residual_binarization_stable_v7(
+                    x, m, order=order, symmetric_damp=True, skip_refinement=True),
                 "crbog": binary.coupled_residual_binarization(x, m, order=order),
             }
             for k, v in outs.items():
@@ -139,6 +146,54 @@ def main(ref_root: str):
             if small:
                 arrays[f"fq_{name}_{method}_Wq"] = Wq.numpy()
         summary["fasterquant"].append(ent)
+
+    # ---- technique flags off the default path, on one small layer ----------
+    # (case, method, salient_metric, disable_gptq, partition, dtype)
+    flag_cases = [
+        ("rtn", "crb", "hessian", True, 3, "f32"),
+        ("rtn", "braq", "hessian", True, 3, "f32"),
+        ("part1", "crb", "hessian", False, 1, "f32"),
+        ("part1", "braq", "hessian", False, 1, "f32"),
+        ("part1", "crbog", "hessian", False, 1, "f32"),
+        ("rtn_part1", "crb", "hessian", True, 1, "f32"),
+        ("magnitude", "crb", "magnitude", False, 3, "f32"),
+        ("magnitude", "braq", "magnitude", False, 3, "f32"),
+        ("norefine", "crb_norefine", "hessian", False, 3, "f32"),
+        ("symdamp", "crb_symdamp", "hessian", False, 3, "f32"),
+        ("symdamp_norefine", "crb_symdamp_norefine", "hessian", False, 3, "f32"),
+        ("bf16", "crb", "hessian", False, 3, "bf16"),
+        ("bf16", "crbog", "hessian", False, 3, "bf16"),
+    ]
+    R, C, nseq, seqlen, seed = 64, 256, 4, 64, 41
+    summary["flags"] = {"R": R, "C": C, "nseq": nseq, "seqlen": seqlen, "seed": seed,
+                        "cases": []}
+    for case, method, metric, rtn, part, dt in flag_cases:
+        if dt == "bf16":
+            # 1 % of the input columns x10, bf16 in and out
+            W = synth.weight(R, C, seed, outlier_frac=0.01, outlier_scale=10.0,
+                             dtype=torch.bfloat16)
+            X = synth.calibration(nseq, seqlen, C, seed + 1, kind="lognormal",
+                                  dtype=torch.bfloat16)
+        else:
+            W = synth.weight(R, C, seed, outlier_frac=0.02)
+            X = synth.calibration(nseq, seqlen, C, seed + 1, kind="lognormal")
+        layer = torch.nn.Linear(C, R, bias=False).to(W.dtype)
+        layer.weight.data = W.clone()
+        q = binary.Binarization(layer.weight, method=method, groupsize=128)
+        bq = bigptq.BRAGPTQ(layer, q, metric, disable_gptq=rtn)
+        for s in range(nseq):
+            bq.add_batch(X[s:s + 1], None)
+        with contextlib.redirect_stdout(io.StringIO()):
+            info = bq.fasterquant(blocksize=128, percdamp=0.01, partition=part,
+                                  orders=(1, 1, 2))
+        Wq = layer.weight.data.clone().float()
+        key = f"flag_{case}_{method}"
+        arrays[key + "_Wq"] = Wq.numpy()
+        summary["flags"]["cases"].append({
+            "case": case, "method": method, "metric": metric, "disable_gptq": rtn,
+            "partition": part, "dtype": dt, "key": key, "W_sha": sha(W.float()),
+            "X_sha": sha(X.float()), "error": info["error"],
+            "error_hex": float(info["error"]).hex()})
 
     np.savez_compressed(os.path.join(HERE, "golden_vectors.npz"), **arrays)
     with open(os.path.join(HERE, "golden_summary.json"), "w") as f:

@@ -56,3 +56,58 @@ def test_driver_matches_per_sublayer_api(kind, method):
     for s in sl:
         assert torch.equal(s.weight.cpu(), ref_w[s.name]), s.name
         assert abs(errs[s.name] - ref_err[s.name]) <= 1e-6 * abs(ref_err[s.name]), s.name
+
+
+@pytest.mark.parametrize("need", [3, "fallback"])
+def test_driver_retry_and_fallback_match_per_sublayer_api(need):
+    """A Hessian whose Cholesky needs the reference's extra damping rounds
+    (bigptq.py:114-123) or its diagonal fallback (:124-126) for one input:
+    the driver recomputes that input's sublayers with the final factor,
+    which must give what the per-sublayer API gives."""
+    print(f"driver retries {need}", flush=True)
+    from crb_amd import BRAGPTQ, Binarization
+    from crb_amd.driver import LayerQuantizer, Sublayer
+    subs, Ws, X = _layer("opt")
+    C = 256
+    g = torch.Generator().manual_seed(11)
+    if need == "fallback":
+        Hbad = torch.eye(C) * 2.0
+        Hbad[3, 3] = -1e9
+    else:
+        Q, _ = torch.linalg.qr(torch.randn(C, C, generator=g, dtype=torch.float64))
+        ev = torch.rand(C, generator=g, dtype=torch.float64) + 0.5
+        ev[0] = -(0.01 + (need - 0.5) * 1e-3) * float(ev.mean()) * 0.994
+        Hbad = ((Q * ev) @ Q.t()).float()
+    special = "qkv"
+    ref_w, ref_err = {}, {}
+    for n, r, c, grp in subs:
+        layer = torch.nn.Linear(c, r, bias=False).to(DEV).to(Ws[n].dtype)
+        layer.weight.data = Ws[n].to(DEV).clone()
+        q = Binarization(layer.weight, method="crb", groupsize=128)
+        bq = BRAGPTQ(layer, q, "hessian")
+        if grp == special:
+            bq._S = Hbad.to(DEV).clone()
+            bq.nsamples = 2                     # H = (2 / 2) * S
+        else:
+            for s in range(X[grp].shape[0]):
+                bq.add_batch(X[grp][s:s + 1].to(DEV), None)
+        ref_err[n] = bq.fasterquant()["error"]
+        if grp == special:
+            info = bq.last
+            assert info["fallback"] if need == "fallback" else info["retries"] == need, info
+        ref_w[n] = layer.weight.data.cpu()
+    sl = [Sublayer(n, Ws[n].to(DEV).clone(), grp) for n, r, c, grp in subs]
+    lq = LayerQuantizer(sl, method="crb")
+    for grp, x in X.items():
+        if grp == special:
+            lq.S[grp] = Hbad.to(DEV).clone()
+            lq.nsamples[grp] = 2
+            continue
+        for s in range(x.shape[0]):
+            lq.add_batch(grp, x[s:s + 1].to(DEV))
+    errs = lq.quantize()
+    assert lq.info[special]["fallback"] if need == "fallback" else \
+        lq.info[special]["retries"] == need
+    for s in sl:
+        assert torch.equal(s.weight.cpu(), ref_w[s.name]), s.name
+        assert abs(errs[s.name] - ref_err[s.name]) <= 1e-6 * abs(ref_err[s.name]), s.name

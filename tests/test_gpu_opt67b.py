@@ -1,0 +1,176 @@
+"""BASELINE configs[2] on the GPU: the OPT-6.7B shapes the headline metric
+is quoted on (hidden 4096, ffn 16384, 128 x 2048 calibration tokens).
+
+1. One full decoder layer through the layer driver (LayerQuantizer, the path
+   bench.py times): k/v/q/out_proj 4096 x 4096, fc1 16384 x 4096 and
+   fc2 4096 x 16384, fp16 weights W ~ N(0, 0.02^2), seeded fp16 activations
+   with Student-t(4) channel scales.
+   * GPTQ identity per sublayer: W0 - Q = E U with U the upper Cholesky
+     factor of H_d^-1 (H_d the damped Hessian), so
+     sum_j e_j^2 / 2 = (W0 - Q) H_d (W0 - Q)^T / 2, the loss the block loop
+     accumulates (bigptq.py:240-262); within 1e-3 relative.
+   * every quantized sublayer packs (shared salient columns, at most 2 / 4
+     values per group apart from rare ties at a group mean) and unpacks
+     bit-exactly.
+   * elementwise parity on the first 4 column blocks of q_proj (4096 rows)
+     and fc1 (16384 rows) against the CPU oracle (bigptq.py:131-264)
+     started from the same U and W: >= 99.99 % of weights within 1e-4
+     relative, and the salient count / split of every block identical to
+     the oracle's unless the oracle's own candidate errors tie within 1e-5.
+2. A two-layer OPT-6.7B-shaped model quantized by the stack driver
+   (crb_amd/stack.py, default mode) from 128 x 2048 random token ids
+   propagated through the layers (run.py:122-387): the GPTQ identity for
+   every sublayer of both layers.
+"""
+import numpy as np
+import pytest
+import torch
+
+from crb_amd import synth
+from oracle import crb_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+NTOK = 128 * 2048
+NBLK = 4
+
+
+def _acts(C, seed):
+    s = synth.channel_scales(C, seed, kind="student_t4", device=DEV)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    x = torch.empty(NTOK, C, dtype=torch.float16, device=DEV)
+    for t0 in range(0, NTOK, 8192):
+        x[t0:t0 + 8192] = (torch.randn(8192, C, generator=g, device=DEV) * s).half()
+    return x
+
+
+def _identity(W0, Q, Hd, err):
+    """(W0 - Q) H_d (W0 - Q)^T / 2 summed over rows, against the block loop's
+    summed loss: relative difference."""
+    D = W0 - Q
+    quad = 0.0
+    for r0 in range(0, D.shape[0], 4096):
+        d = D[r0:r0 + 4096]
+        quad += float(((d @ Hd) * d).double().sum()) / 2
+    return abs(quad - err) / err
+
+
+def _pack_check(name, Q, masks):
+    from crb_amd import kernels
+    Wq = Q.half().contiguous()
+    codes, lut, sal, ex = kernels.pack(Wq, masks)
+    n_ex = int(ex.idx.numel())
+    back = kernels.unpack(codes, lut, sal, Q.shape[1], ex)
+    assert torch.equal(back.view(torch.int16), Wq.view(torch.int16)), name
+    assert n_ex * 10000 <= Wq.numel(), (name, n_ex)
+    return n_ex
+
+
+def _first_blocks(name, W0, Qd, H, p):
+    """First NBLK blocks of one sublayer: the oracle's block loop started
+    from the GPU's U and the same W, against the driver's output."""
+    from crb_amd import kernels
+    U, retries, fb = kernels.hinv_upper(H.clone(), None, 0.01)
+    assert retries == 0 and not fb
+    nc = NBLK * 128
+    # the GPU's per-block choices: its block loop on the first NBLK blocks
+    Wsub = W0[:, :nc].clone()
+    lo = torch.zeros(W0.shape[0], device=DEV)
+    _, tr = kernels.fasterquant_blocks(Wsub, U[:nc, :nc].contiguous(), p, lo, want_traces=True)
+    same = bool(torch.equal(Wsub, Qd[:, :nc]))
+    trace = []
+    Wr, _, _, _, _ = O.fasterquant(W0.cpu(), None, method="crb", U0=U.cpu(), max_blocks=NBLK,
+                                   trace=trace)
+    Wr = Wr[:, :nc]
+    Wg = Qd[:, :nc].cpu()
+    close = (Wg - Wr).abs() <= 1e-4 * Wr.abs() + 1e-7
+    agree = float(close.float().mean())
+    print(f"  {name}: first {NBLK} blocks agree {agree:.6f}, identical "
+          f"{float((Wg == Wr).float().mean()):.6f}, driver == block-loop sub-run: {same}",
+          flush=True)
+    for b, (t_o, t_g) in enumerate(zip(trace, tr)):
+        so = t_o.search
+        print(f"    block {b}: i* {t_g['i_star']} vs {so.i_star}, k* {t_g['k_star']} vs "
+              f"{so.k_star}", flush=True)
+        if t_g["i_star"] != so.i_star:
+            ea = np.asarray(so.errs_a)
+            assert abs(ea[t_g["i_star"] - 1] - ea[so.i_star - 1]) <= 1e-5 * ea[so.i_star - 1]
+        elif t_g["k_star"] != so.k_star:
+            ec = np.asarray(so.errs_c)
+            assert abs(ec[t_g["k_star"]] - ec[so.k_star]) <= 1e-5 * ec[so.k_star]
+    assert agree >= 0.9999, agree
+
+
+def test_opt67b_layer_driver():
+    from crb_amd import _lib
+    from crb_amd.driver import LayerQuantizer, Sublayer
+    print("OPT-6.7B layer through the layer driver", flush=True)
+    subs = synth.opt_sublayers("opt-6.7b")
+    W0 = {}
+    for j, (name, r, c, grp) in enumerate(subs):
+        g = torch.Generator(device=DEV).manual_seed(500 + j)
+        W0[name] = (torch.randn(r, c, generator=g, device=DEV) * 0.02).half().float()
+    sl = [Sublayer(name, W0[name].clone(), grp) for name, r, c, grp in subs]
+    lq = LayerQuantizer(sl, method="crb", keep_masks=True, keep_factors=True)
+    H = {}
+    for j, grp in enumerate(("qkv", "out", "fc1", "fc2")):
+        C = 16384 if grp == "fc2" else 4096
+        x = _acts(C, 600 + j)
+        lq.add_batch(grp, x.view(128, 2048, C))
+        # an undamped copy of the Hessian for the first-block checks
+        from crb_amd import kernels
+        S = torch.zeros(C, C, device=DEV)
+        kernels.hessian_accum(x, S)
+        H[grp] = kernels.hessian_finalize(S, 2.0 / 128, S)
+        del x
+    errs = lq.quantize()
+    torch.cuda.synchronize()
+    for name, r, c, grp in subs:
+        Hd, U = lq.factors[grp]
+        Q, losses = lq.quantized[name]
+        assert abs(float(losses.sum()) - errs[name]) <= 1e-6 * errs[name]
+        rel = _identity(W0[name], Q, Hd, errs[name])
+        n_ex = _pack_check(name, Q, lq.masks[name])
+        print(f"  {name} {r}x{c}: error {errs[name]:.6g}, identity rel {rel:.2e}, "
+              f"{n_ex} pack exceptions", flush=True)
+        assert rel < 1e-3, (name, rel)
+    p = _lib.params("crb")
+    for name in ("self_attn.q_proj", "fc1"):
+        grp = next(gg for n, _, _, gg in subs if n == name)
+        _first_blocks(name, W0[name], lq.quantized[name][0], H[grp], p)
+
+
+def test_opt67b_two_layer_stack():
+    transformers = pytest.importorskip("transformers")
+    from crb_amd.driver import LayerQuantizer
+    from crb_amd.stack import StackQuantizer
+    print("OPT-6.7B two-layer stack, 128 x 2048 token ids", flush=True)
+    results = []
+
+    class Checked(LayerQuantizer):
+        def quantize(self, times=None):
+            w0 = {s.name: s.weight.float() for s in self.sublayers}
+            errs = super().quantize(times)
+            for s in self.sublayers:
+                Hd, U = self.factors[s.group]
+                Q, _ = self.quantized[s.name]
+                rel = _identity(w0[s.name], Q, Hd, errs[s.name])
+                results.append((s.name, errs[s.name], rel))
+                print(f"  {s.name}: error {errs[s.name]:.6g}, identity rel {rel:.2e}",
+                      flush=True)
+            self.factors, self.quantized = {}, {}
+            return errs
+
+    torch.manual_seed(0)
+    cfg = transformers.OPTConfig(hidden_size=4096, ffn_dim=16384, num_attention_heads=32,
+                                 num_hidden_layers=2, max_position_embeddings=2048,
+                                 vocab_size=50272, word_embed_proj_dim=4096)
+    with torch.device(DEV):
+        model = transformers.OPTForCausalLM(cfg).half().eval()
+    g = torch.Generator().manual_seed(1)
+    samples = torch.randint(0, cfg.vocab_size, (128, 2048), generator=g).to(DEV)
+    stats = StackQuantizer(model, layer_quantizer=Checked, keep_factors=True).run(samples)
+    assert len(stats) == 2 and len(results) == 12
+    for name, err, rel in results:
+        assert err > 0 and rel < 1e-3, (name, err, rel)

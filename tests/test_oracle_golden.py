@@ -83,3 +83,46 @@ def test_fasterquant_matches_reference(golden, name):
         key = f"fq_{name}_{method}_Wq"
         if key in A.files:
             np.testing.assert_array_equal(Wq.numpy(), A[key])
+
+
+def _flag_inputs(summary, ent):
+    f = summary["flags"]
+    R, C, nseq, seqlen, seed = f["R"], f["C"], f["nseq"], f["seqlen"], f["seed"]
+    if ent["dtype"] == "bf16":
+        W = synth.weight(R, C, seed, outlier_frac=0.01, outlier_scale=10.0,
+                         dtype=torch.bfloat16)
+        X = synth.calibration(nseq, seqlen, C, seed + 1, kind="lognormal",
+                              dtype=torch.bfloat16)
+    else:
+        W = synth.weight(R, C, seed, outlier_frac=0.02)
+        X = synth.calibration(nseq, seqlen, C, seed + 1, kind="lognormal")
+    assert _sha(W.float()) == ent["W_sha"] and _sha(X.float()) == ent["X_sha"]
+    return W, X
+
+
+def test_binarizer_symdamp_norefine_matches_reference(golden):
+    summary, A = golden
+    for c in summary["binarize"]:
+        i = c["case"]
+        x = torch.from_numpy(A[f"bin{i}_x"])
+        m = torch.from_numpy(A[f"bin{i}_m"])
+        for order in (1, 2):
+            got = O.binarize("crb_symdamp_norefine", x, m, order).numpy()
+            np.testing.assert_array_equal(got, A[f"bin{i}_o{order}_crb_symdamp_norefine"])
+
+
+def test_fasterquant_flags_match_reference(golden):
+    """RTN (bigptq.py:149-162), partition=1 (bigptq.py:138-140), the
+    magnitude metric (utils/structure.py:11-12), the norefine / symdamp
+    methods (binary.py:2885-2890) and bf16 layers: the oracle's weights and
+    error bit for bit against the reference's."""
+    summary, A = golden
+    for ent in summary["flags"]["cases"]:
+        W, X = _flag_inputs(summary, ent)
+        H = _oracle_H(X, W.shape[1])
+        Wq, losses, err, info, U = O.fasterquant(
+            W, H, method=ent["method"], partition=ent["partition"],
+            salient_metric=ent["metric"], disable_gptq=ent["disable_gptq"])
+        Wq = Wq.to(W.dtype).float()
+        assert float(err).hex() == ent["error_hex"], ent["key"]
+        np.testing.assert_array_equal(Wq.numpy(), A[ent["key"] + "_Wq"], err_msg=ent["key"])
