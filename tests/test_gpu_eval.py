@@ -50,15 +50,17 @@ def test_ppl_llama_bf16():
 @torch.no_grad()
 def _direct_ppl(model, ids, seqlen):
     """eval_ppl_utils.py:538-637's quantity with whole-model forwards:
-    exp(sum_i CE(logits_i[:-1], ids_i[1:]) * seqlen / (n * seqlen))."""
+    exp(sum_i CE(logits_i[:-1], ids_i[1:]) * seqlen / (n * seqlen)), the
+    cross entropy taken on the model-dtype logits as the reference does
+    (:620-625, then loss.float())."""
     import math
     n = ids.numel() // seqlen
     tot = 0.0
     for i in range(n):
         w = ids[:, i * seqlen:(i + 1) * seqlen]
         logits = model(w).logits
-        loss = torch.nn.functional.cross_entropy(logits[0, :-1].float(), w[0, 1:])
-        tot += float(loss) * seqlen
+        loss = torch.nn.functional.cross_entropy(logits[0, :-1], w[0, 1:])
+        tot += float(loss.float()) * seqlen
     return math.exp(tot / (n * seqlen))
 
 

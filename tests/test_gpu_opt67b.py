@@ -5,10 +5,13 @@ is quoted on (hidden 4096, ffn 16384, 128 x 2048 calibration tokens).
    bench.py times): k/v/q/out_proj 4096 x 4096, fc1 16384 x 4096 and
    fc2 4096 x 16384, fp16 weights W ~ N(0, 0.02^2), seeded fp16 activations
    with Student-t(4) channel scales.
-   * GPTQ identity per sublayer: W0 - Q = E U with U the upper Cholesky
-     factor of H_d^-1 (H_d the damped Hessian), so
-     sum_j e_j^2 / 2 = (W0 - Q) H_d (W0 - Q)^T / 2, the loss the block loop
-     accumulates (bigptq.py:240-262); within 1e-3 relative.
+   * GPTQ identity per sublayer, sum_j e_j^2 / 2 = (W0 - Q) H_d (W0 - Q)^T / 2
+     (H_d the damped Hessian, the left side the loss the block loop
+     accumulates, bigptq.py:240-262), within 1e-3 relative: it holds where
+     U, the upper Cholesky factor of H_d^-1, is near-diagonal inside each
+     128-column block, as these near-diagonal Hessians give;
+   * the exact forms: U^-1 U^-T = H_d to 1e-5 and W0 - Q = E U' to 1e-5
+     (_u_checks).
    * every quantized sublayer packs (shared salient columns, at most 2 / 4
      values per group apart from rare ties at a group mean) and unpacks
      bit-exactly.
@@ -19,8 +22,16 @@ is quoted on (hidden 4096, ffn 16384, 128 x 2048 calibration tokens).
      the oracle's unless the oracle's own candidate errors tie within 1e-5.
 2. A two-layer OPT-6.7B-shaped model quantized by the stack driver
    (crb_amd/stack.py, default mode) from 128 x 2048 random token ids
-   propagated through the layers (run.py:122-387): the GPTQ identity for
-   every sublayer of both layers.
+   propagated through the layers (run.py:122-387), for every sublayer of
+   both layers: U^-1 U^-T = H_d to 1e-5 (the factor's backward error) and
+   W0 - Q = E U' with sum(E^2) / 2 = the accumulated loss to 1e-5 (the
+   block loop's error feedback; U' defined in _u_checks), both evaluated in
+   float64.  The H_d-metric form above is printed but not asserted here:
+   it assumes feedback inside each block too, which the reference's
+   pre-quantize-then-read path (bigptq.py:235-262) does not do, so it only
+   holds where the in-block entries of U are small (near-diagonal
+   Hessians, as the synthetic activations of test 1 give); the real
+   activations' Hessians are strongly correlated.
 """
 import numpy as np
 import pytest
@@ -47,13 +58,51 @@ def _acts(C, seed):
 
 def _identity(W0, Q, Hd, err):
     """(W0 - Q) H_d (W0 - Q)^T / 2 summed over rows, against the block loop's
-    summed loss: relative difference."""
-    D = W0 - Q
+    summed loss: relative difference.  The quadratic form is evaluated in
+    float64: GPTQ pushes W0 - Q towards the small-eigenvalue directions of
+    H_d, so an fp32 product would cancel most of its digits."""
+    D = (W0 - Q).double()
+    Hd64 = Hd.double()
     quad = 0.0
-    for r0 in range(0, D.shape[0], 4096):
-        d = D[r0:r0 + 4096]
-        quad += float(((d @ Hd) * d).double().sum()) / 2
+    for r0 in range(0, D.shape[0], 2048):
+        d = D[r0:r0 + 2048]
+        quad += float(((d @ Hd64) * d).sum()) / 2
     return abs(quad - err) / err
+
+
+def _u_checks(W0, Q, Hd, U, err):
+    """Checks that hold to fp32 backward error whatever the conditioning of
+    H_d (real activations of a random-init model give nearly rank-deficient
+    Hessians, e.g. out_proj's input is a near-uniform average over tokens,
+    and then the identity above is only as good as cond(H_d) * eps):
+    * the factor: U^-1 U^-T against H_d, relative Frobenius error (U is the
+      upper Cholesky factor of H_d^-1, so U^-1 U^-T = H_d);
+    * the block loop: the reference quantizes a 128-column block from its
+      values at the block's start (no feedback inside the block,
+      bigptq.py:235-262) and then updates the later blocks,
+      W[:, ed:] -= Err1 U[st:ed, ed:] (:264), so W0 - Q = E U' with U' = U
+      without the strictly upper entries inside each 128 x 128 diagonal
+      block; E = (W0 - Q) U'^-1 and sum(E^2) / 2 is the accumulated loss.
+    Both in float64 from the fp32 U."""
+    U64 = U.double()
+    C = U.shape[0]
+    I = torch.eye(C, dtype=torch.float64, device=U.device)
+    Ui = torch.linalg.solve_triangular(U64, I, upper=True)
+    Ht = Ui @ Ui.t()
+    back = float((Ht - Hd.double()).norm() / Hd.double().norm())
+    del Ht, Ui
+    blk = torch.arange(C, device=U.device) // 128
+    inner = (blk[:, None] == blk[None, :]) & (torch.arange(C, device=U.device)[:, None]
+                                              != torch.arange(C, device=U.device)[None, :])
+    U64.masked_fill_(inner, 0.0)
+    Upi = torch.linalg.solve_triangular(U64, I, upper=True)
+    del I, U64, inner
+    D = (W0 - Q).double()
+    tot = 0.0
+    for r0 in range(0, D.shape[0], 2048):
+        E = D[r0:r0 + 2048] @ Upi
+        tot += float((E * E).sum()) / 2
+    return back, abs(tot - err) / err
 
 
 def _pack_check(name, Q, masks):
@@ -131,10 +180,13 @@ def test_opt67b_layer_driver():
         Q, losses = lq.quantized[name]
         assert abs(float(losses.sum()) - errs[name]) <= 1e-6 * errs[name]
         rel = _identity(W0[name], Q, Hd, errs[name])
+        back, loop = _u_checks(W0[name], Q, Hd, U, errs[name])
         n_ex = _pack_check(name, Q, lq.masks[name])
         print(f"  {name} {r}x{c}: error {errs[name]:.6g}, identity rel {rel:.2e}, "
-              f"{n_ex} pack exceptions", flush=True)
+              f"U backward {back:.2e}, loop rel {loop:.2e}, {n_ex} pack exceptions",
+              flush=True)
         assert rel < 1e-3, (name, rel)
+        assert back < 1e-5 and loop < 1e-5, (name, back, loop)
     p = _lib.params("crb")
     for name in ("self_attn.q_proj", "fc1"):
         grp = next(gg for n, _, _, gg in subs if n == name)
@@ -156,9 +208,12 @@ def test_opt67b_two_layer_stack():
                 Hd, U = self.factors[s.group]
                 Q, _ = self.quantized[s.name]
                 rel = _identity(w0[s.name], Q, Hd, errs[s.name])
-                results.append((s.name, errs[s.name], rel))
-                print(f"  {s.name}: error {errs[s.name]:.6g}, identity rel {rel:.2e}",
-                      flush=True)
+                back, loop = _u_checks(w0[s.name], Q, Hd, U, errs[s.name])
+                d = torch.diagonal(Hd).double()
+                results.append((s.name, errs[s.name], back, loop))
+                print(f"  {s.name}: error {errs[s.name]:.6g}, U backward {back:.2e}, loop "
+                      f"rel {loop:.2e} (H_d identity rel {rel:.2e}, diag max/min "
+                      f"{float(d.max() / d.min()):.3g})", flush=True)
             self.factors, self.quantized = {}, {}
             return errs
 
@@ -172,5 +227,5 @@ def test_opt67b_two_layer_stack():
     samples = torch.randint(0, cfg.vocab_size, (128, 2048), generator=g).to(DEV)
     stats = StackQuantizer(model, layer_quantizer=Checked, keep_factors=True).run(samples)
     assert len(stats) == 2 and len(results) == 12
-    for name, err, rel in results:
-        assert err > 0 and rel < 1e-3, (name, err, rel)
+    for name, err, back, loop in results:
+        assert err > 0 and back < 1e-5 and loop < 1e-5, (name, err, back, loop)
