@@ -52,6 +52,8 @@ class CrbqBlockTrace(ctypes.Structure):
 
 
 TRACE_BYTES = ctypes.sizeof(CrbqBlockTrace)
+NOALLOC_SCRATCH_BYTES = 80 << 20      # CRBQ_NOALLOC_SCRATCH_BYTES (include/crbq.h)
+ERR_TOO_LARGE = -5                    # CRBQ_ERR_TOO_LARGE
 
 _SIGS = {
     "crbq_version": (c_i32, []),
@@ -76,6 +78,9 @@ _SIGS = {
     "crbq_fasterquant": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64,
                                  ctypes.POINTER(CrbqParams), c_vp, c_vp, c_i64, c_vp, c_vp,
                                  c_size, c_vp]),
+    "crbq_fasterquant_noalloc": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64,
+                                         ctypes.POINTER(CrbqParams), c_vp, c_vp, c_i64, c_vp,
+                                         c_vp]),
     "crbq_block_search_workspace_size": (c_size, [c_i64, c_i32]),
     "crbq_block_search": (c_i32, [c_vp, c_i64, c_i32, c_i64, c_vp, c_i64, c_i32, c_i32, c_vp,
                                   c_i64, c_vp, c_vp, c_size, c_vp]),

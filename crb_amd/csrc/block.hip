@@ -27,6 +27,8 @@
 //
 // T = W^2 / diag(U_blk)^2 (hessian metric) or W (magnitude) is recomputed
 // from W on every pass instead of being stored.
+#include <mutex>
+
 #include "binarize.h"
 #include "gemm_f32.h"
 
@@ -1276,9 +1278,15 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
   return CRBQ_OK;
 }
 
-static bool q_table_ready = false;
+// c_q lives in every device's copy of the code object, so "uploaded" is
+// tracked per device (the current device of the call).
+constexpr int MAXDEV = 64;
+static bool q_table_ready[MAXDEV] = {};
 static int ensure_q_table() {
-  if (q_table_ready) return CRBQ_OK;
+  int dev = 0;
+  CRBQ_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= MAXDEV) return CRBQ_ERR_ARG;
+  if (q_table_ready[dev]) return CRBQ_OK;
   // torch.linspace(0.10, 0.90, 81) (float32, CPU): start + i*step for the
   // first half, end - (steps-1-i)*step for the second, step in float32.
   float q[NQ];
@@ -1288,13 +1296,16 @@ static int ensure_q_table() {
   for (int i = 0; i < NQ; ++i)
     q[i] = i < half ? start + step * (float)i : end - step * (float)(NQ - 1 - i);
   CRBQ_HIP(hipMemcpyToSymbol(HIP_SYMBOL(c_q), q, sizeof(q)));
-  q_table_ready = true;
+  q_table_ready[dev] = true;
   return CRBQ_OK;
 }
 
 int set_q_table(const float* q) {
+  int dev = 0;
+  CRBQ_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= MAXDEV) return CRBQ_ERR_ARG;
   CRBQ_HIP(hipMemcpyToSymbol(HIP_SYMBOL(c_q), q, NQ * sizeof(float)));
-  q_table_ready = true;
+  q_table_ready[dev] = true;
   return CRBQ_OK;
 }
 
@@ -1393,10 +1404,11 @@ extern "C" size_t crbq_fasterquant_workspace_size(int64_t R, int64_t C, const cr
   return search_ws_bytes(R) + (size_t)R * (size_t)sb * sizeof(float) + 512;
 }
 
-extern "C" int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw, const float* U,
-                                int64_t ldu, const crbq_params* p, float* losses,
-                                uint8_t* masks, int64_t ldm, crbq_block_trace* traces,
-                                void* ws, size_t ws_bytes, void* stream) {
+namespace crbq {
+static int fasterquant_impl(float* W, int64_t R, int64_t C, int64_t ldw, const float* U,
+                            int64_t ldu, const crbq_params* p, float* losses, uint8_t* masks,
+                            int64_t ldm, crbq_block_trace* traces, void* ws, size_t ws_bytes,
+                            void* stream) {
   int st = check_params(p);
   if (st) return st;
   if (!W || !U || !losses || R <= 0 || C <= 0 || ldw < C || ldu < C) return CRBQ_ERR_ARG;
@@ -1469,6 +1481,55 @@ extern "C" int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw, con
     }
   }
   return CRBQ_OK;
+}
+
+// Scratch of the allocation-free entry point: one copy per device, in the
+// code object's device memory, held until the process ends.  Host code
+// never uses this name as an address (on the host it is only a stand-in):
+// it asks for each device's address once, with that device current, and
+// passes that pointer to the kernels.
+static __device__ __align__(256) unsigned char scratch[CRBQ_NOALLOC_SCRATCH_BYTES];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MAXDEV] = {};
+
+static int scratch_of_current_device(void** out) {
+  int dev = 0;
+  CRBQ_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= MAXDEV) return CRBQ_ERR_ARG;
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    CRBQ_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) return CRBQ_ERR_HIP;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return CRBQ_OK;
+}
+}  // namespace crbq
+
+extern "C" int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw, const float* U,
+                                int64_t ldu, const crbq_params* p, float* losses,
+                                uint8_t* masks, int64_t ldm, crbq_block_trace* traces,
+                                void* ws, size_t ws_bytes, void* stream) {
+  return crbq::fasterquant_impl(W, R, C, ldw, U, ldu, p, losses, masks, ldm, traces, ws,
+                                ws_bytes, stream);
+}
+
+extern "C" int crbq_fasterquant_noalloc(float* W, int64_t R, int64_t C, int64_t ldw,
+                                        const float* U, int64_t ldu, const crbq_params* p,
+                                        float* losses, uint8_t* masks, int64_t ldm,
+                                        crbq_block_trace* traces, void* stream) {
+  const int st = crbq::check_params(p);
+  if (st) return st;
+  if (R <= 0 || C <= 0) return CRBQ_ERR_ARG;
+  if (crbq_fasterquant_workspace_size(R, C, p) > CRBQ_NOALLOC_SCRATCH_BYTES)
+    return CRBQ_ERR_TOO_LARGE;
+  void* ws = nullptr;
+  const int sst = crbq::scratch_of_current_device(&ws);
+  if (sst) return sst;
+  return crbq::fasterquant_impl(W, R, C, ldw, U, ldu, p, losses, masks, ldm, traces, ws,
+                                CRBQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -12,6 +12,8 @@ extern "C" const char* crbq_status_string(int status) {
     case CRBQ_ERR_HIP: return "HIP runtime call failed";
     case CRBQ_ERR_WORKSPACE: return "workspace missing or too small";
     case CRBQ_ERR_TOPK: return "selected index k out of range (block narrower than up_lim)";
+    case CRBQ_ERR_TOO_LARGE:
+      return "problem larger than the allocation-free entry point's static scratch";
     default: return "unknown status";
   }
 }

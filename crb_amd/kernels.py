@@ -158,6 +158,25 @@ def fasterquant_blocks(W: torch.Tensor, U: torch.Tensor, p: _lib.CrbqParams,
     return masks, traces
 
 
+def fasterquant_blocks_noalloc(W: torch.Tensor, U: torch.Tensor, p: _lib.CrbqParams,
+                               losses: torch.Tensor, masks: torch.Tensor | None = None,
+                               traces: torch.Tensor | None = None) -> None:
+    """fasterquant_blocks through crbq_fasterquant_noalloc: no workspace, and
+    no allocation at all (the outputs, masks and the raw trace buffer are
+    the caller's).  Raises CrbqError for problems beyond the library's
+    static scratch."""
+    _dev_check(W, U, losses, masks, traces)
+    if W.dtype != torch.float32 or W.stride(1) != 1 or U.stride(1) != 1:
+        raise _lib.CrbqError("fasterquant_blocks_noalloc works in place on row-major fp32 W, U")
+    R, C = W.shape
+    lib = _lib.ready(W.device)
+    check(lib.crbq_fasterquant_noalloc(W.data_ptr(), R, C, W.stride(0), U.data_ptr(),
+                                       U.stride(0), ctypes.byref(p), losses.data_ptr(),
+                                       ptr(masks), masks.stride(0) if masks is not None else 0,
+                                       ptr(traces), stream_of(W)),
+          "crbq_fasterquant_noalloc")
+
+
 def decode_traces(buf: torch.Tensor, n: int):
     raw = bytes(buf.cpu().numpy().tobytes())
     out = []

@@ -3,7 +3,8 @@
  * Every pointer argument named as "device" is a device pointer owned by the
  * caller (for the Python host: the PyTorch caching allocator).  The library
  * never allocates device memory: scratch space comes in through `ws`
- * (size from the matching *_workspace_size query).  `stream` is a
+ * (size from the matching *_workspace_size query), or, for
+ * crbq_fasterquant_noalloc, is a static device array of the library.  `stream` is a
  * hipStream_t passed as void*; NULL means the default stream.  Every entry
  * point returns a status: 0 = ok, < 0 = error (see crbq_status_string), and
  * never throws across the ABI.  Entry points that must read a device result
@@ -38,6 +39,8 @@ extern "C" {
 #define CRBQ_ERR_WORKSPACE  -3   /* workspace pointer NULL or too small */
 #define CRBQ_ERR_TOPK       -4   /* block narrower than the salient search limit
                                     (torch.topk k out of range, utils/autosearch.py:42) */
+#define CRBQ_ERR_TOO_LARGE  -5   /* problem needs more scratch than the
+                                    allocation-free entry point holds */
 
 /* ---- enums -------------------------------------------------------------- */
 enum crbq_dtype  { CRBQ_F32 = 0, CRBQ_F16 = 1, CRBQ_BF16 = 2 };
@@ -164,6 +167,23 @@ int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw,
                      float* losses, uint8_t* masks, int64_t ldm,
                      crbq_block_trace* traces, void* ws, size_t ws_bytes,
                      void* stream);
+
+/* Allocation-free variant of crbq_fasterquant.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as crbq_fasterquant without the
+ * workspace: the scratch it needs (crbq_fasterquant_workspace_size(R, C, p)
+ * bytes) lives in a static device array of CRBQ_NOALLOC_SCRATCH_BYTES per
+ * device, which every GPU the library runs on holds until the process
+ * ends; larger problems (for blocksize 128: R above about 16000 rows)
+ * return CRBQ_ERR_TOO_LARGE.  It calls no hipMalloc / hipFree.  All calls
+ * on one device share that device's scratch, so calls that overlap on one
+ * GPU (different streams, or host threads) race: serialize them. */
+#define CRBQ_NOALLOC_SCRATCH_BYTES ((size_t)80 << 20)
+int crbq_fasterquant_noalloc(float* W, int64_t R, int64_t C, int64_t ldw,
+                             const float* U, int64_t ldu, const crbq_params* p,
+                             float* losses, uint8_t* masks, int64_t ldm,
+                             crbq_block_trace* traces, void* stream);
 
 /* ---- one-block pieces (for tests and the Binarization API) --------------
  * Search of one column block (utils/structure.py:8-20): writes the
