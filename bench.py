@@ -221,15 +221,38 @@ def _ev_ms(fn, reps):
     return a.elapsed_time(b) / reps
 
 
+def _graph_ms(fn, reps):
+    """Average ms of one fn() launch: reps calls captured in a HIP graph,
+    replayed between two events recorded on the replay stream."""
+    fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=s):
+            for _ in range(reps):
+                fn()
+    torch.cuda.synchronize()
+    gr.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        a.record(s)
+        gr.replay()
+        b.record(s)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
 def kernel_rooflines(dev, R=4096, C=16384, reps=20):
     """The block loop's kernels launched alone at the fc2 sublayer's shapes
     (R x C = 4096 x 16384, 128-column blocks, 1024-column super-blocks),
     each against its roofline:
     * trailing update W[:, sb1:] -= Err @ U[sb0:sb1, sb1:] (k_sgemm, fp32
       MFMA), K = 1024, N = 8192 remaining columns: 2 M N K flop;
-    * binarization (k_binarize_g, crb order 2) over 65536 rows x 128 columns
-      in one launch, 9 bytes per element (fp32 in, mask byte, fp32 out)
-      against HBM;
+    * binarization (k_binarize_g; crb order 2 and 1, braq and crbog order 2)
+      over 65536 rows x 128 columns in one launch, 9 bytes per element (fp32
+      in, mask byte, fp32 out) against HBM;
     * one block step (salient/split search + binarize + in-block error
       feedback, crbq_fasterquant on a 4096 x 128 block): its algorithmic
       bytes (W block in, U block in, Q, Err and masks out) against HBM;
@@ -251,17 +274,28 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
         "kernel": "k_sgemm<128> (fp32 MFMA)", "shape": [R, N, K], "ms": round(ms, 4),
         "achieved": round(fl / ms / 1e9, 1), "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
         "frac": round(fl / ms / 1e9 / (PEAK_F32 / 1e12), 3)}
-    # binarization, streaming shape
+    # binarization, streaming shape: launches of crbq_binarize through the C
+    # ABI (uint8 mask prepared once), captured in a HIP graph and replayed
+    # between two events on the replay stream, so the figure is the kernel's
+    # and not the Python wrapper's
     nb = 65536
     x = torch.randn(nb, 128, device=dev, generator=g) * 0.02
-    m = torch.rand(nb, 128, device=dev, generator=g) < 0.9
+    m = (torch.rand(nb, 128, device=dev, generator=g) < 0.9).to(torch.uint8)
     ob = torch.empty_like(x)
-    ms = _ev_ms(lambda: kernels.binarize(x, m, 2, "crb", out=ob), reps)
-    by = nb * 128 * 9
-    out["binarize"] = {
-        "kernel": "k_binarize_g<16> (crb, order 2)", "shape": [nb, 128], "ms": round(ms, 4),
-        "achieved": round(by / ms / 1e6, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-        "frac": round(by / ms / 1e6 / (PEAK_HBM / 1e9), 3)}
+    lib = _lib.ready(dev)
+    out["binarize"] = {}
+    for method, order in (("crb", 2), ("crb", 1), ("braq", 2), ("crbog", 2)):
+        def launch(method=method, order=order):
+            st = torch.cuda.current_stream().cuda_stream
+            _lib.check(lib.crbq_binarize(x.data_ptr(), nb, 128, 128, m.data_ptr(), 128, order,
+                                         _lib.METHODS[method], 1e-5, 0.1, 1, ob.data_ptr(),
+                                         128, st), "crbq_binarize")
+        ms = _graph_ms(launch, reps)
+        by = nb * 128 * 9
+        out["binarize"][f"{method}_order{order}"] = {
+            "kernel": "k_binarize_g (8 lanes x 16 columns per row)", "shape": [nb, 128],
+            "ms": round(ms, 5), "achieved": round(by / ms / 1e6, 1), "peak": PEAK_HBM / 1e9,
+            "unit": "GB/s", "frac": round(by / ms / 1e6 / (PEAK_HBM / 1e9), 3)}
     # one block step and the whole loop
     p = _lib.params("crb")
     U = torch.triu(torch.randn(C, C, device=dev, generator=g) * 1e-3)

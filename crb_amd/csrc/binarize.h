@@ -2,8 +2,10 @@
 // aligned group of LPR lanes (64: one wavefront per row; 16: four rows per
 // wavefront), EPL elements per lane.  Elementwise arithmetic is fp32 in the
 // reference's operation order (compiled with -ffp-contract=off so nothing is
-// fused); every row reduction is summed exactly enough in fp64 and rounded
-// to fp32, the value the reference's fp32 torch.sum approximates.
+// fused); row reductions are fp32 sums as the reference's torch.sum is: each
+// lane adds its EPL elements in order, then the lanes are combined pairwise
+// (DPP / permlane tree, every lane of the group ending with the same bits).
+// The order differs from torch's, so sums agree to fp32 rounding.
 #pragma once
 #include "common.h"
 
@@ -19,18 +21,37 @@ struct CrbConsts {
 
 template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rsum(const float (&v)[EPL], const bool (&m)[EPL]) {
-  double s = 0.0;
+  float s = 0.f;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) s += m[e] ? (double)v[e] : 0.0;
-  return (float)group_sum<LPR>(s);
+  for (int e = 0; e < EPL; ++e) s += m[e] ? v[e] : 0.f;
+  return group_sum_f<LPR>(s);
 }
 
 template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rsum_abs(const float (&v)[EPL], const bool (&m)[EPL]) {
-  double s = 0.0;
+  float s = 0.f;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) s += m[e] ? (double)fabsf(v[e]) : 0.0;
-  return (float)group_sum<LPR>(s);
+  for (int e = 0; e < EPL; ++e) s += m[e] ? fabsf(v[e]) : 0.f;
+  return group_sum_f<LPR>(s);
+}
+
+// x / d for an integer-valued d in [1, 1024] given r = 1 / d (IEEE): the
+// product and one fma correction give the correctly rounded quotient, the
+// same bits as x / d (checked for every fp32 significand and every such d:
+// tests/test_arith.py), for 3 instructions instead of a full division.
+__device__ __forceinline__ float div_cnt(float x, float d, float r) {
+  const float q = x * r;
+  const float e = __builtin_fmaf(-q, d, x);
+  return __builtin_fmaf(e, r, q);
+}
+
+// sum of values that are already 0 outside the mask
+template <int EPL, int LPR = 64>
+__device__ __forceinline__ float rsum_z(const float (&v)[EPL]) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) s += v[e];
+  return group_sum_f<LPR>(s);
 }
 
 template <int EPL, int LPR = 64>
@@ -46,16 +67,17 @@ template <int EPL, int LPR = 64>
 __device__ void hor_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
                         float (&acc)[EPL]) {
   const float cnt = rcount<EPL, LPR>(m);
+  const float rc = 1.f / fmaxf(cnt, 1.f);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
   for (int od = 0; od < order; ++od) {
     float c[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) c[e] = x[e] - acc[e];            // residual
-    const float mu = cnt > 0.f ? rsum<EPL, LPR>(c, m) / cnt : 0.f;           // nanmean, NaN->0
+    const float mu = cnt > 0.f ? div_cnt(rsum<EPL, LPR>(c, m), cnt, rc) : 0.f;  // nanmean, NaN->0
 #pragma unroll
     for (int e = 0; e < EPL; ++e) c[e] = c[e] - mu;
-    const float alpha = cnt > 0.f ? rsum_abs<EPL, LPR>(c, m) / cnt : 0.f;
+    const float alpha = cnt > 0.f ? div_cnt(rsum_abs<EPL, LPR>(c, m), cnt, rc) : 0.f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
       float b = tsign(c[e]) * alpha;
@@ -81,78 +103,87 @@ __device__ __forceinline__ void crb_solve(float d, float c12, float c1w, float c
 }
 
 // coupled_residual_binarization_stable_v7, binary.py:1544-1638.
+// Outside the mask cen = 0, so B1 = sign(cen) = 0 there and every
+// cen - a*B term is 0 too: those values need no mask, and their sums none
+// either (the reference multiplies them by the mask, giving the same zeros).
+// Only the signs taken of shifted values (B2 and the refined B1) and the
+// output are masked explicitly.
 template <int EPL, int LPR = 64>
 __device__ void crb_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
                         const CrbConsts& k, float (&out)[EPL],
                         float* scales = nullptr) {
   const float d = rcount<EPL, LPR>(m);
   const float ds = fmaxf(d, 1.f);
-  const float mean = rsum<EPL, LPR>(x, m) / ds;
+  const float rds = 1.f / ds;
+  const float mean = div_cnt(rsum<EPL, LPR>(x, m), ds, rds);
   float cen[EPL], B1[EPL], B2[EPL], t[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) cen[e] = m[e] ? x[e] - mean : 0.f;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) B1[e] = m[e] ? tsign(cen[e]) : 0.f;
+  for (int e = 0; e < EPL; ++e) B1[e] = tsign(cen[e]);
+  float ac[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) ac[e] = fabsf(cen[e]);
+  const float sabs = rsum_z<EPL, LPR>(ac);
   if (order == 1) {                                                 // :1570-1576
-    const float a1 = rsum_abs<EPL, LPR>(cen, m) / ds;
+    const float a1 = div_cnt(sabs, ds, rds);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) out[e] = m[e] ? mean + a1 * B1[e] : 0.f;
     if (scales) { scales[0] = mean; scales[1] = 0.f; scales[2] = a1; scales[3] = 0.f; }
     return;
   }
-  const float a10 = rsum_abs<EPL, LPR>(cen, m) / ds;                          // step 2
+  const float a10 = div_cnt(sabs, ds, rds);                          // step 2
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) t[e] = m[e] ? cen[e] - a10 * B1[e] : 0.f;   // step 3
-  const float rmean = rsum<EPL, LPR>(t, m) / ds;
+  for (int e = 0; e < EPL; ++e) t[e] = cen[e] - a10 * B1[e];        // step 3
+  const float rmean = div_cnt(rsum_z<EPL, LPR>(t), ds, rds);
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) B2[e] = m[e] ? tsign(t[e] - rmean) : 0.f;
+  for (int e = 0; e < EPL; ++e) B2[e] = tsign_m(m[e], t[e] - rmean);
   float c12, c1w, c2w, a1, a2;
   {                                                                 // step 4
 #pragma unroll
     for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
-    c12 = rsum<EPL, LPR>(t, m);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B1[e];
-    c1w = rsum<EPL, LPR>(t, m);
+    c12 = rsum_z<EPL, LPR>(t);
+    // cen * B1 = |cen| elementwise (B1 = sign(cen) here): the same sum as a10's
+    c1w = sabs;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B2[e];
-    c2w = rsum<EPL, LPR>(t, m);
+    c2w = rsum_z<EPL, LPR>(t);
   }
   crb_solve(d, c12, c1w, c2w, k, a1, a2);
   if (!k.skip) {
     for (int it = 0; it < k.iters; ++it) {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) t[e] = m[e] ? cen[e] - a1 * B1[e] : 0.f;  // step 5
-      const float t5m = rsum<EPL, LPR>(t, m) / ds;
+      for (int e = 0; e < EPL; ++e) t[e] = cen[e] - a1 * B1[e];     // step 5
+      const float t5m = div_cnt(rsum_z<EPL, LPR>(t), ds, rds);
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) B2[e] = m[e] ? tsign(t[e] - t5m) : 0.f;
+      for (int e = 0; e < EPL; ++e) B2[e] = tsign_m(m[e], t[e] - t5m);
 #pragma unroll
       for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B2[e];
-      c2w = rsum<EPL, LPR>(t, m);
+      c2w = rsum_z<EPL, LPR>(t);
 #pragma unroll
       for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
-      c12 = rsum<EPL, LPR>(t, m);
+      c12 = rsum_z<EPL, LPR>(t);
       crb_solve(d, c12, c1w, c2w, k, a1, a2);
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) t[e] = m[e] ? cen[e] - a2 * B2[e] : 0.f;  // step 6
-      const float t6m = rsum<EPL, LPR>(t, m) / ds;
+      for (int e = 0; e < EPL; ++e) t[e] = cen[e] - a2 * B2[e];     // step 6
+      const float t6m = div_cnt(rsum_z<EPL, LPR>(t), ds, rds);
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) B1[e] = m[e] ? tsign(t[e] - t6m) : 0.f;
+      for (int e = 0; e < EPL; ++e) B1[e] = tsign_m(m[e], t[e] - t6m);
 #pragma unroll
       for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B1[e];
-      c1w = rsum<EPL, LPR>(t, m);
+      c1w = rsum_z<EPL, LPR>(t);
 #pragma unroll
       for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
-      c12 = rsum<EPL, LPR>(t, m);
+      c12 = rsum_z<EPL, LPR>(t);
       crb_solve(d, c12, c1w, c2w, k, a1, a2);
     }
   }
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {                                   // step 7
     const float ap = a1 * B1[e] + a2 * B2[e];
-    t[e] = m[e] ? cen[e] - ap : 0.f;
+    t[e] = cen[e] - ap;
   }
-  const float muc = rsum<EPL, LPR>(t, m) / ds;
+  const float muc = div_cnt(rsum_z<EPL, LPR>(t), ds, rds);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     float v = mean + muc;
@@ -172,14 +203,15 @@ __device__ void crbog_row(const float (&x)[EPL], const bool (&m)[EPL], int order
 #pragma unroll
   for (int e = 0; e < EPL; ++e) out[e] = 0.f;
   if (n == 0.f) return;                                             // :647-649
-  const float mean = rsum<EPL, LPR>(x, m) / n;
+  const float rn = 1.f / n;
+  const float mean = div_cnt(rsum<EPL, LPR>(x, m), n, rn);
   float cen[EPL], B1[EPL], B2[EPL], t[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) { cen[e] = x[e] - mean; B1[e] = tsign(cen[e]); }
-  float a1 = rsum_abs<EPL, LPR>(cen, m) / n;
+  float a1 = div_cnt(rsum_abs<EPL, LPR>(cen, m), n, rn);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) { t[e] = cen[e] - a1 * B1[e]; B2[e] = tsign(t[e]); }
-  float a2 = rsum_abs<EPL, LPR>(t, m) / n;
+  float a2 = div_cnt(rsum_abs<EPL, LPR>(t, m), n, rn);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
   const double c12 = (double)rsum<EPL, LPR>(t, m);
@@ -205,20 +237,27 @@ __device__ void crbog_row(const float (&x)[EPL], const bool (&m)[EPL], int order
   }
 }
 
-// Binarization.quantize dispatch, binary.py:2874-2890.
-template <int EPL, int LPR = 64>
+// Method families of Binarization.quantize (binary.py:2874-2890): kernels
+// are instantiated per family so each carries only its own registers.
+enum { MF_BRAQ = 0, MF_CRB = 1, MF_CRBOG = 2 };
+__host__ __device__ inline int method_family(int method) {
+  return method == CRBQ_BRAQ ? MF_BRAQ : (method == CRBQ_CRBOG ? MF_CRBOG : MF_CRB);
+}
+
+// Binarization.quantize dispatch, binary.py:2874-2890, within a family.
+template <int MF, int EPL, int LPR = 64>
 __device__ __forceinline__ void binarize_row(int method, const float (&x)[EPL],
                                              const bool (&m)[EPL], int order,
                                              const CrbConsts& base, float (&out)[EPL]) {
-  switch (method) {
-    case CRBQ_BRAQ: hor_row<EPL, LPR>(x, m, order, out); break;
-    case CRBQ_CRBOG: crbog_row<EPL, LPR>(x, m, order, out); break;
-    default: {
-      CrbConsts k = base;
-      k.skip = (method == CRBQ_CRB_NOREFINE || method == CRBQ_CRB_SYMDAMP_NOREFINE);
-      k.sym = (method == CRBQ_CRB_SYMDAMP || method == CRBQ_CRB_SYMDAMP_NOREFINE);
-      crb_row<EPL, LPR>(x, m, order, k, out);
-    }
+  if (MF == MF_BRAQ) {
+    hor_row<EPL, LPR>(x, m, order, out);
+  } else if (MF == MF_CRBOG) {
+    crbog_row<EPL, LPR>(x, m, order, out);
+  } else {
+    CrbConsts k = base;
+    k.skip = (method == CRBQ_CRB_NOREFINE || method == CRBQ_CRB_SYMDAMP_NOREFINE);
+    k.sym = (method == CRBQ_CRB_SYMDAMP || method == CRBQ_CRB_SYMDAMP_NOREFINE);
+    crb_row<EPL, LPR>(x, m, order, k, out);
   }
 }
 

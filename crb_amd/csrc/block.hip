@@ -1073,7 +1073,7 @@ struct QuantArgs {
   uint8_t* masks; int64_t ldm;       // optional
 };
 
-template <int EPL>
+template <int MF, int EPL>
 __global__ __launch_bounds__(256) void k_quantize(QuantArgs a, SearchWs s) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -1111,7 +1111,7 @@ __global__ __launch_bounds__(256) void k_quantize(QuantArgs a, SearchWs s) {
     for (int e = 0; e < EPL; ++e) { m[e] = grp[e] == g; any |= m[e]; }
     (void)any;
     float out[EPL];
-    binarize_row<EPL>(a.method, x, m, a.orders[g], a.k, out);
+    binarize_row<MF, EPL>(a.method, x, m, a.orders[g], a.k, out);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) if (m[e]) q[e] = out[e];
   }
@@ -1141,6 +1141,7 @@ __global__ __launch_bounds__(256) void k_quantize(QuantArgs a, SearchWs s) {
 // rows per workgroup), 8 elements per lane at columns 4r .. 4r+3 and
 // 64 + 4r .. 64 + 4r+3, 16-byte loads and stores (W, err and their row
 // strides 16-byte aligned, masks 4-byte aligned; the host checks).
+template <int MF>
 __global__ __launch_bounds__(256) void k_quantize_g(QuantArgs a, SearchWs s) {
   constexpr int EPL = 8, LPR = 16;
   const int r = threadIdx.x % LPR;
@@ -1188,7 +1189,7 @@ __global__ __launch_bounds__(256) void k_quantize_g(QuantArgs a, SearchWs s) {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) m[e] = grp[e] == g;
     float out[EPL];
-    binarize_row<EPL, LPR>(a.method, x, m, a.orders[g], a.k, out);
+    binarize_row<MF, EPL, LPR>(a.method, x, m, a.orders[g], a.k, out);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) if (m[e]) q[e] = out[e];
   }
@@ -1462,10 +1463,18 @@ static int fasterquant_impl(float* W, int64_t R, int64_t C, int64_t ldw, const f
       const bool vec = ((uintptr_t)Wb % 16 == 0) && ldw % 4 == 0 &&
                        ((uintptr_t)a.err % 16 == 0) && a.lde % 4 == 0 &&
                        (!a.masks || (((uintptr_t)a.masks % 4 == 0) && ldm % 4 == 0));
-      if (vec && nc <= 128)
-        k_quantize_g<<<(unsigned)cdiv(R, 16), 256, 0, hs>>>(a, s);
-      else
-        k_quantize<2><<<(unsigned)cdiv(R, 4), 256, 0, hs>>>(a, s);
+      const int mf = method_family(p->method);
+#define CRBQ_QUANT_GO(MF_)                                                  \
+  do {                                                                      \
+    if (vec && nc <= 128)                                                   \
+      k_quantize_g<MF_><<<(unsigned)cdiv(R, 16), 256, 0, hs>>>(a, s);       \
+    else                                                                    \
+      k_quantize<MF_, 2><<<(unsigned)cdiv(R, 4), 256, 0, hs>>>(a, s);       \
+  } while (0)
+      if (mf == MF_BRAQ) CRBQ_QUANT_GO(MF_BRAQ);
+      else if (mf == MF_CRBOG) CRBQ_QUANT_GO(MF_CRBOG);
+      else CRBQ_QUANT_GO(MF_CRB);
+#undef CRBQ_QUANT_GO
       CRBQ_LAUNCH_CHECK();
       const int64_t ed = st0 + nc;
       if (gptq && ed < sb1) {            // rest of this super-block
@@ -1536,7 +1545,7 @@ extern "C" int crbq_fasterquant_noalloc(float* W, int64_t R, int64_t C, int64_t 
 // standalone Binarization.quantize
 // ---------------------------------------------------------------------------
 namespace crbq {
-template <int EPL>
+template <int MF, int EPL>
 __global__ __launch_bounds__(256) void k_binarize(const float* x, int R, int nc, int64_t ldx,
                                                   const uint8_t* __restrict__ mask, int64_t ldm,
                                                   int order, int method, CrbConsts k, float* out,
@@ -1553,24 +1562,25 @@ __global__ __launch_bounds__(256) void k_binarize(const float* x, int R, int nc,
     v[e] = ok ? x[(int64_t)row * ldx + c] : 0.f;
     m[e] = ok && mask[(int64_t)row * ldm + c] != 0;
   }
-  binarize_row<EPL>(method, v, m, order, k, o);
+  binarize_row<MF, EPL>(method, v, m, order, k, o);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     const int c = lane + 64 * e;
     if (c < nc) out[(int64_t)row * ldo + c] = o[e];
   }
 }
-// Rows of at most 4 * LPR columns, LPR lanes per row (256 / LPR rows per
-// workgroup), 8 elements per lane: lane r of a row holds columns
-// 4r .. 4r+3 and 4 LPR + 4r .. 4 LPR + 4r+3, moved with 16-byte accesses
-// (x, out and their row strides 16-byte aligned, mask rows 4-byte aligned;
-// the host checks).  Row reductions stay inside the row's lane group.
-template <int LPR>
+// Rows of at most EPL * LPR columns, LPR lanes per row (256 / LPR rows per
+// workgroup), EPL elements per lane: lane r of a row holds columns
+// h * 4 LPR + 4r .. h * 4 LPR + 4r + 3 for h < EPL / 4, moved with 16-byte
+// accesses (x, out and their row strides 16-byte aligned, mask rows 4-byte
+// aligned; the host checks).  Row reductions stay inside the row's lane
+// group.
+template <int MF, int LPR, int EPL>
 __global__ __launch_bounds__(256) void k_binarize_g(const float* x, int R, int nc, int64_t ldx,
                                                     const uint8_t* __restrict__ mask, int64_t ldm,
                                                     int order, int method, CrbConsts k,
                                                     float* out, int64_t ldo) {
-  constexpr int EPL = 8;
+  constexpr int NH = EPL / 4;
   const int r = threadIdx.x % LPR;
   const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
   if (row >= R) return;                      // whole lane groups leave together
@@ -1579,7 +1589,7 @@ __global__ __launch_bounds__(256) void k_binarize_g(const float* x, int R, int n
   const float* xr = x + (int64_t)row * ldx;
   const uint8_t* mr = mask + (int64_t)row * ldm;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < NH; ++h) {
     const int c0 = h * 4 * LPR + r * 4;
     if (c0 + 3 < nc) {
       const float4 q = *(const float4*)(xr + c0);
@@ -1596,10 +1606,10 @@ __global__ __launch_bounds__(256) void k_binarize_g(const float* x, int R, int n
       }
     }
   }
-  binarize_row<EPL, LPR>(method, v, m, order, k, o);
+  binarize_row<MF, EPL, LPR>(method, v, m, order, k, o);
   float* orow = out + (int64_t)row * ldo;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < NH; ++h) {
     const int c0 = h * 4 * LPR + r * 4;
     if (c0 + 3 < nc) {
       *(float4*)(orow + c0) = make_float4(o[4 * h], o[4 * h + 1], o[4 * h + 2], o[4 * h + 3]);
@@ -1612,6 +1622,9 @@ __global__ __launch_bounds__(256) void k_binarize_g(const float* x, int R, int n
 }
 }  // namespace crbq
 
+#ifndef CRBQ_BIN_LPR
+#define CRBQ_BIN_LPR 8
+#endif
 extern "C" int crbq_binarize(const float* x, int64_t R, int32_t ncols, int64_t ldx,
                              const uint8_t* mask, int64_t ldm, int32_t order, int32_t method,
                              float lam, float corr_damp, int32_t refine_iters, float* out,
@@ -1630,23 +1643,35 @@ extern "C" int crbq_binarize(const float* x, int64_t R, int32_t ncols, int64_t l
   const int r = (int)R;
   const bool vec = ((uintptr_t)x % 16 == 0) && ((uintptr_t)out % 16 == 0) && ldx % 4 == 0 &&
                    ldo % 4 == 0 && ((uintptr_t)mask % 4 == 0) && ldm % 4 == 0;
-  if (vec && ncols <= 128) {
-    k_binarize_g<16><<<(unsigned)cdiv(R, 16), 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order,
-                                                          method, k, out, ldo);
-    CRBQ_LAUNCH_CHECK();
-    return CRBQ_OK;
-  }
-  if (vec && ncols <= 256) {
-    k_binarize_g<32><<<(unsigned)cdiv(R, 8), 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order,
-                                                         method, k, out, ldo);
-    CRBQ_LAUNCH_CHECK();
-    return CRBQ_OK;
-  }
-  const unsigned g = (unsigned)cdiv(R, 4);
-  if (ncols <= 128) k_binarize<2><<<g, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, out, ldo);
-  else if (ncols <= 256) k_binarize<4><<<g, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, out, ldo);
-  else if (ncols <= 512) k_binarize<8><<<g, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, out, ldo);
-  else k_binarize<16><<<g, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, out, ldo);
+  const unsigned g4 = (unsigned)cdiv(R, 4);
+#define CRBQ_BIN_GO(MF_)                                                                   \
+  do {                                                                                     \
+    if (vec && ncols <= 128)                                                               \
+      k_binarize_g<MF_, CRBQ_BIN_LPR, 128 / CRBQ_BIN_LPR>                                    \
+          <<<(unsigned)cdiv(R, 256 / CRBQ_BIN_LPR), 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, \
+                                                                order, method, k, out, ldo); \
+    else if (vec && ncols <= 256)                                                          \
+      k_binarize_g<MF_, 32, 8><<<(unsigned)cdiv(R, 8), 256, 0, hs>>>(x, r, ncols, ldx, mask, \
+                                                                      ldm, order, method, k, \
+                                                                      out, ldo);           \
+    else if (ncols <= 128)                                                                 \
+      k_binarize<MF_, 2><<<g4, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, \
+                                             out, ldo);                                    \
+    else if (ncols <= 256)                                                                 \
+      k_binarize<MF_, 4><<<g4, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, \
+                                             out, ldo);                                    \
+    else if (ncols <= 512)                                                                 \
+      k_binarize<MF_, 8><<<g4, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, k, \
+                                             out, ldo);                                    \
+    else                                                                                   \
+      k_binarize<MF_, 16><<<g4, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method,  \
+                                              k, out, ldo);                                \
+  } while (0)
+  const int mf = method_family(method);
+  if (mf == MF_BRAQ) CRBQ_BIN_GO(MF_BRAQ);
+  else if (mf == MF_CRBOG) CRBQ_BIN_GO(MF_CRBOG);
+  else CRBQ_BIN_GO(MF_CRB);
+#undef CRBQ_BIN_GO
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }

@@ -21,9 +21,14 @@ typedef __bf16 b8_t __attribute__((ext_vector_type(8)));
 
 namespace crbq {
 
-// torch.sign: (0 < x) - (x < 0); +-0 and NaN give 0.
+// torch.sign: (0 < x) - (x < 0); +-0 and NaN give 0.  |x| > 0 is false
+// exactly for +-0 and NaN, and copysign gives +-1 otherwise.
 __device__ __forceinline__ float tsign(float x) {
-  return (float)((0.f < x) - (x < 0.f));
+  return fabsf(x) > 0.f ? __builtin_copysignf(1.f, x) : 0.f;
+}
+// tsign(x) inside a mask, 0 outside
+__device__ __forceinline__ float tsign_m(bool m, float x) {
+  return (m && fabsf(x) > 0.f) ? __builtin_copysignf(1.f, x) : 0.f;
 }
 
 // torch.clamp(x, min=0): NaN propagates.
