@@ -38,7 +38,10 @@ constexpr int NQ = 81;       // percentiles linspace(0.10, 0.90, 81)
 constexpr int NT = 2 * NQ;   // order statistics needed (lo, hi per percentile)
 constexpr int NCMAX = 128;   // widest block
 constexpr int UPMAX = 64;    // largest supported up_lim
-constexpr int Q_RPW = 16;    // rows per workgroup in the quantile passes
+#ifndef CRBQ_Q_RPW
+#define CRBQ_Q_RPW 16
+#endif
+constexpr int Q_RPW = CRBQ_Q_RPW;   // rows per workgroup in the quantile passes
 #ifndef CRBQ_CS_MAXWG
 #define CRBQ_CS_MAXWG 128
 #endif
@@ -75,9 +78,7 @@ enum { CNT_CS = 0, CNT_A = 1, CNT_C = 2 };
 struct Tgt {         // one order statistic being selected
   int64_t rank;      // absolute rank in the sorted flattened block
   int bin1, r1;      // level-1 bin and rank within it
-  int slot1;         // leader target index of bin1
-  int bin2, r2;
-  int bin3;
+  int slot1;         // leader target index of bin1 (the first target in it)
 };
 
 struct SearchWs {
@@ -90,9 +91,9 @@ struct SearchWs {
   int* slot1map;     // [H1]
   Tgt* tgt;          // [NT]
   float* gam;        // [NQ]
-  uint32_t* hist2;   // [NXCD][NT][H2]
-  int* slot2map;     // [NT][H2]
-  uint32_t* hist3;   // [NT][H3]
+  int* list_off;     // [NT]: start of each leader target's element list
+  int* list_cnt;     // [NT]: elements appended to it
+  uint32_t* lists;   // [R * NCMAX]: bit patterns of the elements of every target bin
   float* tval;       // [NT]
   float* pvals;      // [NQ]
 };
@@ -109,9 +110,9 @@ static void carve_search(WsCarver& c, int64_t R, SearchWs& s) {
   s.slot1map = c.take<int>(H1);
   s.tgt = c.take<Tgt>(NT);
   s.gam = c.take<float>(NQ);
-  s.hist2 = c.take<uint32_t>((size_t)NXCD * NT * H2);
-  s.slot2map = c.take<int>((size_t)NT * H2);
-  s.hist3 = c.take<uint32_t>((size_t)NT * H3);
+  s.list_off = c.take<int>(NT);
+  s.list_cnt = c.take<int>(NT);
+  s.lists = c.take<uint32_t>((size_t)R * NCMAX);
   s.tval = c.take<float>(NT);
   s.pvals = c.take<float>(NQ);
 }
@@ -208,10 +209,8 @@ __global__ __launch_bounds__(CS_THREADS) void k_colscore(
       acc += (double)fabsf(target_of(W[(int64_t)r * ldw + col], d2, metric));
   }
   part[ph][col] = acc;
-  // zero the histograms used later by this block (grid-stride)
+  // zero the level-1 histogram used later by this block (grid-stride)
   const size_t gsz = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)NT * H3; i += gsz)
-    s.hist3[i] = 0u;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)H1; i += gsz) s.hist1[i] = 0u;
   __syncthreads();
   if (ph == 0) {
@@ -222,14 +221,25 @@ __global__ __launch_bounds__(CS_THREADS) void k_colscore(
   }
   if (!last_block(&s.ctrl->cnt[CNT_CS])) return;
   reduce_partials<NCMAX, CS_PH>(s.colpart, NCMAX, gridDim.x, NCMAX, red, sc);
-  // rank of column c by descending score, ties to the lower column
+  // rank of column c by descending score, ties to the lower column: phase
+  // ph counts the columns k = ph, ph + CS_PH, ... that precede c
+  __shared__ int cntp[CS_PH][NCMAX];
+  {
+    const int c = col;
+    const double v = sc[c];
+    int r = 0;
+    if (c < nc)
+      for (int k = ph; k < nc; k += CS_PH) r += (sc[k] > v) || (sc[k] == v && k < c);
+    cntp[ph][c] = r;
+  }
+  __syncthreads();
   if (tid < NCMAX) {
     const int c = tid;
-    const double v = sc[c];
     int r = NCMAX;
     if (c < nc) {
       r = 0;
-      for (int k = 0; k < nc; ++k) r += (sc[k] > v) || (sc[k] == v && k < c);
+#pragma unroll
+      for (int q = 0; q < CS_PH; ++q) r += cntp[q][c];
     }
     s.rank[c] = r;
   }
@@ -474,6 +484,48 @@ __global__ __launch_bounds__(64 * NW) void k_phase_a(
 // ---------------------------------------------------------------------------
 // exact float32 np.quantile of S = |T * ~M3| (utils/autosearch.py:62-68)
 // ---------------------------------------------------------------------------
+// The passes' per-thread elements: element i = tid + 256 k of the
+// workgroup's rows (row r0 + i / nc, column i % nc).  Every load of W is
+// issued before any is used, so the loads overlap instead of each waiting
+// out a memory latency.
+constexpr int QE = Q_RPW * NCMAX / 256;
+static_assert(QE * 256 == Q_RPW * NCMAX, "quantile pass geometry");
+
+__device__ __forceinline__ void q_load(const float* __restrict__ W, int64_t ldw, int r0, int r1,
+                                       int nc, float (&w)[QE], int (&col)[QE]) {
+  const int n = (r1 - r0) * nc;
+#pragma unroll
+  for (int k = 0; k < QE; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    col[k] = -1;
+    w[k] = 0.f;
+    if (i < n) {
+      const int r = r0 + i / nc, c = i - (i / nc) * nc;
+      col[k] = c;
+      w[k] = W[(int64_t)r * ldw + c];
+    }
+  }
+}
+
+// rank and squared U diagonal of every column into LDS
+__device__ __forceinline__ void q_cols(const float* __restrict__ U, int64_t ldu, int nc,
+                                       const SearchWs& s, int* rk, float* d2s) {
+  const int c = threadIdx.x;
+  if (c < NCMAX) {
+    rk[c] = s.rank[c];
+    if (c < nc) { const float dg = U[(int64_t)c * ldu + c]; d2s[c] = dg * dg; }
+  }
+}
+
+// the level-1 leader map into LDS (H1 / 256 loads per thread, issued together)
+__device__ __forceinline__ void q_slotmap(const SearchWs& s, int* sm) {
+  int v[H1 / 256];
+#pragma unroll
+  for (int k = 0; k < H1 / 256; ++k) v[k] = s.slot1map[threadIdx.x + 256 * k];
+#pragma unroll
+  for (int k = 0; k < H1 / 256; ++k) sm[threadIdx.x + 256 * k] = v[k];
+}
+
 // Level-1: histogram of bits [31:20] of the (non-negative) float pattern.
 __global__ __launch_bounds__(256) void k_qpass1(
     const float* __restrict__ W, int64_t ldw, int R, int nc,
@@ -482,26 +534,20 @@ __global__ __launch_bounds__(256) void k_qpass1(
   __shared__ float d2s[NCMAX];
   __shared__ int rk[NCMAX];
   const int tid = threadIdx.x;
+  const int r0 = blockIdx.x * Q_RPW, r1 = min(R, r0 + Q_RPW);
+  float w[QE];
+  int col[QE];
+  q_load(W, ldw, r0, r1, nc, w, col);
   for (int i = tid; i < H1; i += 256) lh[i] = 0u;
   const int istar = s.ctrl->istar;
-  for (int c = tid; c < NCMAX; c += 256) {
-    rk[c] = s.rank[c];
-    if (c < nc) { const float dg = U[(int64_t)c * ldu + c]; d2s[c] = dg * dg; }
-  }
+  q_cols(U, ldu, nc, s, rk, d2s);
   __syncthreads();
-  const int r0 = blockIdx.x * Q_RPW, r1 = min(R, r0 + Q_RPW);
-  for (int i = tid; i < (r1 - r0) * nc; i += 256) {
-    const int r = r0 + i / nc, c = i % nc;
-    if (rk[c] < istar) continue;           // M3 zeros are counted below
-    const float v = fabsf(target_of(W[(int64_t)r * ldw + c], d2s[c], metric));
+#pragma unroll
+  for (int k = 0; k < QE; ++k) {
+    const int c = col[k];
+    if (c < 0 || rk[c] < istar) continue;  // M3 zeros are counted below
+    const float v = fabsf(target_of(w[k], d2s[c], metric));
     atomicAdd(&lh[__float_as_uint(v) >> SH1], 1u);
-  }
-  // zero the level-2 copies for k_qpass2 (16-byte stores, grid-stride)
-  {
-    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-    uint4* h2 = (uint4*)s.hist2;
-    const size_t n4 = (size_t)NXCD * NT * H2 / 4, gsz = (size_t)gridDim.x * 256;
-    for (size_t i = (size_t)blockIdx.x * 256 + tid; i < n4; i += gsz) h2[i] = z;
   }
   __syncthreads();
   for (int i = tid; i < H1; i += 256)
@@ -515,32 +561,32 @@ __global__ __launch_bounds__(256) void k_qpass1(
 
 // Block-wide exclusive scan of H (multiple of 256) counters in LDS.
 // The counters are the sums of NC copies `cstride` apart.
-template <int H, int NC = 1>
-__device__ void block_scan(const uint32_t* __restrict__ src, uint32_t* cum,
-                           uint32_t* tmp /* 256 */, size_t cstride = 0) {
+// The first 256 threads do the work; every thread of the workgroup (256 or
+// more) must call it, for the barriers.
+template <int H>
+__device__ void block_scan(const uint32_t* src, uint32_t* cum, uint32_t* tmp /* 256 */) {
   constexpr int PER = H / 256;
   const int tid = threadIdx.x;
+  const bool act = tid < 256;
   uint32_t loc[PER];
   uint32_t sum = 0;
 #pragma unroll
-  for (int k = 0; k < PER; ++k) loc[k] = src[tid * PER + k];
-#pragma unroll
-  for (int x = 1; x < NC; ++x)
-#pragma unroll
-    for (int k = 0; k < PER; ++k) loc[k] += src[x * cstride + tid * PER + k];
+  for (int k = 0; k < PER; ++k) loc[k] = act ? src[tid * PER + k] : 0u;
 #pragma unroll
   for (int k = 0; k < PER; ++k) sum += loc[k];
-  tmp[tid] = sum;
+  if (act) tmp[tid] = sum;
   __syncthreads();
   for (int o = 1; o < 256; o <<= 1) {
-    const uint32_t v = tid >= o ? tmp[tid - o] : 0u;
+    const uint32_t v = (act && tid >= o) ? tmp[tid - o] : 0u;
     __syncthreads();
-    tmp[tid] += v;
+    if (act) tmp[tid] += v;
     __syncthreads();
   }
-  uint32_t run = tmp[tid] - sum;
+  if (act) {
+    uint32_t run = tmp[tid] - sum;
 #pragma unroll
-  for (int k = 0; k < PER; ++k) { cum[tid * PER + k] = run; run += loc[k]; }
+    for (int k = 0; k < PER; ++k) { cum[tid * PER + k] = run; run += loc[k]; }
+  }
   __syncthreads();
 }
 
@@ -578,120 +624,171 @@ __global__ __launch_bounds__(256) void k_qscan1(int64_t n, SearchWs s) {
     s.tgt[2 * tid + 1].rank = hi;
   }
   __syncthreads();
+  __shared__ int bins[NT];
   if (tid < NT) {
     Tgt& t = s.tgt[tid];
     const uint32_t r = (uint32_t)t.rank;
     const int b = find_bin<H1>(cum, r);
     t.bin1 = b;
     t.r1 = (int)(r - cum[b]);
+    bins[tid] = b;
     atomicMin(&lead[b], tid);
   }
   __syncthreads();
   for (int i = tid; i < H1; i += 256) s.slot1map[i] = lead[i] == NONE ? -1 : lead[i];
-  if (tid < NT) s.tgt[tid].slot1 = lead[s.tgt[tid].bin1];
+  if (tid < NT) s.tgt[tid].slot1 = lead[bins[tid]];
+  // element lists of the target bins, one per leader, in target order; a
+  // list's capacity is its bin's count (bin 0's also counts the salient
+  // columns' zeros, which are not stored): exclusive scan over the targets
+  __shared__ uint32_t cap[256];
+  if (tid < NT) s.list_cnt[tid] = 0;
+  {
+    uint32_t c = 0;
+    if (tid < NT) {
+      const int b = bins[tid];
+      if (lead[b] == tid) c = (b + 1 < H1 ? cum[b + 1] : (uint32_t)n) - cum[b];
+    }
+    cap[tid] = c;
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {
+      const uint32_t v = tid >= o ? cap[tid - o] : 0u;
+      __syncthreads();
+      cap[tid] += v;
+      __syncthreads();
+    }
+    if (tid < NT) s.list_off[tid] = (int)(cap[tid] - c);
+  }
 }
 
-// Level-2: bits [19:10] of elements whose level-1 bin holds a target.
-__global__ __launch_bounds__(256) void k_qpass2(
+// Elements of the target bins into their leader's list: each workgroup
+// counts its elements per list in LDS, reserves room with one global atomic
+// per list, then writes the elements' bit patterns (the order inside a list
+// does not matter to the selection).
+__global__ __launch_bounds__(256) void k_qlist(
     const float* __restrict__ W, int64_t ldw, int R, int nc,
     const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
   __shared__ int sm[H1];
   __shared__ float d2s[NCMAX];
   __shared__ int rk[NCMAX];
+  __shared__ int cnt[NT];
+  __shared__ int base[NT];
   const int tid = threadIdx.x;
-  for (int i = tid; i < H1; i += 256) sm[i] = s.slot1map[i];
-  const int istar = s.ctrl->istar;
-  for (int c = tid; c < NCMAX; c += 256) {
-    rk[c] = s.rank[c];
-    if (c < nc) { const float dg = U[(int64_t)c * ldu + c]; d2s[c] = dg * dg; }
-  }
-  // reset the level-2 leader map (read by k_qscan2 / k_qpass3 only)
-  const size_t gsz = (size_t)gridDim.x * 256;
-  for (size_t i = (size_t)blockIdx.x * 256 + tid; i < (size_t)NT * H2; i += gsz)
-    s.slot2map[i] = NONE;
-  __syncthreads();
-  uint32_t* h2 = s.hist2 + (size_t)xcd_id() * NT * H2;
   const int r0 = blockIdx.x * Q_RPW, r1 = min(R, r0 + Q_RPW);
-  for (int i = tid; i < (r1 - r0) * nc; i += 256) {
-    const int r = r0 + i / nc, c = i % nc;
-    if (rk[c] < istar) continue;
-    const float v = fabsf(target_of(W[(int64_t)r * ldw + c], d2s[c], metric));
-    const uint32_t key = __float_as_uint(v);
-    const int sl = sm[key >> SH1];
-    if (sl >= 0)
-      __hip_atomic_fetch_add(&h2[(size_t)sl * H2 + ((key >> SH2) & (H2 - 1))], 1u,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  float w[QE];
+  int col[QE];
+  q_load(W, ldw, r0, r1, nc, w, col);
+  q_slotmap(s, sm);
+  const int istar = s.ctrl->istar;
+  q_cols(U, ldu, nc, s, rk, d2s);
+  if (tid < NT) cnt[tid] = 0;
+  __syncthreads();
+  int slot[QE], pos[QE];
+  uint32_t key[QE];
+#pragma unroll
+  for (int k = 0; k < QE; ++k) {
+    const int c = col[k];
+    slot[k] = -1;
+    pos[k] = 0;
+    key[k] = 0u;
+    if (c < 0 || rk[c] < istar) continue;  // salient columns: implicit zeros
+    const float v = fabsf(target_of(w[k], d2s[c], metric));
+    key[k] = __float_as_uint(v);
+    const int sl = sm[key[k] >> SH1];
+    if (sl >= 0) {
+      slot[k] = sl;
+      pos[k] = atomicAdd(&cnt[sl], 1);
+    }
   }
-  if (blockIdx.x == 0 && tid == 0 && sm[0] >= 0) {
-    int nsal = 0;
-    for (int c = 0; c < nc; ++c) nsal += rk[c] < istar;
-    if (nsal)
-      __hip_atomic_fetch_add(&h2[(size_t)sm[0] * H2], (uint32_t)R * (uint32_t)nsal,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __syncthreads();
+  if (tid < NT && cnt[tid] > 0) base[tid] = s.list_off[tid] + atomicAdd(&s.list_cnt[tid], cnt[tid]);
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < QE; ++k)
+    if (slot[k] >= 0) s.lists[base[slot[k]] + pos[k]] = key[k];
+}
+
+// One workgroup per target: the r1-th smallest bit pattern of its level-1
+// bin, from the bin's list, by two histogram rounds (bits [19:10], then
+// bits [9:0] among the elements with the chosen [19:10]).  In bin 0 the
+// salient columns' R * nsal zeros come first.
+constexpr int QS_T = 1024;           // threads per target
+constexpr int QS_UNROLL = 8;
+constexpr int QS_LDS = 32768;        // lists up to this long are staged in LDS (128 KB)
+template <bool ROUND_B>
+__device__ void qselect_hist(const uint32_t* list, int n, int b2, uint32_t* h) {
+  for (int i0 = threadIdx.x; i0 < n; i0 += QS_T * QS_UNROLL) {
+    uint32_t k[QS_UNROLL];
+#pragma unroll
+    for (int u = 0; u < QS_UNROLL; ++u) {
+      const int i = i0 + QS_T * u;
+      k[u] = i < n ? list[i] : 0xffffffffu;
+    }
+#pragma unroll
+    for (int u = 0; u < QS_UNROLL; ++u) {
+      if (i0 + QS_T * u >= n) continue;
+      const uint32_t mid = (k[u] >> SH2) & (H2 - 1);
+      if (!ROUND_B) atomicAdd(&h[mid], 1u);
+      else if ((int)mid == b2) atomicAdd(&h[k[u] & (H3 - 1)], 1u);
+    }
   }
 }
 
-// one workgroup per target: resolve its level-2 bin; elect level-2 leaders
-__global__ __launch_bounds__(256) void k_qscan2(SearchWs s) {
+__global__ __launch_bounds__(QS_T) void k_qselect(int R, int nc, SearchWs s) {
+  static_assert(H2 == H3, "one histogram buffer for both rounds");
+  __shared__ uint32_t h[H2];
   __shared__ uint32_t cum[H2];
   __shared__ uint32_t tmp[256];
-  const int t = blockIdx.x;
-  const int sl = s.tgt[t].slot1;
-  block_scan<H2, NXCD>(s.hist2 + (size_t)sl * H2, cum, tmp, (size_t)NT * H2);
-  if (threadIdx.x == 0) {
-    Tgt& g = s.tgt[t];
-    const int b = find_bin<H2>(cum, (uint32_t)g.r1);
-    g.bin2 = b;
-    g.r2 = (int)((uint32_t)g.r1 - cum[b]);
-    atomicMin(&s.slot2map[(size_t)sl * H2 + b], t);
-  }
-}
-
-// Level-3: bits [9:0] of elements whose (level-1, level-2) prefix holds a target.
-__global__ __launch_bounds__(256) void k_qpass3(
-    const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
-  __shared__ int sm[H1];
-  __shared__ float d2s[NCMAX];
-  __shared__ int rk[NCMAX];
-  const int tid = threadIdx.x;
-  for (int i = tid; i < H1; i += 256) sm[i] = s.slot1map[i];
-  const int istar = s.ctrl->istar;
-  for (int c = tid; c < NCMAX; c += 256) {
-    rk[c] = s.rank[c];
-    if (c < nc) { const float dg = U[(int64_t)c * ldu + c]; d2s[c] = dg * dg; }
-  }
-  __syncthreads();
-  const int r0 = blockIdx.x * Q_RPW, r1 = min(R, r0 + Q_RPW);
-  for (int i = tid; i < (r1 - r0) * nc; i += 256) {
-    const int r = r0 + i / nc, c = i % nc;
-    if (rk[c] < istar) continue;
-    const float v = fabsf(target_of(W[(int64_t)r * ldw + c], d2s[c], metric));
-    const uint32_t key = __float_as_uint(v);
-    const int sl = sm[key >> SH1];
-    if (sl < 0) continue;
-    const int l2 = s.slot2map[(size_t)sl * H2 + ((key >> SH2) & (H2 - 1))];
-    if (l2 != NONE) atomicAdd(&s.hist3[(size_t)l2 * H3 + (key & (H3 - 1))], 1u);
-  }
-  if (blockIdx.x == 0 && tid == 0 && sm[0] >= 0) {
-    const int l2 = s.slot2map[(size_t)sm[0] * H2];
-    int nsal = 0;
-    for (int c = 0; c < nc; ++c) nsal += rk[c] < istar;
-    if (l2 != NONE && nsal) atomicAdd(&s.hist3[(size_t)l2 * H3], (uint32_t)R * (uint32_t)nsal);
-  }
-}
-
-__global__ __launch_bounds__(256) void k_qscan3(SearchWs s) {
-  __shared__ uint32_t cum[H3];
-  __shared__ uint32_t tmp[256];
-  const int t = blockIdx.x;
+  __shared__ int nsal;
+  const int t = blockIdx.x, tid = threadIdx.x;
   const Tgt g = s.tgt[t];
-  const int l2 = s.slot2map[(size_t)g.slot1 * H2 + g.bin2];
-  block_scan<H3>(s.hist3 + (size_t)l2 * H3, cum, tmp);
-  if (threadIdx.x == 0) {
-    const int b = find_bin<H3>(cum, (uint32_t)g.r2);
-    s.tgt[t].bin3 = b;
-    const uint32_t key = ((uint32_t)g.bin1 << SH1) | ((uint32_t)g.bin2 << SH2) | (uint32_t)b;
+  if (tid == 0) nsal = 0;
+  __syncthreads();
+  if (g.bin1 == 0 && tid < nc && s.rank[tid] < s.ctrl->istar) atomicAdd(&nsal, 1);
+  __syncthreads();
+  uint32_t r = (uint32_t)g.r1;
+  if (g.bin1 == 0) {
+    const uint32_t nz = (uint32_t)R * (uint32_t)nsal;
+    if (r < nz) {                            // one of the salient columns' zeros
+      if (tid == 0) s.tval[t] = 0.f;
+      return;
+    }
+    r -= nz;
+  }
+  const uint32_t* glist = s.lists + s.list_off[g.slot1];
+  const int n = s.list_cnt[g.slot1];
+  __shared__ uint32_t stage[QS_LDS];
+  const uint32_t* list = glist;
+  if (n <= QS_LDS) {                         // one read of the list from memory
+    for (int i0 = tid; i0 < n; i0 += QS_T * QS_UNROLL) {
+      uint32_t k[QS_UNROLL];
+#pragma unroll
+      for (int u = 0; u < QS_UNROLL; ++u) k[u] = i0 + QS_T * u < n ? glist[i0 + QS_T * u] : 0u;
+#pragma unroll
+      for (int u = 0; u < QS_UNROLL; ++u)
+        if (i0 + QS_T * u < n) stage[i0 + QS_T * u] = k[u];
+    }
+    list = stage;
+  }
+  for (int i = tid; i < H2; i += QS_T) h[i] = 0u;
+  __syncthreads();
+  qselect_hist<false>(list, n, 0, h);
+  __syncthreads();
+  block_scan<H2>(h, cum, tmp);
+  __shared__ int b2s, r2s;
+  if (tid == 0) {
+    const int b = find_bin<H2>(cum, r);
+    b2s = b;
+    r2s = (int)(r - cum[b]);
+  }
+  for (int i = tid; i < H3; i += QS_T) h[i] = 0u;
+  __syncthreads();
+  const int b2 = b2s;
+  qselect_hist<true>(list, n, b2, h);
+  __syncthreads();
+  block_scan<H3>(h, cum, tmp);
+  if (tid == 0) {
+    const int b3 = find_bin<H3>(cum, (uint32_t)r2s);
+    const uint32_t key = ((uint32_t)g.bin1 << SH1) | ((uint32_t)b2 << SH2) | (uint32_t)b3;
     s.tval[t] = __uint_as_float(key);
   }
 }
@@ -1270,10 +1367,8 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
                                                                 ncand, up_lim, s, tr);
   k_qpass1<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_qscan1<<<1, 256, 0, st>>>((int64_t)R * nc, s);
-  k_qpass2<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  k_qscan2<<<NT, 256, 0, st>>>(s);
-  k_qpass3<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  k_qscan3<<<NT, 256, 0, st>>>(s);
+  k_qlist<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
+  k_qselect<<<NT, QS_T, 0, st>>>(R, nc, s);
   k_phase_c<<<nwg_c, 64 * PC_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s, tr);
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;

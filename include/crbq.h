@@ -175,7 +175,7 @@ int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw,
  * workspace: the scratch it needs (crbq_fasterquant_workspace_size(R, C, p)
  * bytes) lives in a static device array of CRBQ_NOALLOC_SCRATCH_BYTES per
  * device, which every GPU the library runs on holds until the process
- * ends; larger problems (for blocksize 128: R above about 16000 rows)
+ * ends; larger problems (for blocksize 128: R above about 18000 rows)
  * return CRBQ_ERR_TOO_LARGE.  It calls no hipMalloc / hipFree.  All calls
  * on one device share that device's scratch, so calls that overlap on one
  * GPU (different streams, or host threads) race: serialize them. */
