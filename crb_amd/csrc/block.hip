@@ -162,17 +162,27 @@ __device__ __forceinline__ bool last_block(uint32_t* cnt) {
 }
 
 // Fixed-order sum of nwg partials (row stride `stride` doubles) for `ncand`
-// candidates with NK * PARTS threads: PARTS threads per candidate, each
-// summing every PARTS-th partial, then the PARTS subtotals in order.
+// candidates with NK * PARTS threads: thread (k, pp) adds partials
+// g = pp * G .. pp * G + G - 1 (G = ceil(nwg / PARTS) <= GMAX) of candidate
+// k in order, loading all of them before the first add (the partials were
+// written by other workgroups, so every load goes out to memory: one round
+// trip instead of one per batch), then the PARTS subtotals in order.
 // Result in out[0..ncand).
-template <int NK, int PARTS>
+template <int NK, int PARTS, int GMAX>
 __device__ void reduce_partials(const double* part, int stride, int nwg, int ncand,
                                 double (*red)[NK], double* out) {
   const int t = threadIdx.x, k = t % NK, pp = t / NK;
+  const int G = (nwg + PARTS - 1) / PARTS;
   double v = 0.0;
   if (k < ncand && pp < PARTS) {
-#pragma unroll 8
-    for (int g = pp; g < nwg; g += PARTS) v += part[(size_t)g * stride + k];
+    double x[GMAX];
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j) {
+      const int g = pp * G + j;
+      x[j] = (j < G && g < nwg) ? part[(size_t)g * stride + k] : 0.0;
+    }
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j) v += x[j];
   }
   if (pp < PARTS) red[pp][k] = v;
   __syncthreads();
@@ -182,6 +192,27 @@ __device__ void reduce_partials(const double* part, int stride, int nwg, int nca
     out[t] = a;
   }
   __syncthreads();
+}
+
+// Index of the first strict minimum of v[0..n) (the reference's
+// `if e < best` scan from best = inf), or -1 when no value is below
+// infinity (NaN never wins); computed by the calling wavefront, every lane
+// gets the result.  Each lane scans its indices in ascending order, then
+// pairs combine keeping the smaller value and, on equal values, the
+// smaller index.
+__device__ int wave_argmin(const double* v, int n) {
+  const int lane = threadIdx.x & 63;
+  double b = INFINITY;
+  int bi = 0x7fffffff;
+  for (int j = lane; j < n; j += 64)
+    if (v[j] < b) { b = v[j]; bi = j; }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const double ob = __shfl_xor(b, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (ob < b || (ob == b && oi < bi)) { b = ob; bi = oi; }
+  }
+  return bi == 0x7fffffff ? -1 : bi;
 }
 
 // ---------------------------------------------------------------------------
@@ -220,7 +251,7 @@ __global__ __launch_bounds__(CS_THREADS) void k_colscore(
     s.colpart[(size_t)blockIdx.x * NCMAX + col] = v;
   }
   if (!last_block(&s.ctrl->cnt[CNT_CS])) return;
-  reduce_partials<NCMAX, CS_PH>(s.colpart, NCMAX, gridDim.x, NCMAX, red, sc);
+  reduce_partials<NCMAX, CS_PH, CS_MAXWG / CS_PH>(s.colpart, NCMAX, gridDim.x, NCMAX, red, sc);
   // rank of column c by descending score, ties to the lower column: phase
   // ph counts the columns k = ph, ph + CS_PH, ... that precede c
   __shared__ int cntp[CS_PH][NCMAX];
@@ -468,14 +499,14 @@ __global__ __launch_bounds__(64 * NW) void k_phase_a(
     s.parta[(size_t)blockIdx.x * UPMAX + tid] = v;
   }
   if (!last_block(&s.ctrl->cnt[CNT_A])) return;
-  reduce_partials<UPMAX, NW>(s.parta, UPMAX, gridDim.x, ncand, red, e);
-  if (tid == 0) {
-    double best = INFINITY;
-    int istar = max(1, up_lim / 3);                                  // :43
-    for (int k = 0; k < ncand; ++k)
-      if (e[k] < best) { best = e[k]; istar = k + 1; }
-    s.ctrl->istar = istar;
-    if (tr) tr->i_star = istar;
+  reduce_partials<UPMAX, NW, (PX_MAXWG + NW - 1) / NW>(s.parta, UPMAX, gridDim.x, ncand, red, e);
+  if (tid < 64) {
+    const int am = wave_argmin(e, ncand);
+    const int istar = am < 0 ? max(1, up_lim / 3) : am + 1;         // :43
+    if (tid == 0) {
+      s.ctrl->istar = istar;
+      if (tr) tr->i_star = istar;
+    }
   }
   if (tr && tid < UPMAX) tr->errs_a[tid] = (tid >= 1 && tid <= ncand) ? e[tid - 1] : 0.0;
 }
@@ -1004,7 +1035,7 @@ __global__ __launch_bounds__(1024) void k_phase_a_pairs(
   __shared__ __attribute__((aligned(16))) float xs[PF_RB][XS];
   __shared__ double pre[PF_RB][NCMAX + 1];   // pre[q][k]: sum of ranks [0, k) of row q
   __shared__ double errs[1024];
-  __shared__ double red[8][UPMAX];
+  __shared__ double red[9][UPMAX];
   __shared__ double e[UPMAX];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
   const bool act = tid < PF_RB * ncand;
@@ -1076,14 +1107,14 @@ __global__ __launch_bounds__(1024) void k_phase_a_pairs(
     s.parta[(size_t)blockIdx.x * UPMAX + tid] = v;
   }
   if (!last_block(&s.ctrl->cnt[CNT_A])) return;
-  reduce_partials<UPMAX, 8>(s.parta, UPMAX, gridDim.x, ncand, red, e);
-  if (tid == 0) {
-    double best = INFINITY;
-    int istar = max(1, up_lim / 3);                                  // :43
-    for (int k = 0; k < ncand; ++k)
-      if (e[k] < best) { best = e[k]; istar = k + 1; }
-    s.ctrl->istar = istar;
-    if (tr) tr->i_star = istar;
+  reduce_partials<UPMAX, 9, (PX_MAXWG + 8) / 9>(s.parta, UPMAX, gridDim.x, ncand, red, e);
+  if (tid < 64) {
+    const int am = wave_argmin(e, ncand);
+    const int istar = am < 0 ? max(1, up_lim / 3) : am + 1;         // :43
+    if (tid == 0) {
+      s.ctrl->istar = istar;
+      if (tr) tr->i_star = istar;
+    }
   }
   if (tr && tid < UPMAX) tr->errs_a[tid] = (tid >= 1 && tid <= ncand) ? e[tid - 1] : 0.0;
 }
@@ -1092,7 +1123,7 @@ __global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
     const float* __restrict__ W, int64_t ldw, int R, int nc,
     const float* __restrict__ U, int64_t ldu, int metric, SearchWs s, crbq_block_trace* tr) {
   __shared__ SortedRow rows[PC_WAVES];
-  __shared__ double red[PC_WAVES / 2][128];
+  __shared__ double red[10][96];
   __shared__ double e[128];
   __shared__ float pv[NQ];
   __shared__ double errs[PC_WAVES][NQ];
@@ -1142,17 +1173,17 @@ __global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
   __syncthreads();
   for (int k = tid; k < NQ; k += 64 * PC_WAVES) s.partc[(size_t)blockIdx.x * 96 + k] = acc[k];
   if (!last_block(&s.ctrl->cnt[CNT_C])) return;
-  reduce_partials<128, PC_WAVES / 2>(s.partc, 96, gridDim.x, NQ, red, e);
-  if (tid == 0) {
-    double best = INFINITY;
-    int ks = NQ / 2;                                                 // :71 median
-    for (int j = 0; j < NQ; ++j)
-      if (e[j] < best) { best = e[j]; ks = j; }
-    s.ctrl->kstar = ks;
-    s.ctrl->split = s.pvals[ks];
-    if (tr) { tr->k_star = ks; tr->split = s.pvals[ks]; }
+  reduce_partials<96, 10, (PX_MAXWG + 9) / 10>(s.partc, 96, gridDim.x, NQ, red, e);
+  if (tid < 64) {
+    const int am = wave_argmin(e, NQ);
+    const int ks = am < 0 ? NQ / 2 : am;                             // :71 median
+    if (tid == 0) {
+      s.ctrl->kstar = ks;
+      s.ctrl->split = pv[ks];
+      if (tr) { tr->k_star = ks; tr->split = pv[ks]; }
+    }
   }
-  if (tr && tid < NQ) { tr->errs_c[tid] = e[tid]; tr->pvals[tid] = s.pvals[tid]; }
+  if (tr && tid < NQ) { tr->errs_c[tid] = e[tid]; tr->pvals[tid] = pv[tid]; }
 }
 
 // ---------------------------------------------------------------------------
@@ -1359,7 +1390,7 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
   if (two)
     k_phase_a<PA2_WAVES, true><<<nwg_a, 64 * PA2_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric,
                                                                  ncand, up_lim, s, tr);
-  else if (pairs)   // wavefronts for PF_RB * ncand pairs (>= 9: reduce_partials uses 512)
+  else if (pairs)   // wavefronts for PF_RB * ncand pairs (>= 9: reduce_partials uses 576)
     k_phase_a_pairs<<<nwg_a, 64 * (int)cdiv(PF_RB * ncand, 64), 0, st>>>(
         W, ldw, R, nc, U, ldu, metric, ncand, up_lim, s, tr);
   else
