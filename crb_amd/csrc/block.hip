@@ -1020,6 +1020,58 @@ __device__ __forceinline__ void wave_prefix(SortedRow& r, float x0, float x1, in
   r.v[lane + 64] = x1;
 }
 
+// The pure part of a row (ranks >= ncand, never salient: always in the
+// complement group) sorted by value with fp64 prefix sums, so each
+// candidate's two passes over it are closed forms with binary searches
+// instead of loops.  Sign decisions use the fp32 expressions of the
+// elementwise passes as search predicates (each is monotone in x); the sums
+// are fp64 closed forms of the same quantities.
+template <typename P>
+__device__ __forceinline__ int first_true(const float* v, int lo, int hi, P pred) {
+  while (lo < hi) {
+    const int m = (lo + hi) >> 1;
+    if (pred(v[m])) hi = m; else lo = m + 1;
+  }
+  return lo;
+}
+
+// sum |x - m1| and the sign counts over the sorted pure part (pass_abs)
+__device__ __forceinline__ void pure_abs(const SortedRow& r, int np, float m1, GroupA& C,
+                                         int& lb, int& ub) {
+  lb = lbound(r.v, np, m1);
+  ub = ubound(r.v, np, m1);
+  const double m = (double)m1;
+  C.ad += ((r.S[np] - r.S[ub]) - (double)(np - ub) * m) + ((double)lb * m - r.S[lb]);
+  C.npos += np - ub;
+  C.nneg += lb;
+}
+
+// |e|, e^2 and e != 0 summed over the sorted range [l, h) split at the e = 0
+// run [z, t): e < 0 below z, e > 0 from t, with e = x - c
+__device__ __forceinline__ void pure_range(const SortedRow& r, int l, int z, int t, int h,
+                                           double c, GroupA& C) {
+  const Stat lo = rstat(r, l, z), hi = rstat(r, t, h);
+  C.e1 += (lo.n * c - lo.s) + (hi.s - hi.n * c);
+  C.e2 += sqdev(lo, c) + sqdev(hi, c);
+  C.nz += (z - l) + (h - t);
+}
+
+// pass_res over the sorted pure part: e = fl(fl(x - s1) - m2), s1 = hi above
+// m1, lo below, m1 at m1 (where e = -m2)
+__device__ __forceinline__ void pure_res(const SortedRow& r, int np, int lb, int ub,
+                                         const ParA& g, GroupA& C) {
+  const int zA = first_true(r.v, ub, np, [&](float x) { return x - g.hi >= g.m2; });
+  const int sA = first_true(r.v, zA, np, [&](float x) { return x - g.hi > g.m2; });
+  pure_range(r, ub, zA, sA, np, (double)g.hi + (double)g.m2, C);
+  const int zB = first_true(r.v, 0, lb, [&](float x) { return x - g.lo >= g.m2; });
+  const int sB = first_true(r.v, zB, lb, [&](float x) { return x - g.lo > g.m2; });
+  pure_range(r, 0, zB, sB, lb, (double)g.lo + (double)g.m2, C);
+  const int nm = ub - lb;
+  C.e1 += (double)nm * fabs((double)g.m2);
+  C.e2 += (double)nm * ((double)g.m2 * (double)g.m2);
+  C.nz += g.m2 != 0.f ? nm : 0;
+}
+
 // Salient-count candidates as (row, candidate) pairs when 32 < ncand <= 64:
 // PF_RB rows per workgroup iteration, thread f evaluates row f / ncand with
 // candidate f % ncand + 1, so only the tail of the last wavefront idles
@@ -1034,6 +1086,7 @@ __global__ __launch_bounds__(1024) void k_phase_a_pairs(
   constexpr int XS = NCMAX + 4;
   __shared__ __attribute__((aligned(16))) float xs[PF_RB][XS];
   __shared__ double pre[PF_RB][NCMAX + 1];   // pre[q][k]: sum of ranks [0, k) of row q
+  __shared__ SortedRow pure[PF_RB];          // ranks >= mix_end, sorted by value
   __shared__ double errs[1024];
   __shared__ double red[9][UPMAX];
   __shared__ double e[UPMAX];
@@ -1048,6 +1101,7 @@ __global__ __launch_bounds__(1024) void k_phase_a_pairs(
   if (c1 < nc) { const float dg = U[(int64_t)c1 * ldu + c1]; d21 = dg * dg; }
   const float nS = (float)i, nC = (float)(nc - i);
   const int mix_end = min(nc, ncand);
+  const int np = nc - mix_end;                 // pure part: ranks [mix_end, nc)
   double acc = 0.0;
   for (int r0 = blockIdx.x * PF_RB; r0 < R; r0 += gridDim.x * PF_RB) {
     __syncthreads();                             // previous rows' readers are done
@@ -1068,6 +1122,12 @@ __global__ __launch_bounds__(1024) void k_phase_a_pairs(
         pre[qq][lane + 1] = p0;
         pre[qq][lane + 65] = p1;
         if (lane == 0) pre[qq][0] = 0.0;
+        if (np > 0) {
+          float z0 = mix_end + lane < nc ? xs[qq][mix_end + lane] : INFINITY;
+          float z1 = mix_end + 64 + lane < nc ? xs[qq][mix_end + 64 + lane] : INFINITY;
+          wave_sort128(z0, z1);
+          wave_prefix(pure[qq], z0, z1, np);
+        }
       }
     }
     __syncthreads();
@@ -1079,7 +1139,8 @@ __global__ __launch_bounds__(1024) void k_phase_a_pairs(
       const float m1C = nC > 0.f ? (float)(tot - ps) / nC : 0.f;
       GroupA S = {0.0, 0.0, 0.0, 0, 0, 0}, Cg = {0.0, 0.0, 0.0, 0, 0, 0};
       pass_abs<true>(x, 0, mix_end, i, m1S, m1C, S, Cg);
-      pass_abs<false>(x, mix_end, nc, i, m1S, m1C, S, Cg);
+      int lb = 0, ub = 0;
+      if (np > 0) pure_abs(pure[q], np, m1C, Cg, lb, ub);
       const float a1S = (float)S.ad / nS;
       const float a1C = nC > 0.f ? (float)Cg.ad / nC : 0.f;
       float hiS = a1S + m1S, loS = -a1S + m1S, hiC = a1C + m1C, loC = -a1C + m1C;
@@ -1091,7 +1152,7 @@ __global__ __launch_bounds__(1024) void k_phase_a_pairs(
       const float m2C = nC > 0.f ? (float)((tot - ps) - s1C) / nC : 0.f;
       const ParA PS = {m1S, hiS, loS, m2S}, PC = {m1C, hiC, loC, m2C};
       pass_res<true>(x, 0, mix_end, i, PS, PC, S, Cg);
-      pass_res<false>(x, mix_end, nc, i, PS, PC, S, Cg);
+      if (np > 0) pure_res(pure[q], np, lb, ub, PC, Cg);
       const double a2S = (double)((float)S.e1 / nS);
       const double a2C = nC > 0.f ? (double)((float)Cg.e1 / nC) : 0.0;
       const double eS = S.e2 - 2.0 * a2S * S.e1 + a2S * a2S * (double)S.nz;
