@@ -310,7 +310,7 @@ struct GroupA {         // per-lane accumulators of one group
 };
 
 struct ParA {           // a group's fp32 parameters for the residual pass
-  float m1, hi, lo, m2;   // hi = fl(a1 + m1), lo = fl(-a1 + m1)
+  float m1, hi, lo, m2, a1;   // hi = fl(a1 + m1), lo = fl(-a1 + m1)
 };
 
 // sum |x - m1| and the sign counts of x - m1 over ranks [c0, c1)
@@ -352,10 +352,13 @@ __device__ __forceinline__ void pass_abs(const float* xs, int c0, int c1, int i,
 }
 
 // e = (x - s1) - m2 with s1 = sign(x - m1)*a1 + m1 in fp32 (binary.py:26,
-// 32-34): sign*a1 is exact, so s1 is one of hi, lo, m1
+// 32-34): sign*a1 is exact, so the fma rounds once, like the reference's
+// add, and s1 is one of hi, lo, m1 (arithmetic rather than a select chain,
+// which the compiler turns into branches)
 __device__ __forceinline__ float resid(float x, const ParA& g) {
   const float d = x - g.m1;
-  const float s1 = d > 0.f ? g.hi : (d < 0.f ? g.lo : g.m1);
+  const float sg = copysignf(d != 0.f ? 1.f : 0.f, d);
+  const float s1 = fmaf(sg, g.a1, g.m1);
   const float r = x - s1;
   return r - g.m2;
 }
@@ -370,6 +373,7 @@ __device__ __forceinline__ void res_elem(float x, bool inS, const ParA& PS, cons
     g.hi = inS ? PS.hi : PC.hi;
     g.lo = inS ? PS.lo : PC.lo;
     g.m2 = inS ? PS.m2 : PC.m2;
+    g.a1 = inS ? PS.a1 : PC.a1;
   }
   const float e = resid(x, g);
   const float ae = fabsf(e);
@@ -477,7 +481,7 @@ __global__ __launch_bounds__(64 * NW) void k_phase_a(
                          ((double)nC - Cg.npos - Cg.nneg) * (double)m1C;
       const float m2S = (float)(ps - s1S) / nS;
       const float m2C = nC > 0.f ? (float)((tot - ps) - s1C) / nC : 0.f;
-      const ParA PS = {m1S, hiS, loS, m2S}, PC = {m1C, hiC, loC, m2C};
+      const ParA PS = {m1S, hiS, loS, m2S, a1S}, PC = {m1C, hiC, loC, m2C, a1C};
       pass_res<true>(x, 0, mix_end, i, PS, PC, S, Cg);
       pass_res<false>(x, mix_end, nc, i, PS, PC, S, Cg);
       const double a2S = (double)((float)S.e1 / nS);
@@ -1150,7 +1154,7 @@ __global__ __launch_bounds__(1024) void k_phase_a_pairs(
                          ((double)nC - Cg.npos - Cg.nneg) * (double)m1C;
       const float m2S = (float)(ps - s1S) / nS;
       const float m2C = nC > 0.f ? (float)((tot - ps) - s1C) / nC : 0.f;
-      const ParA PS = {m1S, hiS, loS, m2S}, PC = {m1C, hiC, loC, m2C};
+      const ParA PS = {m1S, hiS, loS, m2S, a1S}, PC = {m1C, hiC, loC, m2C, a1C};
       pass_res<true>(x, 0, mix_end, i, PS, PC, S, Cg);
       if (np > 0) pure_res(pure[q], np, lb, ub, PC, Cg);
       const double a2S = (double)((float)S.e1 / nS);
@@ -1434,8 +1438,188 @@ __global__ void k_init_ctrl(SearchWs s) {
 }
 
 // ---------------------------------------------------------------------------
+// Salient-count candidates with the rows on the lanes: lane = row of a
+// 64-row group, wavefront = candidate i.  A candidate's salient group (ranks
+// [0, i)) and complement (ranks [i, nc)) are then wavefront-uniform ranges,
+// so each of the three passes (group sums, |x - m1| with sign counts,
+// residual moments) is two select-free loops, and no lane idles.  The group
+// sums run in fp64 (exact for these fp32 values unless their exponents span
+// more than 29 binades); the other passes sum in fp32 over chunks of 8
+// elements, accumulated in fp64, with integer counts.  A workgroup holds one
+// row group in LDS and evaluates cw candidates; ncg = ceil(ncand / cw)
+// workgroups share a row group, each writing its candidates' partial sums.
+// ---------------------------------------------------------------------------
+#ifndef CRBQ_PR_CW
+#define CRBQ_PR_CW 16
+#endif
+constexpr int PR_CW = CRBQ_PR_CW;   // most candidates (wavefronts) per workgroup
+constexpr int PR_MINW = 9;          // reduce_partials<UPMAX, 9> needs 576 threads
+constexpr int PR_XS = NCMAX + 4;    // row stride: 33 16-byte units
+
+struct RowAbs { double ad; int npos, nneg; };
+struct RowRes { double e1, e2; int nz; };
+
+__device__ __forceinline__ void row_abs(const float* x, int c0, int c1, float m1, RowAbs& a) {
+  int c = c0;
+  for (; c + 8 <= c1; c += 8) {
+    float p = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float d = x[c + u] - m1;
+      p += fabsf(d);
+      a.npos += d > 0.f ? 1 : 0;
+      a.nneg += d < 0.f ? 1 : 0;
+    }
+    a.ad += (double)p;
+  }
+  float p = 0.f;
+  for (; c < c1; ++c) {
+    const float d = x[c] - m1;
+    p += fabsf(d);
+    a.npos += d > 0.f ? 1 : 0;
+    a.nneg += d < 0.f ? 1 : 0;
+  }
+  a.ad += (double)p;
+}
+
+__device__ __forceinline__ void row_res(const float* x, int c0, int c1, const ParA& g,
+                                        RowRes& r) {
+  int c = c0;
+  for (; c + 8 <= c1; c += 8) {
+    float p1 = 0.f, p2 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float e = resid(x[c + u], g);
+      p1 += fabsf(e);
+      p2 += e * e;
+      r.nz += e != 0.f ? 1 : 0;
+    }
+    r.e1 += (double)p1;
+    r.e2 += (double)p2;
+  }
+  float p1 = 0.f, p2 = 0.f;
+  for (; c < c1; ++c) {
+    const float e = resid(x[c], g);
+    p1 += fabsf(e);
+    p2 += e * e;
+    r.nz += e != 0.f ? 1 : 0;
+  }
+  r.e1 += (double)p1;
+  r.e2 += (double)p2;
+}
+
+// fp64 sum of x[c0, c1): eight loads in flight per step, each step's
+// values summed in a tree first
+__device__ __forceinline__ double row_sum(const float* x, int c0, int c1) {
+  double a = 0.0;
+  int c = c0;
+  for (; c + 8 <= c1; c += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = x[c + u];
+    a += (((double)v[0] + (double)v[1]) + ((double)v[2] + (double)v[3])) +
+         (((double)v[4] + (double)v[5]) + ((double)v[6] + (double)v[7]));
+  }
+  for (; c < c1; ++c) a += (double)x[c];
+  return a;
+}
+
+// order-2 residual binarization error of {ranks [0, i)} + {ranks [i, nc)}
+// of one row x in rank order (binary.py:17-41 via utils/autosearch.py:44-55)
+__device__ __forceinline__ double row_cand_err(const float* x, int i, int nc) {
+  const float nS = (float)i, nC = (float)(nc - i);
+  const double ps = row_sum(x, 0, i), pc = row_sum(x, i, nc);
+  const float m1S = (float)ps / nS;
+  const float m1C = nC > 0.f ? (float)pc / nC : 0.f;
+  RowAbs aS = {0.0, 0, 0}, aC = {0.0, 0, 0};
+  row_abs(x, 0, i, m1S, aS);
+  row_abs(x, i, nc, m1C, aC);
+  const float a1S = (float)aS.ad / nS;
+  const float a1C = nC > 0.f ? (float)aC.ad / nC : 0.f;
+  // sum r = sum x - sum s1, s1 in {fl(a1 + m1), fl(-a1 + m1), m1}
+  const float hiS = a1S + m1S, loS = -a1S + m1S, hiC = a1C + m1C, loC = -a1C + m1C;
+  const double s1S = aS.npos * (double)hiS + aS.nneg * (double)loS +
+                     ((double)nS - aS.npos - aS.nneg) * (double)m1S;
+  const double s1C = aC.npos * (double)hiC + aC.nneg * (double)loC +
+                     ((double)nC - aC.npos - aC.nneg) * (double)m1C;
+  const float m2S = (float)(ps - s1S) / nS;
+  const float m2C = nC > 0.f ? (float)(pc - s1C) / nC : 0.f;
+  const ParA PS = {m1S, hiS, loS, m2S, a1S}, PC = {m1C, hiC, loC, m2C, a1C};
+  RowRes rS = {0.0, 0.0, 0}, rC = {0.0, 0.0, 0};
+  row_res(x, 0, i, PS, rS);
+  row_res(x, i, nc, PC, rC);
+  // sum (e - a2 sign(e))^2 = sum e^2 - 2 a2 sum |e| + a2^2 #(e != 0)
+  const double a2S = (double)((float)rS.e1 / nS);
+  const double a2C = nC > 0.f ? (double)((float)rC.e1 / nC) : 0.0;
+  return (rS.e2 - 2.0 * a2S * rS.e1 + a2S * a2S * (double)rS.nz) +
+         (rC.e2 - 2.0 * a2C * rC.e1 + a2C * a2C * (double)rC.nz);
+}
+
+__global__ __launch_bounds__(64 * PR_CW) void k_phase_a_rows(
+    const float* __restrict__ W, int64_t ldw, int R, int nc,
+    const float* __restrict__ U, int64_t ldu, int metric, int ncand, int up_lim, int ncg,
+    int cw, SearchWs s, crbq_block_trace* tr) {
+  constexpr int LMAX = (64 + PR_MINW - 1) / PR_MINW;   // rows loaded per wavefront
+  __shared__ __attribute__((aligned(16))) float xs[64][PR_XS];
+  __shared__ double red[PR_MINW][UPMAX];
+  __shared__ double e[UPMAX];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
+  const int cg = (int)blockIdx.x % ncg, nrg = (int)gridDim.x / ncg;
+  const int i = cg * cw + wv + 1;                // this wavefront's candidate
+  const bool live = wv < cw && i <= ncand;
+  const int c0 = lane, c1 = lane + 64;
+  const int rk0 = c0 < nc ? s.rank[c0] : -1, rk1 = c1 < nc ? s.rank[c1] : -1;
+  float d20 = 1.f, d21 = 1.f;
+  if (c0 < nc) { const float dg = U[(int64_t)c0 * ldu + c0]; d20 = dg * dg; }
+  if (c1 < nc) { const float dg = U[(int64_t)c1 * ldu + c1]; d21 = dg * dg; }
+  double acc = 0.0;
+  for (int rg = (int)blockIdx.x / ncg; rg * 64 < R; rg += nrg) {
+    const int r0 = rg * 64;
+    __syncthreads();                             // previous rows' readers are done
+    float v0[LMAX], v1[LMAX];                    // every load issued before the first store
+#pragma unroll
+    for (int k = 0; k < LMAX; ++k) {
+      const int q = wv + k * nw, rq = r0 + q;
+      const bool ok = q < 64 && rq < R;
+      v0[k] = ok && rk0 >= 0 ? W[(int64_t)rq * ldw + c0] : 0.f;
+      v1[k] = ok && rk1 >= 0 ? W[(int64_t)rq * ldw + c1] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < LMAX; ++k) {
+      const int q = wv + k * nw;
+      if (q < 64) {
+        if (rk0 >= 0) xs[q][rk0] = target_of(v0[k], d20, metric);
+        if (rk1 >= 0) xs[q][rk1] = target_of(v1[k], d21, metric);
+      }
+    }
+    __syncthreads();
+    if (live) {
+      const double err = row_cand_err(xs[lane], i, nc);
+      const double t = lane63_f64(wave_scan_f64(r0 + lane < R ? err : 0.0));
+      acc += t;
+    }
+  }
+  if (live && lane == 0) s.parta[(size_t)((int)blockIdx.x / ncg) * UPMAX + (i - 1)] = acc;
+  if (!last_block(&s.ctrl->cnt[CNT_A])) return;
+  reduce_partials<UPMAX, PR_MINW, (PX_MAXWG + PR_MINW - 1) / PR_MINW>(s.parta, UPMAX, nrg,
+                                                                      ncand, red, e);
+  if (tid < 64) {
+    const int am = wave_argmin(e, ncand);
+    const int istar = am < 0 ? max(1, up_lim / 3) : am + 1;         // :43
+    if (tid == 0) {
+      s.ctrl->istar = istar;
+      if (tr) tr->i_star = istar;
+    }
+  }
+  if (tr && tid < UPMAX) tr->errs_a[tid] = (tid >= 1 && tid <= ncand) ? e[tid - 1] : 0.0;
+}
+
+// ---------------------------------------------------------------------------
 // host drivers
 // ---------------------------------------------------------------------------
+#ifndef CRBQ_PA_ROWS
+#define CRBQ_PA_ROWS 1
+#endif
 static int search_block(const float* W, int64_t ldw, int R, int nc, const float* U,
                         int64_t ldu, int metric, int up_lim, SearchWs& s,
                         crbq_block_trace* tr, hipStream_t st) {
@@ -1448,7 +1632,12 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
       cdiv(R, two ? 2 * PA2_WAVES : (pairs ? PF_RB : PA_WAVES)), PX_MAXWG);
   const int nwg_c = (int)std::min<int64_t>(cdiv(R, PC_WAVES), PX_MAXWG);
   k_colscore<<<nwg_cs, CS_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  if (two)
+  if (CRBQ_PA_ROWS) {
+    const int ncg = (int)cdiv(ncand, PR_CW), cw = (int)cdiv(ncand, ncg);
+    const int nrg = (int)std::min<int64_t>(cdiv(R, 64), PX_MAXWG);
+    k_phase_a_rows<<<nrg * ncg, 64 * std::max(cw, PR_MINW), 0, st>>>(
+        W, ldw, R, nc, U, ldu, metric, ncand, up_lim, ncg, cw, s, tr);
+  } else if (two)
     k_phase_a<PA2_WAVES, true><<<nwg_a, 64 * PA2_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric,
                                                                  ncand, up_lim, s, tr);
   else if (pairs)   // wavefronts for PF_RB * ncand pairs (>= 9: reduce_partials uses 576)
