@@ -251,7 +251,7 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
     * trailing update W[:, sb1:] -= Err @ U[sb0:sb1, sb1:] (k_sgemm, fp32
       MFMA), K = 1024, N = 8192 remaining columns: 2 M N K flop;
     * binarization (k_binarize_g; crb order 2 and 1, braq and crbog order 2)
-      over 65536 rows x 128 columns in one launch, 9 bytes per element (fp32
+      over 524288 rows x 128 columns in one launch, 9 bytes per element (fp32
       in, mask byte, fp32 out) against HBM;
     * one block step (salient/split search + binarize + in-block error
       feedback, crbq_fasterquant on a 4096 x 128 block): its algorithmic
@@ -278,7 +278,7 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
     # ABI (uint8 mask prepared once), captured in a HIP graph and replayed
     # between two events on the replay stream, so the figure is the kernel's
     # and not the Python wrapper's
-    nb = 65536
+    nb = 524288                 # 604 MB per launch: the launch gaps amortized
     x = torch.randn(nb, 128, device=dev, generator=g) * 0.02
     m = (torch.rand(nb, 128, device=dev, generator=g) < 0.9).to(torch.uint8)
     ob = torch.empty_like(x)
@@ -312,7 +312,7 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
     ms = _ev_ms(step, reps) - ms_copy
     by = R * 128 * 4 * 3 + 128 * 128 * 4 + R * 128
     out["block_step"] = {
-        "kernels": "colscore, phase_a, qpass1-3, qscan1-3, phase_c, quantize",
+        "kernels": "colscore, phase_a, qpass1, qscan1, qlist, qselect, phase_c, quantize",
         "shape": [R, 128], "ms": round(ms, 4), "achieved": round(by / ms / 1e6, 1),
         "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(by / ms / 1e6 / (PEAK_HBM / 1e9), 4),
         "note": "2 MB working set per block, resident in L2/MALL; bound by the search's "
@@ -482,6 +482,9 @@ def main():
                     help="layers of the OPT-6.7B-shaped stack run (0: skip)")
     ap.add_argument("--fc2-last", action="store_true",
                     help="accumulate the fc2 input's Hessian last (forward order)")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only the block loop's kernels against their rooflines (the "
+                         "'kernels' object), for counter runs of those kernels")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy a 1 GiB buffer 3 times: the known-size copy kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE for the traffic figure")
@@ -493,6 +496,11 @@ def main():
             y.copy_(x)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": x.numel() * 4, "copies": 3}))
+        return
+    if args.kernels_only:
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        print(json.dumps({"kernels": kernel_rooflines(dev)}))
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the path would shard "
