@@ -137,25 +137,29 @@ __device__ __forceinline__ float target_of(float w, float d2, int metric) {
 // ---------------------------------------------------------------------------
 // Every workgroup calls this after writing its partial results.  It returns
 // true in exactly one workgroup, the last to arrive, which then sees every
-// other workgroup's writes (release/acquire fences at device scope around
-// the arrival counter) and resets the counter for the next launch.
-#ifndef CRBQ_FENCE_ALL
-#define CRBQ_FENCE_ALL 0
-#endif
+// other workgroup's partials, and resets the counter for the next launch.
+// The partials travel through device-coherent accesses (pstore / pload:
+// agent-scope atomic stores and loads, written through to and read from
+// the point of coherence of all XCDs), so the arrival needs no cache-wide
+// release / acquire fences (an L2 write-back and invalidate per workgroup):
+// every thread waits for its own partial stores to be acknowledged before
+// the barrier that precedes the arrival on the counter, and the last
+// workgroup reads the partials only after its arrival returned.
+__device__ __forceinline__ void pstore(double* p, double v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ double pload(const double* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ bool last_block(uint32_t* cnt) {
   __shared__ bool last;
-#if CRBQ_FENCE_ALL
-  __threadfence();
-#endif
-  __syncthreads();   // every wave's partial stores have completed
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this thread's stores acknowledged
+  __syncthreads();
   if (threadIdx.x == 0) {
-    __threadfence();   // release (device scope) before arriving
     const uint32_t prev = atomicAdd(cnt, 1u);
     last = prev == gridDim.x - 1;
-    if (last) {
-      atomicExch(cnt, 0u);
-      __threadfence();   // acquire: drop stale cached partials
-    }
+    if (last) atomicExch(cnt, 0u);
   }
   __syncthreads();
   return last;
@@ -179,7 +183,7 @@ __device__ void reduce_partials(const double* part, int stride, int nwg, int nca
 #pragma unroll
     for (int j = 0; j < GMAX; ++j) {
       const int g = pp * G + j;
-      x[j] = (j < G && g < nwg) ? part[(size_t)g * stride + k] : 0.0;
+      x[j] = (j < G && g < nwg) ? pload(&part[(size_t)g * stride + k]) : 0.0;
     }
 #pragma unroll
     for (int j = 0; j < GMAX; ++j) v += x[j];
@@ -248,7 +252,7 @@ __global__ __launch_bounds__(CS_THREADS) void k_colscore(
     double v = 0.0;
 #pragma unroll
     for (int q = 0; q < CS_PH; ++q) v += part[q][col];
-    s.colpart[(size_t)blockIdx.x * NCMAX + col] = v;
+    pstore(&s.colpart[(size_t)blockIdx.x * NCMAX + col], v);
   }
   if (!last_block(&s.ctrl->cnt[CNT_CS])) return;
   reduce_partials<NCMAX, CS_PH, CS_MAXWG / CS_PH>(s.colpart, NCMAX, gridDim.x, NCMAX, red, sc);
@@ -500,7 +504,7 @@ __global__ __launch_bounds__(64 * NW) void k_phase_a(
       v += errs[w][tid];
       if (TWO) v += errs[w][tid + 32];
     }
-    s.parta[(size_t)blockIdx.x * UPMAX + tid] = v;
+    pstore(&s.parta[(size_t)blockIdx.x * UPMAX + tid], v);
   }
   if (!last_block(&s.ctrl->cnt[CNT_A])) return;
   reduce_partials<UPMAX, NW, (PX_MAXWG + NW - 1) / NW>(s.parta, UPMAX, gridDim.x, ncand, red, e);
@@ -1169,7 +1173,7 @@ __global__ __launch_bounds__(1024) void k_phase_a_pairs(
   if (tid < ncand) {
     double v = 0.0;
     for (int qq = 0; qq < PF_RB; ++qq) v += errs[qq * ncand + tid];
-    s.parta[(size_t)blockIdx.x * UPMAX + tid] = v;
+    pstore(&s.parta[(size_t)blockIdx.x * UPMAX + tid], v);
   }
   if (!last_block(&s.ctrl->cnt[CNT_A])) return;
   reduce_partials<UPMAX, 9, (PX_MAXWG + 8) / 9>(s.parta, UPMAX, gridDim.x, ncand, red, e);
@@ -1236,7 +1240,7 @@ __global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
     }
   }
   __syncthreads();
-  for (int k = tid; k < NQ; k += 64 * PC_WAVES) s.partc[(size_t)blockIdx.x * 96 + k] = acc[k];
+  for (int k = tid; k < NQ; k += 64 * PC_WAVES) pstore(&s.partc[(size_t)blockIdx.x * 96 + k], acc[k]);
   if (!last_block(&s.ctrl->cnt[CNT_C])) return;
   reduce_partials<96, 10, (PX_MAXWG + 9) / 10>(s.partc, 96, gridDim.x, NQ, red, e);
   if (tid < 64) {
@@ -1599,7 +1603,7 @@ __global__ __launch_bounds__(64 * PR_CW) void k_phase_a_rows(
       acc += t;
     }
   }
-  if (live && lane == 0) s.parta[(size_t)((int)blockIdx.x / ncg) * UPMAX + (i - 1)] = acc;
+  if (live && lane == 0) pstore(&s.parta[(size_t)((int)blockIdx.x / ncg) * UPMAX + (i - 1)], acc);
   if (!last_block(&s.ctrl->cnt[CNT_A])) return;
   reduce_partials<UPMAX, PR_MINW, (PX_MAXWG + PR_MINW - 1) / PR_MINW>(s.parta, UPMAX, nrg,
                                                                       ncand, red, e);
