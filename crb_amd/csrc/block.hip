@@ -1222,13 +1222,16 @@ __global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
       if (lane == 0) sr.n = n;
     }
     __syncthreads();
-    if (row < R) {
-      for (int k = lane; k < NQ; k += 64) {
+    // the workgroup's (row, candidate) pairs spread over all its lanes
+    for (int pq = tid; pq < PC_WAVES * NQ; pq += 64 * PC_WAVES) {
+      const int q = pq / NQ, k = pq - q * NQ;
+      if (r0 + q < R) {
+        const SortedRow& rq = rows[q];
         const float thr = pv[k];
         // M1 = {-thr < v < thr} = [a, b), M2 = [0, a) + [b, n)
-        const int a = ubound(sr.v, n, -thr);
-        const int b = max(lbound(sr.v, n, thr), a);
-        errs[wv][k] = group_err1(sr, a, b, 0, 0) + group_err1(sr, 0, a, b, n);
+        const int a = ubound(rq.v, n, -thr);
+        const int b = max(lbound(rq.v, n, thr), a);
+        errs[q][k] = group_err1(rq, a, b, 0, 0) + group_err1(rq, 0, a, b, n);
       }
     }
     __syncthreads();
