@@ -1533,9 +1533,9 @@ __device__ __forceinline__ double row_sum(const float* x, int c0, int c1) {
 
 // order-2 residual binarization error of {ranks [0, i)} + {ranks [i, nc)}
 // of one row x in rank order (binary.py:17-41 via utils/autosearch.py:44-55)
-__device__ __forceinline__ double row_cand_err(const float* x, int i, int nc) {
+__device__ __forceinline__ double row_cand_err(const float* x, int i, int nc, double ps,
+                                               double pc) {
   const float nS = (float)i, nC = (float)(nc - i);
-  const double ps = row_sum(x, 0, i), pc = row_sum(x, i, nc);
   const float m1S = (float)ps / nS;
   const float m1C = nC > 0.f ? (float)pc / nC : 0.f;
   RowAbs aS = {0.0, 0, 0}, aC = {0.0, 0, 0};
@@ -1568,6 +1568,7 @@ __global__ __launch_bounds__(64 * PR_CW) void k_phase_a_rows(
     int cw, SearchWs s, crbq_block_trace* tr) {
   constexpr int LMAX = (64 + PR_MINW - 1) / PR_MINW;   // rows loaded per wavefront
   __shared__ __attribute__((aligned(16))) float xs[64][PR_XS];
+  __shared__ double cs[NCMAX / 8][64];           // fp64 sums of 8-rank chunks, per row
   __shared__ double red[PR_MINW][UPMAX];
   __shared__ double e[UPMAX];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
@@ -1600,8 +1601,20 @@ __global__ __launch_bounds__(64 * PR_CW) void k_phase_a_rows(
       }
     }
     __syncthreads();
+    // chunk sums once per row group, shared by the candidates' group sums
+    for (int j = wv; j < NCMAX / 8; j += nw) cs[j][lane] = row_sum(xs[lane], 8 * j, min(nc, 8 * j + 8));
+    __syncthreads();
     if (live) {
-      const double err = row_cand_err(xs[lane], i, nc);
+      // group sums: whole chunks below i, then the ranks of i's chunk
+      double ps = 0.0, tot = 0.0;
+      const int ji = i >> 3;
+      for (int j = 0; j < NCMAX / 8; ++j) {
+        const double v = cs[j][lane];
+        if (j < ji) ps += v;
+        tot += v;
+      }
+      ps += row_sum(xs[lane], 8 * ji, i);
+      const double err = row_cand_err(xs[lane], i, nc, ps, tot - ps);
       const double t = lane63_f64(wave_scan_f64(r0 + lane < R ? err : 0.0));
       acc += t;
     }
