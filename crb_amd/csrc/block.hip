@@ -6,19 +6,21 @@
 // -> utils/mask.py:7-18), all on the device with no host round trip:
 //   k_colscore   column scores sum_r |T| (fp64 per-workgroup partials);
 //                the last workgroup ranks the columns (torch.topk order)
-//   k_phase_a    one lane per (row, salient candidate i) -- k_phase_a_pairs
-//                for 33-63 candidates, two rows per wavefront up to 32, one
-//                row per wavefront otherwise: order-2 residual binarization
-//                error of {top i cols} + complement (prefix sums + two
-//                passes, closed-form error); the last workgroup takes
+//   k_phase_a_rows  lanes = 64 rows, wavefront = salient candidate i:
+//                order-2 residual binarization error of {top i cols} +
+//                complement (group sums from fp64 chunk sums, two passes,
+//                closed-form error); the last workgroup takes
 //                i* = first strict minimum
-//   k_qpass/k_qscan (x3)
+//   k_qpass1, k_qscan1, k_qlist, k_qselect
 //                exact np.quantile of |T * ~M3| at the 81 float32
-//                percentiles: 3-level MSD radix select (12/10/10 bits of the
-//                non-negative float's bit pattern) of the 162 order
-//                statistics, then numpy's float32 index/lerp arithmetic
-//   k_phase_c    one lane per (row, split candidate k): order-1 errors of the
-//                two bell groups
+//                percentiles: level-1 histogram of the top 12 bits of the
+//                non-negative float's bit pattern, the bins of the 162
+//                order statistics, the elements of those bins gathered into
+//                per-bin lists, one selection workgroup per statistic; then
+//                numpy's float32 index/lerp arithmetic
+//   k_phase_c    per row a sorted copy with fp64 prefix sums; the
+//                workgroup's (row, split candidate k) pairs over its lanes:
+//                order-1 errors of the two bell groups in closed form;
 //                the last workgroup takes k* = first strict minimum,
 //                split = p[k*]
 //   k_quantize   one wavefront per row: masks, binarization per group,
@@ -286,74 +288,9 @@ __global__ __launch_bounds__(CS_THREADS) void k_colscore(
 // the last workgroup picks i* = first strict minimum (default
 // max(1, up_lim // 3), :43)
 // ---------------------------------------------------------------------------
-// One wavefront per row, one lane per candidate i = lane + 1.  The row's
-// targets are placed in LDS in column-rank order, so the salient group of
-// candidate i is ranks [0, i) and its complement ranks [i, nc).  Order-2
-// residual binarization of a group with mean m1, scale a1, residual
-// r = x - (a1*sign(x - m1) + m1), residual mean m2 and scale a2 has error
-//   sum (e - a2*sign(e))^2 = E2 - 2*a2*E1 + a2^2 * nz,
-// e = r - m2, E1 = sum |e|, E2 = sum e^2, nz = #(e != 0).  Group sums of x
-// come from a wave prefix scan; sum |x - m1| and the sign counts (which give
-// sum r in closed form, s1 taking the three fp32 values m1 +- a1 and m1)
-// from one pass; E1, E2, nz from a second pass in which s1, r and e are
-// formed with the reference's fp32 operations, so every sign decision is
-// the reference's.  Sums run in fp32 over chunks of 8 elements and are
-// accumulated in fp64; counts are integers.  Ranks below ncand are the
-// only ones a candidate's salient group can hold ("mixed" ranks, where each
-// element is routed to its group by a select); the rest always belong to
-// the complement.
-#ifndef CRBQ_PA_WAVES
-#define CRBQ_PA_WAVES 16
-#endif
-constexpr int PA_WAVES = CRBQ_PA_WAVES;
-constexpr int PA2_WAVES = 8;    // wavefronts per workgroup of the two-rows-per-wavefront form
-
-struct GroupA {         // per-lane accumulators of one group
-  double ad, e1, e2;
-  int npos, nneg, nz;
-};
-
 struct ParA {           // a group's fp32 parameters for the residual pass
   float m1, hi, lo, m2, a1;   // hi = fl(a1 + m1), lo = fl(-a1 + m1)
 };
-
-// sum |x - m1| and the sign counts of x - m1 over ranks [c0, c1)
-template <bool MIXED>
-__device__ __forceinline__ void abs_elem(float x, bool inS, float m1S, float m1C, float& pS,
-                                         float& pC, GroupA& S, GroupA& Cg) {
-  const float d = x - (inS ? m1S : m1C);
-  const float ad = fabsf(d);
-  const int pos = d > 0.f ? 1 : 0, neg = d < 0.f ? 1 : 0;
-  if (MIXED) {
-    pS += inS ? ad : 0.f;
-    S.npos += inS ? pos : 0;
-    S.nneg += inS ? neg : 0;
-    pC += inS ? 0.f : ad;
-    Cg.npos += inS ? 0 : pos;
-    Cg.nneg += inS ? 0 : neg;
-  } else {
-    pC += ad;
-    Cg.npos += pos;
-    Cg.nneg += neg;
-  }
-}
-
-template <bool MIXED>
-__device__ __forceinline__ void pass_abs(const float* xs, int c0, int c1, int i, float m1S,
-                                         float m1C, GroupA& S, GroupA& Cg) {
-  int c = c0;
-  for (; c + 8 <= c1; c += 8) {
-    float pS = 0.f, pC = 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) abs_elem<MIXED>(xs[c + u], MIXED && c + u < i, m1S, m1C, pS, pC, S, Cg);
-    if (MIXED) S.ad += (double)pS;
-    Cg.ad += (double)pC;
-  }
-  float pS = 0.f, pC = 0.f;
-  for (; c < c1; ++c) abs_elem<MIXED>(xs[c], MIXED && c < i, m1S, m1C, pS, pC, S, Cg);
-  if (MIXED) S.ad += (double)pS;
-  Cg.ad += (double)pC;
-}
 
 // e = (x - s1) - m2 with s1 = sign(x - m1)*a1 + m1 in fp32 (binary.py:26,
 // 32-34): sign*a1 is exact, so the fma rounds once, like the reference's
@@ -367,158 +304,7 @@ __device__ __forceinline__ float resid(float x, const ParA& g) {
   return r - g.m2;
 }
 
-template <bool MIXED>
-__device__ __forceinline__ void res_elem(float x, bool inS, const ParA& PS, const ParA& PC,
-                                         float& p1S, float& p2S, float& p1C, float& p2C,
-                                         GroupA& S, GroupA& Cg) {
-  ParA g = PC;
-  if (MIXED) {
-    g.m1 = inS ? PS.m1 : PC.m1;
-    g.hi = inS ? PS.hi : PC.hi;
-    g.lo = inS ? PS.lo : PC.lo;
-    g.m2 = inS ? PS.m2 : PC.m2;
-    g.a1 = inS ? PS.a1 : PC.a1;
-  }
-  const float e = resid(x, g);
-  const float ae = fabsf(e);
-  const float e2 = e * e;
-  const int nz = e != 0.f ? 1 : 0;
-  if (MIXED) {
-    p1S += inS ? ae : 0.f;
-    p2S += inS ? e2 : 0.f;
-    S.nz += inS ? nz : 0;
-    p1C += inS ? 0.f : ae;
-    p2C += inS ? 0.f : e2;
-    Cg.nz += inS ? 0 : nz;
-  } else {
-    p1C += ae;
-    p2C += e2;
-    Cg.nz += nz;
-  }
-}
-
-template <bool MIXED>
-__device__ __forceinline__ void pass_res(const float* xs, int c0, int c1, int i, const ParA& PS,
-                                         const ParA& PC, GroupA& S, GroupA& Cg) {
-  int c = c0;
-  for (; c + 8 <= c1; c += 8) {
-    float p1S = 0.f, p2S = 0.f, p1C = 0.f, p2C = 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-      res_elem<MIXED>(xs[c + u], MIXED && c + u < i, PS, PC, p1S, p2S, p1C, p2C, S, Cg);
-    if (MIXED) { S.e1 += (double)p1S; S.e2 += (double)p2S; }
-    Cg.e1 += (double)p1C;
-    Cg.e2 += (double)p2C;
-  }
-  float p1S = 0.f, p2S = 0.f, p1C = 0.f, p2C = 0.f;
-  for (; c < c1; ++c) res_elem<MIXED>(xs[c], MIXED && c < i, PS, PC, p1S, p2S, p1C, p2C, S, Cg);
-  if (MIXED) { S.e1 += (double)p1S; S.e2 += (double)p2S; }
-  Cg.e1 += (double)p1C;
-  Cg.e2 += (double)p2C;
-}
-
-// One wavefront per row (TWO = false: lane i-1 evaluates candidate i, up to
-// 64 candidates) or per two rows (TWO = true, at most 32 candidates: lanes
-// 0-31 and 32-63 each hold one row's candidates, so no lane idles on the
-// reference's default up_lim = 30).  NW wavefronts per workgroup.
-template <int NW, bool TWO>
-__global__ __launch_bounds__(64 * NW) void k_phase_a(
-    const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, int ncand, int up_lim, SearchWs s,
-    crbq_block_trace* tr) {
-  constexpr int RPW = TWO ? 2 : 1;               // rows per wavefront
-  constexpr int XS = NCMAX + 4;                  // row stride: 16-byte aligned, rows 4 banks apart
-  constexpr int GL = 64 / RPW;                   // lanes per row group
-  __shared__ __attribute__((aligned(16))) float xs[NW * RPW][XS];
-  __shared__ double errs[NW][64];
-  __shared__ double red[NW][UPMAX];
-  __shared__ double e[UPMAX];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int h = TWO ? lane >> 5 : 0, gl = lane & (GL - 1);
-  const int c0 = lane, c1 = lane + 64;
-  const int rk0 = c0 < nc ? s.rank[c0] : -1, rk1 = c1 < nc ? s.rank[c1] : -1;
-  float d20 = 1.f, d21 = 1.f;
-  if (c0 < nc) { const float dg = U[(int64_t)c0 * ldu + c0]; d20 = dg * dg; }
-  if (c1 < nc) { const float dg = U[(int64_t)c1 * ldu + c1]; d21 = dg * dg; }
-  const int i = gl + 1;                          // candidate (salient columns)
-  const float nS = (float)i, nC = (float)(nc - i);
-  const int mix_end = min(nc, ncand);            // ranks >= ncand are never salient
-  double acc = 0.0;
-  for (int r0 = blockIdx.x * NW * RPW; r0 < R; r0 += gridDim.x * NW * RPW) {
-    __syncthreads();                             // previous rows' readers are done
-#pragma unroll
-    for (int q = 0; q < RPW; ++q) {
-      const int rq = r0 + wv * RPW + q;
-      float* xq = xs[wv * RPW + q];
-      if (rq < R) {
-        if (rk0 >= 0) xq[rk0] = target_of(W[(int64_t)rq * ldw + c0], d20, metric);
-        if (rk1 >= 0) xq[rk1] = target_of(W[(int64_t)rq * ldw + c1], d21, metric);
-      }
-    }
-    __syncthreads();
-    const int row = r0 + wv * RPW + h;
-    const float* x = xs[wv * RPW + h];
-    if (row < R) {
-      // prefix sums in rank order: candidate i's salient group is ranks [0, i)
-      double ps = gl < nc ? (double)x[gl] : 0.0;
-      double rest = 0.0;
-#pragma unroll
-      for (int k = 1; k < 128 / GL; ++k) rest += gl + k * GL < nc ? (double)x[gl + k * GL] : 0.0;
-      const double tot = group_sum<GL>(ps + rest);
-#pragma unroll
-      for (int o = 1; o < GL; o <<= 1) {
-        const double t = __shfl_up(ps, o, CRBQ_WAVE);
-        if (gl >= o) ps += t;
-      }
-      const float m1S = (float)ps / nS;
-      const float m1C = nC > 0.f ? (float)(tot - ps) / nC : 0.f;
-      GroupA S = {0.0, 0.0, 0.0, 0, 0, 0}, Cg = {0.0, 0.0, 0.0, 0, 0, 0};
-      pass_abs<true>(x, 0, mix_end, i, m1S, m1C, S, Cg);
-      pass_abs<false>(x, mix_end, nc, i, m1S, m1C, S, Cg);
-      const float a1S = (float)S.ad / nS;
-      const float a1C = nC > 0.f ? (float)Cg.ad / nC : 0.f;
-      // sum r = sum x - sum s1, s1 in {fl(a1 + m1), fl(-a1 + m1), m1}
-      float hiS = a1S + m1S, loS = -a1S + m1S, hiC = a1C + m1C, loC = -a1C + m1C;
-      const double s1S = S.npos * (double)hiS + S.nneg * (double)loS +
-                         ((double)nS - S.npos - S.nneg) * (double)m1S;
-      const double s1C = Cg.npos * (double)hiC + Cg.nneg * (double)loC +
-                         ((double)nC - Cg.npos - Cg.nneg) * (double)m1C;
-      const float m2S = (float)(ps - s1S) / nS;
-      const float m2C = nC > 0.f ? (float)((tot - ps) - s1C) / nC : 0.f;
-      const ParA PS = {m1S, hiS, loS, m2S, a1S}, PC = {m1C, hiC, loC, m2C, a1C};
-      pass_res<true>(x, 0, mix_end, i, PS, PC, S, Cg);
-      pass_res<false>(x, mix_end, nc, i, PS, PC, S, Cg);
-      const double a2S = (double)((float)S.e1 / nS);
-      const double a2C = nC > 0.f ? (double)((float)Cg.e1 / nC) : 0.0;
-      const double eS = S.e2 - 2.0 * a2S * S.e1 + a2S * a2S * (double)S.nz;
-      const double eC = Cg.e2 - 2.0 * a2C * Cg.e1 + a2C * a2C * (double)Cg.nz;
-      acc += eS + eC;
-    }
-  }
-  errs[wv][lane] = acc;
-  __syncthreads();
-  if (tid < ncand) {
-    double v = 0.0;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      v += errs[w][tid];
-      if (TWO) v += errs[w][tid + 32];
-    }
-    pstore(&s.parta[(size_t)blockIdx.x * UPMAX + tid], v);
-  }
-  if (!last_block(&s.ctrl->cnt[CNT_A])) return;
-  reduce_partials<UPMAX, NW, (PX_MAXWG + NW - 1) / NW>(s.parta, UPMAX, gridDim.x, ncand, red, e);
-  if (tid < 64) {
-    const int am = wave_argmin(e, ncand);
-    const int istar = am < 0 ? max(1, up_lim / 3) : am + 1;         // :43
-    if (tid == 0) {
-      s.ctrl->istar = istar;
-      if (tr) tr->i_star = istar;
-    }
-  }
-  if (tr && tid < UPMAX) tr->errs_a[tid] = (tid >= 1 && tid <= ncand) ? e[tid - 1] : 0.0;
-}
-
+// The kernel (k_phase_a_rows) follows the sorting helpers below.
 
 // ---------------------------------------------------------------------------
 // exact float32 np.quantile of S = |T * ~M3| (utils/autosearch.py:62-68)
@@ -1028,166 +814,10 @@ __device__ __forceinline__ void wave_prefix(SortedRow& r, float x0, float x1, in
   r.v[lane + 64] = x1;
 }
 
-// The pure part of a row (ranks >= ncand, never salient: always in the
-// complement group) sorted by value with fp64 prefix sums, so each
-// candidate's two passes over it are closed forms with binary searches
-// instead of loops.  Sign decisions use the fp32 expressions of the
-// elementwise passes as search predicates (each is monotone in x); the sums
-// are fp64 closed forms of the same quantities.
-template <typename P>
-__device__ __forceinline__ int first_true(const float* v, int lo, int hi, P pred) {
-  while (lo < hi) {
-    const int m = (lo + hi) >> 1;
-    if (pred(v[m])) hi = m; else lo = m + 1;
-  }
-  return lo;
-}
-
-// sum |x - m1| and the sign counts over the sorted pure part (pass_abs)
-__device__ __forceinline__ void pure_abs(const SortedRow& r, int np, float m1, GroupA& C,
-                                         int& lb, int& ub) {
-  lb = lbound(r.v, np, m1);
-  ub = ubound(r.v, np, m1);
-  const double m = (double)m1;
-  C.ad += ((r.S[np] - r.S[ub]) - (double)(np - ub) * m) + ((double)lb * m - r.S[lb]);
-  C.npos += np - ub;
-  C.nneg += lb;
-}
-
-// |e|, e^2 and e != 0 summed over the sorted range [l, h) split at the e = 0
-// run [z, t): e < 0 below z, e > 0 from t, with e = x - c
-__device__ __forceinline__ void pure_range(const SortedRow& r, int l, int z, int t, int h,
-                                           double c, GroupA& C) {
-  const Stat lo = rstat(r, l, z), hi = rstat(r, t, h);
-  C.e1 += (lo.n * c - lo.s) + (hi.s - hi.n * c);
-  C.e2 += sqdev(lo, c) + sqdev(hi, c);
-  C.nz += (z - l) + (h - t);
-}
-
-// pass_res over the sorted pure part: e = fl(fl(x - s1) - m2), s1 = hi above
-// m1, lo below, m1 at m1 (where e = -m2)
-__device__ __forceinline__ void pure_res(const SortedRow& r, int np, int lb, int ub,
-                                         const ParA& g, GroupA& C) {
-  const int zA = first_true(r.v, ub, np, [&](float x) { return x - g.hi >= g.m2; });
-  const int sA = first_true(r.v, zA, np, [&](float x) { return x - g.hi > g.m2; });
-  pure_range(r, ub, zA, sA, np, (double)g.hi + (double)g.m2, C);
-  const int zB = first_true(r.v, 0, lb, [&](float x) { return x - g.lo >= g.m2; });
-  const int sB = first_true(r.v, zB, lb, [&](float x) { return x - g.lo > g.m2; });
-  pure_range(r, 0, zB, sB, lb, (double)g.lo + (double)g.m2, C);
-  const int nm = ub - lb;
-  C.e1 += (double)nm * fabs((double)g.m2);
-  C.e2 += (double)nm * ((double)g.m2 * (double)g.m2);
-  C.nz += g.m2 != 0.f ? nm : 0;
-}
-
-// Salient-count candidates as (row, candidate) pairs when 32 < ncand <= 64:
-// PF_RB rows per workgroup iteration, thread f evaluates row f / ncand with
-// candidate f % ncand + 1, so only the tail of the last wavefront idles
-// (the reference's up_lim = 50: 784 pairs on 13 wavefronts instead of 16
-// wavefronts with 15 idle lanes each).  Same per-pair arithmetic as
-// k_phase_a, with the rank-order prefix sums of each row staged in LDS.
-constexpr int PF_RB = 16;
-__global__ __launch_bounds__(1024) void k_phase_a_pairs(
-    const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, int ncand, int up_lim, SearchWs s,
-    crbq_block_trace* tr) {
-  constexpr int XS = NCMAX + 4;
-  __shared__ __attribute__((aligned(16))) float xs[PF_RB][XS];
-  __shared__ double pre[PF_RB][NCMAX + 1];   // pre[q][k]: sum of ranks [0, k) of row q
-  __shared__ SortedRow pure[PF_RB];          // ranks >= mix_end, sorted by value
-  __shared__ double errs[1024];
-  __shared__ double red[9][UPMAX];
-  __shared__ double e[UPMAX];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
-  const bool act = tid < PF_RB * ncand;
-  const int q = act ? tid / ncand : 0;
-  const int i = act ? tid % ncand + 1 : 1;   // candidate (salient columns)
-  const int c0 = lane, c1 = lane + 64;
-  const int rk0 = c0 < nc ? s.rank[c0] : -1, rk1 = c1 < nc ? s.rank[c1] : -1;
-  float d20 = 1.f, d21 = 1.f;
-  if (c0 < nc) { const float dg = U[(int64_t)c0 * ldu + c0]; d20 = dg * dg; }
-  if (c1 < nc) { const float dg = U[(int64_t)c1 * ldu + c1]; d21 = dg * dg; }
-  const float nS = (float)i, nC = (float)(nc - i);
-  const int mix_end = min(nc, ncand);
-  const int np = nc - mix_end;                 // pure part: ranks [mix_end, nc)
-  double acc = 0.0;
-  for (int r0 = blockIdx.x * PF_RB; r0 < R; r0 += gridDim.x * PF_RB) {
-    __syncthreads();                             // previous rows' readers are done
-    for (int qq = wv; qq < PF_RB; qq += nw) {    // rows in rank order, one wavefront each
-      const int rq = r0 + qq;
-      if (rq < R) {
-        if (rk0 >= 0) xs[qq][rk0] = target_of(W[(int64_t)rq * ldw + c0], d20, metric);
-        if (rk1 >= 0) xs[qq][rk1] = target_of(W[(int64_t)rq * ldw + c1], d21, metric);
-      }
-    }
-    __syncthreads();
-    for (int qq = wv; qq < PF_RB; qq += nw) {    // exclusive prefix sums in rank order
-      if (r0 + qq < R) {
-        const double y0 = lane < nc ? (double)xs[qq][lane] : 0.0;
-        const double y1 = lane + 64 < nc ? (double)xs[qq][lane + 64] : 0.0;
-        const double p0 = wave_scan_f64(y0);
-        const double p1 = wave_scan_f64(y1) + lane63_f64(p0);
-        pre[qq][lane + 1] = p0;
-        pre[qq][lane + 65] = p1;
-        if (lane == 0) pre[qq][0] = 0.0;
-        if (np > 0) {
-          float z0 = mix_end + lane < nc ? xs[qq][mix_end + lane] : INFINITY;
-          float z1 = mix_end + 64 + lane < nc ? xs[qq][mix_end + 64 + lane] : INFINITY;
-          wave_sort128(z0, z1);
-          wave_prefix(pure[qq], z0, z1, np);
-        }
-      }
-    }
-    __syncthreads();
-    const int row = r0 + q;
-    if (act && row < R) {
-      const float* x = xs[q];
-      const double ps = pre[q][i], tot = pre[q][nc];
-      const float m1S = (float)ps / nS;
-      const float m1C = nC > 0.f ? (float)(tot - ps) / nC : 0.f;
-      GroupA S = {0.0, 0.0, 0.0, 0, 0, 0}, Cg = {0.0, 0.0, 0.0, 0, 0, 0};
-      pass_abs<true>(x, 0, mix_end, i, m1S, m1C, S, Cg);
-      int lb = 0, ub = 0;
-      if (np > 0) pure_abs(pure[q], np, m1C, Cg, lb, ub);
-      const float a1S = (float)S.ad / nS;
-      const float a1C = nC > 0.f ? (float)Cg.ad / nC : 0.f;
-      float hiS = a1S + m1S, loS = -a1S + m1S, hiC = a1C + m1C, loC = -a1C + m1C;
-      const double s1S = S.npos * (double)hiS + S.nneg * (double)loS +
-                         ((double)nS - S.npos - S.nneg) * (double)m1S;
-      const double s1C = Cg.npos * (double)hiC + Cg.nneg * (double)loC +
-                         ((double)nC - Cg.npos - Cg.nneg) * (double)m1C;
-      const float m2S = (float)(ps - s1S) / nS;
-      const float m2C = nC > 0.f ? (float)((tot - ps) - s1C) / nC : 0.f;
-      const ParA PS = {m1S, hiS, loS, m2S, a1S}, PC = {m1C, hiC, loC, m2C, a1C};
-      pass_res<true>(x, 0, mix_end, i, PS, PC, S, Cg);
-      if (np > 0) pure_res(pure[q], np, lb, ub, PC, Cg);
-      const double a2S = (double)((float)S.e1 / nS);
-      const double a2C = nC > 0.f ? (double)((float)Cg.e1 / nC) : 0.0;
-      const double eS = S.e2 - 2.0 * a2S * S.e1 + a2S * a2S * (double)S.nz;
-      const double eC = Cg.e2 - 2.0 * a2C * Cg.e1 + a2C * a2C * (double)Cg.nz;
-      acc += eS + eC;
-    }
-  }
-  errs[tid] = acc;
-  __syncthreads();
-  if (tid < ncand) {
-    double v = 0.0;
-    for (int qq = 0; qq < PF_RB; ++qq) v += errs[qq * ncand + tid];
-    pstore(&s.parta[(size_t)blockIdx.x * UPMAX + tid], v);
-  }
-  if (!last_block(&s.ctrl->cnt[CNT_A])) return;
-  reduce_partials<UPMAX, 9, (PX_MAXWG + 8) / 9>(s.parta, UPMAX, gridDim.x, ncand, red, e);
-  if (tid < 64) {
-    const int am = wave_argmin(e, ncand);
-    const int istar = am < 0 ? max(1, up_lim / 3) : am + 1;         // :43
-    if (tid == 0) {
-      s.ctrl->istar = istar;
-      if (tr) tr->i_star = istar;
-    }
-  }
-  if (tr && tid < UPMAX) tr->errs_a[tid] = (tid >= 1 && tid <= ncand) ? e[tid - 1] : 0.0;
-}
-
+// Phase C: per row (one wavefront) the non-salient targets sorted with
+// fp64 prefix sums of v and v^2; then the workgroup's (row, candidate k)
+// pairs over all its lanes, each two binary searches per group and range
+// sums (group_err1); the last workgroup takes k* = first strict minimum.
 __global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
     const float* __restrict__ W, int64_t ldw, int R, int nc,
     const float* __restrict__ U, int64_t ldu, int metric, SearchWs s, crbq_block_trace* tr) {
@@ -1637,35 +1267,20 @@ __global__ __launch_bounds__(64 * PR_CW) void k_phase_a_rows(
 // ---------------------------------------------------------------------------
 // host drivers
 // ---------------------------------------------------------------------------
-#ifndef CRBQ_PA_ROWS
-#define CRBQ_PA_ROWS 1
-#endif
 static int search_block(const float* W, int64_t ldw, int R, int nc, const float* U,
                         int64_t ldu, int metric, int up_lim, SearchWs& s,
                         crbq_block_trace* tr, hipStream_t st) {
   const int ncand = up_lim - 1;
   const int nwg_cs = (int)std::min<int64_t>(cdiv(R, CS_PH), CS_MAXWG);
   const int nwg_q = (int)cdiv(R, Q_RPW);
-  const bool two = ncand <= 32;
-  const bool pairs = !two && ncand <= 64;
-  const int nwg_a = (int)std::min<int64_t>(
-      cdiv(R, two ? 2 * PA2_WAVES : (pairs ? PF_RB : PA_WAVES)), PX_MAXWG);
   const int nwg_c = (int)std::min<int64_t>(cdiv(R, PC_WAVES), PX_MAXWG);
+  // phase A: ceil(ncand / PR_CW) workgroups of up to PR_CW candidates per
+  // 64-row group (at least PR_MINW wavefronts: the reduction's 576 threads)
+  const int ncg = (int)cdiv(ncand, PR_CW), cw = (int)cdiv(ncand, ncg);
+  const int nrg = (int)std::min<int64_t>(cdiv(R, 64), PX_MAXWG);
   k_colscore<<<nwg_cs, CS_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  if (CRBQ_PA_ROWS) {
-    const int ncg = (int)cdiv(ncand, PR_CW), cw = (int)cdiv(ncand, ncg);
-    const int nrg = (int)std::min<int64_t>(cdiv(R, 64), PX_MAXWG);
-    k_phase_a_rows<<<nrg * ncg, 64 * std::max(cw, PR_MINW), 0, st>>>(
-        W, ldw, R, nc, U, ldu, metric, ncand, up_lim, ncg, cw, s, tr);
-  } else if (two)
-    k_phase_a<PA2_WAVES, true><<<nwg_a, 64 * PA2_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric,
-                                                                 ncand, up_lim, s, tr);
-  else if (pairs)   // wavefronts for PF_RB * ncand pairs (>= 9: reduce_partials uses 576)
-    k_phase_a_pairs<<<nwg_a, 64 * (int)cdiv(PF_RB * ncand, 64), 0, st>>>(
-        W, ldw, R, nc, U, ldu, metric, ncand, up_lim, s, tr);
-  else
-    k_phase_a<PA_WAVES, false><<<nwg_a, 64 * PA_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric,
-                                                                ncand, up_lim, s, tr);
+  k_phase_a_rows<<<nrg * ncg, 64 * std::max(cw, PR_MINW), 0, st>>>(
+      W, ldw, R, nc, U, ldu, metric, ncand, up_lim, ncg, cw, s, tr);
   k_qpass1<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_qscan1<<<1, 256, 0, st>>>((int64_t)R * nc, s);
   k_qlist<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
