@@ -482,6 +482,8 @@ def main():
                     help="layers of the OPT-6.7B-shaped stack run (0: skip)")
     ap.add_argument("--fc2-last", action="store_true",
                     help="accumulate the fc2 input's Hessian last (forward order)")
+    ap.add_argument("--no-kernels", action="store_true",
+                    help="skip the block loop's isolated kernel measurements")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the block loop's kernels against their rooflines (the "
                          "'kernels' object), for counter runs of those kernels")
@@ -574,7 +576,8 @@ def main():
         # and the engine clock it ran at (quoted peaks assume 2.4 GHz)
         out["roofline"]["mfma_busy_per_simd"] = pv["syrk_fc2_mfma_busy_per_simd"]
         out["roofline"]["clock_ghz_under_load"] = pv.get("syrk_fc2_clock_ghz")
-    out["kernels"] = kernel_rooflines(dev)
+    if not args.no_kernels:
+        out["kernels"] = kernel_rooflines(dev)
     print(f"[bench] kernels: {out['kernels']}", file=sys.stderr, flush=True)
     if args.stack_layers > 0:
         del X
