@@ -6,6 +6,10 @@
 // lane adds its EPL elements in order, then the lanes are combined pairwise
 // (DPP / permlane tree, every lane of the group ending with the same bits).
 // The order differs from torch's, so sums agree to fp32 rounding.
+// A product a * B with B = sign(.) in {-1, 0, +1} is exact, so the
+// reference's fl(x - fl(a * B)) and fl(x + fl(a * B)) are one rounding of
+// an exact value: fma(-a, B, x) and fma(a, B, x) give the same bits in one
+// instruction.
 #pragma once
 #include "common.h"
 
@@ -54,6 +58,16 @@ __device__ __forceinline__ float rsum_z(const float (&v)[EPL]) {
   return group_sum_f<LPR>(s);
 }
 
+// sum of a * b where every product is exact (one factor a sign in
+// {-1, 0, +1}): fma(a, b, s) is the reference's fl(s + fl(a * b))
+template <int EPL, int LPR = 64>
+__device__ __forceinline__ float rdot_sign(const float (&a)[EPL], const float (&b)[EPL]) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) s = __builtin_fmaf(a[e], b[e], s);
+  return group_sum_f<LPR>(s);
+}
+
 template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rcount(const bool (&m)[EPL]) {
   float c = 0.f;
@@ -80,8 +94,7 @@ __device__ void hor_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
     const float alpha = cnt > 0.f ? div_cnt(rsum_abs<EPL, LPR>(c, m), cnt, rc) : 0.f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-      float b = tsign(c[e]) * alpha;
-      b = b + mu;
+      const float b = __builtin_fmaf(tsign(c[e]), alpha, mu);
       acc[e] = m[e] ? acc[e] + b : 0.f;
     }
   }
@@ -128,67 +141,55 @@ __device__ void crb_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
   if (order == 1) {                                                 // :1570-1576
     const float a1 = div_cnt(sabs, ds, rds);
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) out[e] = m[e] ? mean + a1 * B1[e] : 0.f;
+    for (int e = 0; e < EPL; ++e) out[e] = m[e] ? __builtin_fmaf(a1, B1[e], mean) : 0.f;
     if (scales) { scales[0] = mean; scales[1] = 0.f; scales[2] = a1; scales[3] = 0.f; }
     return;
   }
   const float a10 = div_cnt(sabs, ds, rds);                          // step 2
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) t[e] = cen[e] - a10 * B1[e];        // step 3
+  for (int e = 0; e < EPL; ++e) t[e] = __builtin_fmaf(-a10, B1[e], cen[e]);   // step 3
   const float rmean = div_cnt(rsum_z<EPL, LPR>(t), ds, rds);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) B2[e] = tsign_m(m[e], t[e] - rmean);
   float c12, c1w, c2w, a1, a2;
   {                                                                 // step 4
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
-    c12 = rsum_z<EPL, LPR>(t);
+    c12 = rdot_sign<EPL, LPR>(B1, B2);
     // cen * B1 = |cen| elementwise (B1 = sign(cen) here): the same sum as a10's
     c1w = sabs;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B2[e];
-    c2w = rsum_z<EPL, LPR>(t);
+    c2w = rdot_sign<EPL, LPR>(cen, B2);
   }
   crb_solve(d, c12, c1w, c2w, k, a1, a2);
   if (!k.skip) {
     for (int it = 0; it < k.iters; ++it) {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) t[e] = cen[e] - a1 * B1[e];     // step 5
+      for (int e = 0; e < EPL; ++e) t[e] = __builtin_fmaf(-a1, B1[e], cen[e]);  // step 5
       const float t5m = div_cnt(rsum_z<EPL, LPR>(t), ds, rds);
 #pragma unroll
       for (int e = 0; e < EPL; ++e) B2[e] = tsign_m(m[e], t[e] - t5m);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B2[e];
-      c2w = rsum_z<EPL, LPR>(t);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
-      c12 = rsum_z<EPL, LPR>(t);
+      c2w = rdot_sign<EPL, LPR>(cen, B2);
+      c12 = rdot_sign<EPL, LPR>(B1, B2);
       crb_solve(d, c12, c1w, c2w, k, a1, a2);
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) t[e] = cen[e] - a2 * B2[e];     // step 6
+      for (int e = 0; e < EPL; ++e) t[e] = __builtin_fmaf(-a2, B2[e], cen[e]);  // step 6
       const float t6m = div_cnt(rsum_z<EPL, LPR>(t), ds, rds);
 #pragma unroll
       for (int e = 0; e < EPL; ++e) B1[e] = tsign_m(m[e], t[e] - t6m);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) t[e] = cen[e] * B1[e];
-      c1w = rsum_z<EPL, LPR>(t);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
-      c12 = rsum_z<EPL, LPR>(t);
+      c1w = rdot_sign<EPL, LPR>(cen, B1);
+      c12 = rdot_sign<EPL, LPR>(B1, B2);
       crb_solve(d, c12, c1w, c2w, k, a1, a2);
     }
   }
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {                                   // step 7
-    const float ap = a1 * B1[e] + a2 * B2[e];
+    const float ap = __builtin_fmaf(a1, B1[e], a2 * B2[e]);
     t[e] = cen[e] - ap;
   }
   const float muc = div_cnt(rsum_z<EPL, LPR>(t), ds, rds);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     float v = mean + muc;
-    v = v + a1 * B1[e];
-    v = v + a2 * B2[e];
+    v = __builtin_fmaf(a1, B1[e], v);
+    v = __builtin_fmaf(a2, B2[e], v);
     out[e] = m[e] ? v : 0.f;
   }
   if (scales) { scales[0] = mean; scales[1] = muc; scales[2] = a1; scales[3] = a2; }
@@ -210,7 +211,7 @@ __device__ void crbog_row(const float (&x)[EPL], const bool (&m)[EPL], int order
   for (int e = 0; e < EPL; ++e) { cen[e] = x[e] - mean; B1[e] = tsign(cen[e]); }
   float a1 = div_cnt(rsum_abs<EPL, LPR>(cen, m), n, rn);
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) { t[e] = cen[e] - a1 * B1[e]; B2[e] = tsign(t[e]); }
+  for (int e = 0; e < EPL; ++e) { t[e] = __builtin_fmaf(-a1, B1[e], cen[e]); B2[e] = tsign(t[e]); }
   float a2 = div_cnt(rsum_abs<EPL, LPR>(t, m), n, rn);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) t[e] = B1[e] * B2[e];
@@ -231,8 +232,8 @@ __device__ void crbog_row(const float (&x)[EPL], const bool (&m)[EPL], int order
   }
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
-    float v = mean + a1 * B1[e];
-    v = v + a2 * B2[e];
+    float v = __builtin_fmaf(a1, B1[e], mean);
+    v = __builtin_fmaf(a2, B2[e], v);
     out[e] = m[e] ? v : 0.f;
   }
 }
