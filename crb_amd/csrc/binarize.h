@@ -23,20 +23,31 @@ struct CrbConsts {
   int iters;    // refinement rounds (reference: 1)
 };
 
+// Pairwise sum of a lane's terms (depth log2(EPL) instead of EPL - 1
+// dependent adds).
+template <int N>
+__device__ __forceinline__ float tree_sum(float (&t)[N]) {
+#pragma unroll
+  for (int w = 1; w < N; w <<= 1)
+#pragma unroll
+    for (int e = 0; e + w < N; e += 2 * w) t[e] = t[e] + t[e + w];
+  return t[0];
+}
+
 template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rsum(const float (&v)[EPL], const bool (&m)[EPL]) {
-  float s = 0.f;
+  float t[EPL];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) s += m[e] ? v[e] : 0.f;
-  return group_sum_f<LPR>(s);
+  for (int e = 0; e < EPL; ++e) t[e] = m[e] ? v[e] : 0.f;
+  return group_sum_f<LPR>(tree_sum(t));
 }
 
 template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rsum_abs(const float (&v)[EPL], const bool (&m)[EPL]) {
-  float s = 0.f;
+  float t[EPL];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) s += m[e] ? fabsf(v[e]) : 0.f;
-  return group_sum_f<LPR>(s);
+  for (int e = 0; e < EPL; ++e) t[e] = m[e] ? fabsf(v[e]) : 0.f;
+  return group_sum_f<LPR>(tree_sum(t));
 }
 
 // x / d for an integer-valued d in [1, 1024] given r = 1 / d (IEEE): the
@@ -52,27 +63,27 @@ __device__ __forceinline__ float div_cnt(float x, float d, float r) {
 // sum of values that are already 0 outside the mask
 template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rsum_z(const float (&v)[EPL]) {
-  float s = 0.f;
+  float t[EPL];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) s += v[e];
-  return group_sum_f<LPR>(s);
+  for (int e = 0; e < EPL; ++e) t[e] = v[e];
+  return group_sum_f<LPR>(tree_sum(t));
 }
 
 // sum of a * b where every product is exact (one factor a sign in
-// {-1, 0, +1}): fma(a, b, s) is the reference's fl(s + fl(a * b))
+// {-1, 0, +1}): fma(a, b, s) is fl(s + fl(a * b)) in one instruction
 template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rdot_sign(const float (&a)[EPL], const float (&b)[EPL]) {
-  float s = 0.f;
+  float t[EPL / 2];
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) s = __builtin_fmaf(a[e], b[e], s);
-  return group_sum_f<LPR>(s);
+  for (int e = 0; e < EPL / 2; ++e) t[e] = __builtin_fmaf(a[2 * e + 1], b[2 * e + 1], a[2 * e] * b[2 * e]);
+  return group_sum_f<LPR>(tree_sum(t));
 }
 
 template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rcount(const bool (&m)[EPL]) {
-  float c = 0.f;
+  float c = m[0] ? 1.f : 0.f;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) c += m[e] ? 1.f : 0.f;
+  for (int e = 1; e < EPL; ++e) c += m[e] ? 1.f : 0.f;
   return group_sum_f<LPR>(c);  // integer-valued, exact
 }
 
