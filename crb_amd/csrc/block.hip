@@ -384,14 +384,32 @@ __global__ __launch_bounds__(256) void k_qpass1(
   }
 }
 
-// Block-wide exclusive scan of H (multiple of 256) counters in LDS.
-// The counters are the sums of NC copies `cstride` apart.
-// The first 256 threads do the work; every thread of the workgroup (256 or
-// more) must call it, for the barriers.
+// Inclusive scan of a 32-bit value over the 64 lanes: row_shr 1, 2, 4, 8
+// inside rows of 16 (zero fill), then row_bcast15 / row_bcast31 carry the
+// row totals.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_u32_rows(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xF, true);
+}
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
+  v += dpp_u32_rows<0x111, 0xF>(v);          // row_shr:1
+  v += dpp_u32_rows<0x112, 0xF>(v);          // row_shr:2
+  v += dpp_u32_rows<0x114, 0xF>(v);          // row_shr:4
+  v += dpp_u32_rows<0x118, 0xF>(v);          // row_shr:8
+  v += dpp_u32_rows<0x142, 0xA>(v);          // row_bcast:15 into rows 1, 3
+  v += dpp_u32_rows<0x143, 0xC>(v);          // row_bcast:31 into rows 2, 3
+  return v;
+}
+
+// Block-wide exclusive scan of H (multiple of 256) counters in LDS: each of
+// the first 256 threads sums H / 256 consecutive counters, the 4 wavefronts
+// scan their sums with DPP, and one barrier shares the wavefront totals.
+// Every thread of the workgroup (256 or more) must call it, for the
+// barriers.
 template <int H>
 __device__ void block_scan(const uint32_t* src, uint32_t* cum, uint32_t* tmp /* 256 */) {
   constexpr int PER = H / 256;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, wv = tid >> 6;
   const bool act = tid < 256;
   uint32_t loc[PER];
   uint32_t sum = 0;
@@ -399,16 +417,12 @@ __device__ void block_scan(const uint32_t* src, uint32_t* cum, uint32_t* tmp /* 
   for (int k = 0; k < PER; ++k) loc[k] = act ? src[tid * PER + k] : 0u;
 #pragma unroll
   for (int k = 0; k < PER; ++k) sum += loc[k];
-  if (act) tmp[tid] = sum;
+  const uint32_t inc = wave_scan_u32(sum);
+  if (act && (tid & 63) == 63) tmp[wv] = inc;
   __syncthreads();
-  for (int o = 1; o < 256; o <<= 1) {
-    const uint32_t v = (act && tid >= o) ? tmp[tid - o] : 0u;
-    __syncthreads();
-    if (act) tmp[tid] += v;
-    __syncthreads();
-  }
   if (act) {
-    uint32_t run = tmp[tid] - sum;
+    uint32_t run = inc - sum;
+    for (int w = 0; w < wv; ++w) run += tmp[w];
 #pragma unroll
     for (int k = 0; k < PER; ++k) { cum[tid * PER + k] = run; run += loc[k]; }
   }
@@ -473,15 +487,12 @@ __global__ __launch_bounds__(256) void k_qscan1(int64_t n, SearchWs s) {
       const int b = bins[tid];
       if (lead[b] == tid) c = (b + 1 < H1 ? cum[b + 1] : (uint32_t)n) - cum[b];
     }
-    cap[tid] = c;
+    const uint32_t inc = wave_scan_u32(c);
+    if ((tid & 63) == 63) cap[tid >> 6] = inc;
     __syncthreads();
-    for (int o = 1; o < 256; o <<= 1) {
-      const uint32_t v = tid >= o ? cap[tid - o] : 0u;
-      __syncthreads();
-      cap[tid] += v;
-      __syncthreads();
-    }
-    if (tid < NT) s.list_off[tid] = (int)(cap[tid] - c);
+    uint32_t off = inc - c;
+    for (int w = 0; w < (tid >> 6); ++w) off += cap[w];
+    if (tid < NT) s.list_off[tid] = (int)off;
   }
 }
 
