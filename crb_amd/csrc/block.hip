@@ -292,18 +292,6 @@ struct ParA {           // a group's fp32 parameters for the residual pass
   float m1, hi, lo, m2, a1;   // hi = fl(a1 + m1), lo = fl(-a1 + m1)
 };
 
-// e = (x - s1) - m2 with s1 = sign(x - m1)*a1 + m1 in fp32 (binary.py:26,
-// 32-34): sign*a1 is exact, so the fma rounds once, like the reference's
-// add, and s1 is one of hi, lo, m1 (arithmetic rather than a select chain,
-// which the compiler turns into branches)
-__device__ __forceinline__ float resid(float x, const ParA& g) {
-  const float d = x - g.m1;
-  const float sg = copysignf(d != 0.f ? 1.f : 0.f, d);
-  const float s1 = fmaf(sg, g.a1, g.m1);
-  const float r = x - s1;
-  return r - g.m2;
-}
-
 // The kernel (k_phase_a_rows) follows the sorting helpers below.
 
 // ---------------------------------------------------------------------------
@@ -1130,16 +1118,27 @@ __device__ __forceinline__ void row_abs(const float* x, int c0, int c1, float m1
   a.ad += (double)p;
 }
 
-__device__ __forceinline__ void row_res(const float* x, int c0, int c1, const ParA& g,
+// Residual moments over x[c0, c1) of a group with parameters g.  Each
+// element takes s1 = m1 + (x > m1 ? a1 : -a1), the reference's
+// sign(x - m1) * a1 + m1 (binary.py:26, 32-34; the product is exact, so
+// the add rounds as the reference's does) except where x == m1, whose sign
+// is 0 and s1 = m1.  Those n0 elements (known from the sign counts) all
+// contributed the same e0 = fl(fl(m1 - lo) - m2) here, and their sums are
+// moved to the reference's e = -m2 afterwards, so the loop carries no zero
+// test.  e^2 is accumulated with fma.
+__device__ __forceinline__ void row_res(const float* x, int c0, int c1, const ParA& g, int n0,
                                         RowRes& r) {
+  const float na1 = -g.a1;
   int c = c0;
   for (; c + 8 <= c1; c += 8) {
     float p1 = 0.f, p2 = 0.f;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const float e = resid(x[c + u], g);
+      const float v = x[c + u];
+      const float s1 = g.m1 + (v > g.m1 ? g.a1 : na1);
+      const float e = (v - s1) - g.m2;
       p1 += fabsf(e);
-      p2 += e * e;
+      p2 = __builtin_fmaf(e, e, p2);
       r.nz += e != 0.f ? 1 : 0;
     }
     r.e1 += (double)p1;
@@ -1147,13 +1146,22 @@ __device__ __forceinline__ void row_res(const float* x, int c0, int c1, const Pa
   }
   float p1 = 0.f, p2 = 0.f;
   for (; c < c1; ++c) {
-    const float e = resid(x[c], g);
+    const float v = x[c];
+    const float s1 = g.m1 + (v > g.m1 ? g.a1 : na1);
+    const float e = (v - s1) - g.m2;
     p1 += fabsf(e);
-    p2 += e * e;
+    p2 = __builtin_fmaf(e, e, p2);
     r.nz += e != 0.f ? 1 : 0;
   }
   r.e1 += (double)p1;
   r.e2 += (double)p2;
+  if (n0 > 0) {
+    const float e0 = (g.m1 - g.lo) - g.m2;
+    const double m2 = (double)g.m2, d0 = (double)e0;
+    r.e1 += (double)n0 * (fabs(m2) - fabs(d0));
+    r.e2 += (double)n0 * (m2 * m2 - d0 * d0);
+    r.nz += n0 * ((g.m2 != 0.f ? 1 : 0) - (e0 != 0.f ? 1 : 0));
+  }
 }
 
 // fp64 sum of x[c0, c1): eight loads in flight per step, each step's
@@ -1194,8 +1202,8 @@ __device__ __forceinline__ double row_cand_err(const float* x, int i, int nc, do
   const float m2C = nC > 0.f ? (float)(pc - s1C) / nC : 0.f;
   const ParA PS = {m1S, hiS, loS, m2S, a1S}, PC = {m1C, hiC, loC, m2C, a1C};
   RowRes rS = {0.0, 0.0, 0}, rC = {0.0, 0.0, 0};
-  row_res(x, 0, i, PS, rS);
-  row_res(x, i, nc, PC, rC);
+  row_res(x, 0, i, PS, i - aS.npos - aS.nneg, rS);
+  row_res(x, i, nc, PC, (nc - i) - aC.npos - aC.nneg, rC);
   // sum (e - a2 sign(e))^2 = sum e^2 - 2 a2 sum |e| + a2^2 #(e != 0)
   const double a2S = (double)((float)rS.e1 / nS);
   const double a2C = nC > 0.f ? (double)((float)rC.e1 / nC) : 0.0;
