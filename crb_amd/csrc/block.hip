@@ -656,18 +656,6 @@ struct SortedRow {
   int n;
 };
 
-// first index in [0, n) with v[i] >= x (lower bound) / v[i] > x (upper bound)
-__device__ __forceinline__ int lbound(const float* v, int n, float x) {
-  int lo = 0, hi = n;
-  while (lo < hi) { const int m = (lo + hi) >> 1; if (v[m] < x) lo = m + 1; else hi = m; }
-  return lo;
-}
-__device__ __forceinline__ int ubound(const float* v, int n, float x) {
-  int lo = 0, hi = n;
-  while (lo < hi) { const int m = (lo + hi) >> 1; if (v[m] <= x) lo = m + 1; else hi = m; }
-  return lo;
-}
-
 struct Stat { double n, s, q; };
 __device__ __forceinline__ Stat rstat(const SortedRow& r, int l, int h) {
   if (h <= l) return Stat{0.0, 0.0, 0.0};
@@ -677,14 +665,35 @@ __device__ __forceinline__ double sqdev(const Stat& a, double t) {   // sum (v -
   return a.q - 2.0 * t * a.s + a.n * t * t;
 }
 
-// order-1 error of the group made of sorted ranges [l1,h1) and [l2,h2)
-__device__ double group_err1(const SortedRow& r, int l1, int h1, int l2, int h2) {
-  const int n = max(h1 - l1, 0) + max(h2 - l2, 0);
+// Number of v[0, n) below x (STRICT: the lower bound) or not above x (the
+// upper bound) in a sorted row, n <= 128: 8 fixed halving steps instead of
+// a data-dependent loop, since the lanes of a wavefront search different
+// rows and thresholds; independent searches interleave their LDS reads.
+template <bool STRICT>
+__device__ __forceinline__ int bcount(const float* v, int n, float x) {
+  int pos = 0;
+#pragma unroll
+  for (int step = NCMAX; step >= 1; step >>= 1) {
+    const float y = v[min(pos + step - 1, NCMAX - 1)];
+    const bool take = pos + step <= n && (STRICT ? y < x : y <= x);
+    pos += take ? step : 0;
+  }
+  return pos;
+}
+
+// sum over the group made of sorted ranges [l1,h1) and [l2,h2) and its size
+__device__ __forceinline__ double group_sum2(const SortedRow& r, int l1, int h1, int l2, int h2,
+                                             int& n) {
+  n = max(h1 - l1, 0) + max(h2 - l2, 0);
+  return rstat(r, l1, h1).s + rstat(r, l2, h2).s;
+}
+
+// order-1 error of that group (binary.py:18-39 with order 1) given its mean
+// mu and the row's lower / upper bounds lb / ub of mu
+__device__ double group_err1(const SortedRow& r, int l1, int h1, int l2, int h2, int n,
+                             float mu, int lb, int ub) {
   if (n == 0) return 0.0;
-  const Stat a1 = rstat(r, l1, h1), a2 = rstat(r, l2, h2);
   const float nf = (float)n;
-  const float mu = (float)(a1.s + a2.s) / nf;
-  const int lb = lbound(r.v, r.n, mu), ub = ubound(r.v, r.n, mu);
   double sabs = 0.0, err = 0.0;
   Stat parts[2][3];
   const int L[2] = {l1, l2}, Hh[2] = {h1, h2};
@@ -704,6 +713,20 @@ __device__ double group_err1(const SortedRow& r, int l1, int h1, int l2, int h2)
     err += sqdev(parts[g][0], (double)lo) + sqdev(parts[g][1], (double)mu) +
            sqdev(parts[g][2], (double)hi);
   return err;
+}
+
+// Error of split candidate thr on a sorted row of n non-salient targets
+// (utils/autosearch.py:72-80): M1 = {-thr < v < thr} = [a, b),
+// M2 = [0, a) + [b, n), each binarized at order 1 (utils/mask.py:7-18).
+__device__ double split_err(const SortedRow& r, int n, float thr) {
+  const int a = bcount<false>(r.v, n, -thr);
+  const int b = max(bcount<true>(r.v, n, thr), a);
+  int n1, n2;
+  const double s1 = group_sum2(r, a, b, 0, 0, n1), s2 = group_sum2(r, 0, a, b, n, n2);
+  const float mu1 = n1 ? (float)s1 / (float)n1 : 0.f, mu2 = n2 ? (float)s2 / (float)n2 : 0.f;
+  const int lb1 = bcount<true>(r.v, n, mu1), ub1 = bcount<false>(r.v, n, mu1);
+  const int lb2 = bcount<true>(r.v, n, mu2), ub2 = bcount<false>(r.v, n, mu2);
+  return group_err1(r, a, b, 0, 0, n1, mu1, lb1, ub1) + group_err1(r, 0, a, b, n, n2, mu2, lb2, ub2);
 }
 
 // Partner value of a xor-j exchange inside the wavefront, without the LDS
@@ -855,12 +878,7 @@ __global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
     for (int pq = tid; pq < PC_WAVES * NQ; pq += 64 * PC_WAVES) {
       const int q = pq / NQ, k = pq - q * NQ;
       if (r0 + q < R) {
-        const SortedRow& rq = rows[q];
-        const float thr = pv[k];
-        // M1 = {-thr < v < thr} = [a, b), M2 = [0, a) + [b, n)
-        const int a = ubound(rq.v, n, -thr);
-        const int b = max(lbound(rq.v, n, thr), a);
-        errs[q][k] = group_err1(rq, a, b, 0, 0) + group_err1(rq, 0, a, b, n);
+        errs[q][k] = split_err(rows[q], n, pv[k]);
       }
     }
     __syncthreads();
