@@ -984,13 +984,34 @@ __global__ __launch_bounds__(256) void k_quantize(QuantArgs a, SearchWs s) {
   }
 }
 
-// k_quantize for blocks of at most 128 columns with 16 lanes per row (16
-// rows per workgroup), 8 elements per lane at columns 4r .. 4r+3 and
-// 64 + 4r .. 64 + 4r+3, 16-byte loads and stores (W, err and their row
-// strides 16-byte aligned, masks 4-byte aligned; the host checks).
+// VW consecutive floats through one 16-, 8- or 4-byte access
+template <int VW>
+__device__ __forceinline__ void vload(const float* p, float* v) {
+  if constexpr (VW == 4) { const float4 q = *(const float4*)p; v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w; }
+  else if constexpr (VW == 2) { const float2 q = *(const float2*)p; v[0] = q.x; v[1] = q.y; }
+  else v[0] = *p;
+}
+template <int VW>
+__device__ __forceinline__ void vstore(float* p, const float* v) {
+  if constexpr (VW == 4) *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
+  else if constexpr (VW == 2) *(float2*)p = make_float2(v[0], v[1]);
+  else *p = v[0];
+}
+// k_quantize for blocks of at most 128 columns with QG_LPR lanes per row
+// (256 / QG_LPR rows per workgroup) and 128 / QG_LPR elements per lane, in
+// runs of VW = min(4, 128 / QG_LPR) consecutive columns: lane r holds columns
+// h*VW*QG_LPR + r*VW + j.  Loads and stores move VW floats at a time (W, err
+// and their row strides 16-byte aligned, masks 4-byte aligned; the host
+// checks).  32 lanes per row (8 rows per workgroup) keeps two wavefronts per
+// SIMD on a 4096-row block, which hides more of the reductions' latency than
+// 16 lanes (one wavefront per SIMD) or 8.
+#ifndef CRBQ_QG_LPR
+#define CRBQ_QG_LPR 32
+#endif
+constexpr int QG_LPR = CRBQ_QG_LPR;          // lanes per row of the block quantize
 template <int MF>
 __global__ __launch_bounds__(256) void k_quantize_g(QuantArgs a, SearchWs s) {
-  constexpr int EPL = 8, LPR = 16;
+  constexpr int LPR = QG_LPR, EPL = 128 / LPR, VW = EPL < 4 ? EPL : 4, NH = EPL / VW;
   const int r = threadIdx.x % LPR;
   const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
   if (row >= a.R) return;                    // whole lane groups leave together
@@ -1001,19 +1022,18 @@ __global__ __launch_bounds__(256) void k_quantize_g(QuantArgs a, SearchWs s) {
   bool valid[EPL];
   float* wr = a.W + (int64_t)row * a.ldw;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int c0 = h * 64 + r * 4;
-    if (c0 + 3 < a.nc) {
-      const float4 q = *(const float4*)(wr + c0);
-      x[4 * h] = q.x; x[4 * h + 1] = q.y; x[4 * h + 2] = q.z; x[4 * h + 3] = q.w;
+  for (int h = 0; h < NH; ++h) {
+    const int c0 = h * VW * LPR + r * VW;
+    if (c0 + VW - 1 < a.nc) {
+      vload<VW>(wr + c0, x + VW * h);
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[4 * h + j] = c0 + j < a.nc ? wr[c0 + j] : 0.f;
+      for (int j = 0; j < VW; ++j) x[VW * h + j] = c0 + j < a.nc ? wr[c0 + j] : 0.f;
     }
   }
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
-    const int c = (e >> 2) * 64 + r * 4 + (e & 3);
+    const int c = (e / VW) * VW * LPR + r * VW + e % VW;
     valid[e] = c < a.nc;
     dd[e] = valid[e] ? a.U[(int64_t)c * a.ldu + c] : 1.f;
     int g = -1;
@@ -1058,25 +1078,26 @@ __global__ __launch_bounds__(256) void k_quantize_g(QuantArgs a, SearchWs s) {
   float* er = a.err + (int64_t)row * a.lde;
   uint8_t* mr = a.masks ? a.masks + (int64_t)row * a.ldm : nullptr;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int c0 = h * 64 + r * 4;
-    if (c0 + 3 < a.nc) {
-      *(float4*)(wr + c0) = make_float4(q[4 * h], q[4 * h + 1], q[4 * h + 2], q[4 * h + 3]);
-      if (a.gptq)
-        *(float4*)(er + c0) = make_float4(ev[4 * h], ev[4 * h + 1], ev[4 * h + 2], ev[4 * h + 3]);
+  for (int h = 0; h < NH; ++h) {
+    const int c0 = h * VW * LPR + r * VW;
+    if (c0 + VW - 1 < a.nc) {
+      vstore<VW>(wr + c0, q + VW * h);
+      if (a.gptq) vstore<VW>(er + c0, ev + VW * h);
       if (mr) {
         unsigned mb = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) mb |= (unsigned)(grp[4 * h + j] + 1) << (8 * j);
-        *(unsigned*)(mr + c0) = mb;
+        for (int j = 0; j < VW; ++j) mb |= (unsigned)(grp[VW * h + j] + 1) << (8 * j);
+        if (VW == 4) *(unsigned*)(mr + c0) = mb;
+        else if (VW == 2) *(uint16_t*)(mr + c0) = (uint16_t)mb;
+        else mr[c0] = (uint8_t)mb;
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < VW; ++j) {
         if (c0 + j >= a.nc) continue;
-        wr[c0 + j] = q[4 * h + j];
-        if (a.gptq) er[c0 + j] = ev[4 * h + j];
-        if (mr) mr[c0 + j] = (uint8_t)(grp[4 * h + j] + 1);
+        wr[c0 + j] = q[VW * h + j];
+        if (a.gptq) er[c0 + j] = ev[VW * h + j];
+        if (mr) mr[c0 + j] = (uint8_t)(grp[VW * h + j] + 1);
       }
     }
   }
@@ -1515,7 +1536,7 @@ static int fasterquant_impl(float* W, int64_t R, int64_t C, int64_t ldw, const f
 #define CRBQ_QUANT_GO(MF_)                                                  \
   do {                                                                      \
     if (vec && nc <= 128)                                                   \
-      k_quantize_g<MF_><<<(unsigned)cdiv(R, 16), 256, 0, hs>>>(a, s);       \
+      k_quantize_g<MF_><<<(unsigned)cdiv(R, 256 / QG_LPR), 256, 0, hs>>>(a, s); \
     else                                                                    \
       k_quantize<MF_, 2><<<(unsigned)cdiv(R, 4), 256, 0, hs>>>(a, s);       \
   } while (0)
