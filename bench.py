@@ -312,7 +312,7 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
     ms = _ev_ms(step, reps) - ms_copy
     by = R * 128 * 4 * 3 + 128 * 128 * 4 + R * 128
     out["block_step"] = {
-        "kernels": "colscore, phase_a, qpass1, qscan1, qlist, qselect, phase_c, quantize",
+        "kernels": "colscore, phase_a, qpass1, qlist, qselect, phase_c, quantize",
         "shape": [R, 128], "ms": round(ms, 4), "achieved": round(by / ms / 1e6, 1),
         "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(by / ms / 1e6 / (PEAK_HBM / 1e9), 4),
         "note": "2 MB working set per block, resident in L2/MALL; bound by the search's "

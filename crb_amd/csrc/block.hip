@@ -11,7 +11,7 @@
 //                complement (group sums from fp64 chunk sums, two passes,
 //                closed-form error); the last workgroup takes
 //                i* = first strict minimum
-//   k_qpass1, k_qscan1, k_qlist, k_qselect
+//   k_qpass1, k_qlist, k_qselect
 //                exact np.quantile of |T * ~M3| at the 81 float32
 //                percentiles: level-1 histogram of the top 12 bits of the
 //                non-negative float's bit pattern, the bins of the 162
@@ -90,7 +90,6 @@ struct SearchWs {
   double* parta;     // [nwg_a][UPMAX]
   double* partc;     // [nwg_c][96]
   uint32_t* hist1;   // [H1]
-  int* slot1map;     // [H1]
   Tgt* tgt;          // [NT]
   float* gam;        // [NQ]
   int* list_off;     // [NT]: start of each leader target's element list
@@ -109,7 +108,6 @@ static void carve_search(WsCarver& c, int64_t R, SearchWs& s) {
   s.parta = c.take<double>((size_t)PX_MAXWG * UPMAX);
   s.partc = c.take<double>((size_t)PX_MAXWG * 96);
   s.hist1 = c.take<uint32_t>(H1);
-  s.slot1map = c.take<int>(H1);
   s.tgt = c.take<Tgt>(NT);
   s.gam = c.take<float>(NQ);
   s.list_off = c.take<int>(NT);
@@ -249,6 +247,7 @@ __global__ __launch_bounds__(CS_THREADS) void k_colscore(
   // zero the level-1 histogram used later by this block (grid-stride)
   const size_t gsz = (size_t)gridDim.x * blockDim.x;
   for (size_t i = (size_t)blockIdx.x * blockDim.x + tid; i < (size_t)H1; i += gsz) s.hist1[i] = 0u;
+  if (blockIdx.x == 0 && tid < NT) s.list_cnt[tid] = 0;       // k_qlist's list counters
   __syncthreads();
   if (ph == 0) {
     double v = 0.0;
@@ -328,15 +327,6 @@ __device__ __forceinline__ void q_cols(const float* __restrict__ U, int64_t ldu,
     rk[c] = s.rank[c];
     if (c < nc) { const float dg = U[(int64_t)c * ldu + c]; d2s[c] = dg * dg; }
   }
-}
-
-// the level-1 leader map into LDS (H1 / 256 loads per thread, issued together)
-__device__ __forceinline__ void q_slotmap(const SearchWs& s, int* sm) {
-  int v[H1 / 256];
-#pragma unroll
-  for (int k = 0; k < H1 / 256; ++k) v[k] = s.slot1map[threadIdx.x + 256 * k];
-#pragma unroll
-  for (int k = 0; k < H1 / 256; ++k) sm[threadIdx.x + 256 * k] = v[k];
 }
 
 // Level-1: histogram of bits [31:20] of the (non-negative) float pattern.
@@ -428,17 +418,45 @@ __device__ __forceinline__ int find_bin(const uint32_t* cum, uint32_t r) {
   return lo;
 }
 
-__global__ __launch_bounds__(256) void k_qscan1(int64_t n, SearchWs s) {
+// Elements of the target bins into their bin's list.  Every workgroup
+// first places the NT order statistics in the level-1 histogram itself (the
+// 4096 counters come from L2; repeating this small scan per workgroup costs
+// less than a launch of its own): an exclusive scan of the counters, numpy
+// 'linear' ranks, each target's bin by binary search, a leader per bin (its
+// first target) and the lists' offsets (exclusive scan of the leaders' bin
+// counts; bin 0's count also holds the salient columns' zeros, which are
+// not stored).  Workgroup 0 publishes the targets for the selection.  Then
+// each workgroup counts its elements per list in LDS, reserves room with
+// one global atomic per list, and writes the elements' bit patterns (the
+// order inside a list does not matter to the selection).  The list counters
+// are cleared by k_colscore.
+__global__ __launch_bounds__(256) void k_qlist(
+    const float* __restrict__ W, int64_t ldw, int R, int nc,
+    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
   __shared__ uint32_t cum[H1];
-  __shared__ uint32_t tmp[256];
   __shared__ int lead[H1];
+  __shared__ uint32_t tmp[256];
+  __shared__ float d2s[NCMAX];
+  __shared__ int rk[NCMAX];
+  __shared__ int cnt[NT];
+  __shared__ int base[NT];
+  __shared__ int loff[NT];
+  __shared__ int bins[NT];
   const int tid = threadIdx.x;
-  block_scan<H1>(s.hist1, cum, tmp);
+  const int r0 = blockIdx.x * Q_RPW, r1 = min(R, r0 + Q_RPW);
+  const int64_t n = (int64_t)R * nc;
+  float w[QE];
+  int col[QE];
+  q_load(W, ldw, r0, r1, nc, w, col);
+  const int istar = s.ctrl->istar;
+  q_cols(U, ldu, nc, s, rk, d2s);
   for (int i = tid; i < H1; i += 256) lead[i] = NONE;
-  __syncthreads();
-  if (tid < NQ) {
+  if (tid < NT) cnt[tid] = 0;
+  block_scan<H1>(s.hist1, cum, tmp);
+  if (tid < NT) {
     // numpy 'linear': virtual index (n-1)*q in float32, floor, fractional gamma
-    const float vi = (float)(n - 1) * c_q[tid];
+    const int q = tid >> 1;
+    const float vi = (float)(n - 1) * c_q[q];
     int64_t lo, hi;
     float g;
     if (vi >= (float)(n - 1)) { lo = hi = n - 1; g = 0.f; }
@@ -446,29 +464,19 @@ __global__ __launch_bounds__(256) void k_qscan1(int64_t n, SearchWs s) {
       const float fl = floorf(vi);
       lo = (int64_t)fl; hi = lo + 1; g = vi - fl;
     }
-    s.gam[tid] = g;
-    s.tgt[2 * tid].rank = lo;
-    s.tgt[2 * tid + 1].rank = hi;
-  }
-  __syncthreads();
-  __shared__ int bins[NT];
-  if (tid < NT) {
-    Tgt& t = s.tgt[tid];
-    const uint32_t r = (uint32_t)t.rank;
-    const int b = find_bin<H1>(cum, r);
-    t.bin1 = b;
-    t.r1 = (int)(r - cum[b]);
+    const int64_t rnk = (tid & 1) ? hi : lo;
+    const int b = find_bin<H1>(cum, (uint32_t)rnk);
     bins[tid] = b;
     atomicMin(&lead[b], tid);
+    if (blockIdx.x == 0) {
+      Tgt& t = s.tgt[tid];
+      t.rank = rnk;
+      t.bin1 = b;
+      t.r1 = (int)((uint32_t)rnk - cum[b]);
+      if (!(tid & 1)) s.gam[q] = g;
+    }
   }
   __syncthreads();
-  for (int i = tid; i < H1; i += 256) s.slot1map[i] = lead[i] == NONE ? -1 : lead[i];
-  if (tid < NT) s.tgt[tid].slot1 = lead[bins[tid]];
-  // element lists of the target bins, one per leader, in target order; a
-  // list's capacity is its bin's count (bin 0's also counts the salient
-  // columns' zeros, which are not stored): exclusive scan over the targets
-  __shared__ uint32_t cap[256];
-  if (tid < NT) s.list_cnt[tid] = 0;
   {
     uint32_t c = 0;
     if (tid < NT) {
@@ -476,36 +484,18 @@ __global__ __launch_bounds__(256) void k_qscan1(int64_t n, SearchWs s) {
       if (lead[b] == tid) c = (b + 1 < H1 ? cum[b + 1] : (uint32_t)n) - cum[b];
     }
     const uint32_t inc = wave_scan_u32(c);
-    if ((tid & 63) == 63) cap[tid >> 6] = inc;
+    if ((tid & 63) == 63) tmp[tid >> 6] = inc;
     __syncthreads();
     uint32_t off = inc - c;
-    for (int w = 0; w < (tid >> 6); ++w) off += cap[w];
-    if (tid < NT) s.list_off[tid] = (int)off;
+    for (int v = 0; v < (tid >> 6); ++v) off += tmp[v];
+    if (tid < NT) {
+      loff[tid] = (int)off;
+      if (blockIdx.x == 0) {
+        s.list_off[tid] = (int)off;
+        s.tgt[tid].slot1 = lead[bins[tid]];
+      }
+    }
   }
-}
-
-// Elements of the target bins into their leader's list: each workgroup
-// counts its elements per list in LDS, reserves room with one global atomic
-// per list, then writes the elements' bit patterns (the order inside a list
-// does not matter to the selection).
-__global__ __launch_bounds__(256) void k_qlist(
-    const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
-  __shared__ int sm[H1];
-  __shared__ float d2s[NCMAX];
-  __shared__ int rk[NCMAX];
-  __shared__ int cnt[NT];
-  __shared__ int base[NT];
-  const int tid = threadIdx.x;
-  const int r0 = blockIdx.x * Q_RPW, r1 = min(R, r0 + Q_RPW);
-  float w[QE];
-  int col[QE];
-  q_load(W, ldw, r0, r1, nc, w, col);
-  q_slotmap(s, sm);
-  const int istar = s.ctrl->istar;
-  q_cols(U, ldu, nc, s, rk, d2s);
-  if (tid < NT) cnt[tid] = 0;
-  __syncthreads();
   int slot[QE], pos[QE];
   uint32_t key[QE];
 #pragma unroll
@@ -517,14 +507,14 @@ __global__ __launch_bounds__(256) void k_qlist(
     if (c < 0 || rk[c] < istar) continue;  // salient columns: implicit zeros
     const float v = fabsf(target_of(w[k], d2s[c], metric));
     key[k] = __float_as_uint(v);
-    const int sl = sm[key[k] >> SH1];
-    if (sl >= 0) {
+    const int sl = lead[key[k] >> SH1];
+    if (sl != NONE) {
       slot[k] = sl;
       pos[k] = atomicAdd(&cnt[sl], 1);
     }
   }
   __syncthreads();
-  if (tid < NT && cnt[tid] > 0) base[tid] = s.list_off[tid] + atomicAdd(&s.list_cnt[tid], cnt[tid]);
+  if (tid < NT && cnt[tid] > 0) base[tid] = loff[tid] + atomicAdd(&s.list_cnt[tid], cnt[tid]);
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < QE; ++k)
@@ -1340,7 +1330,6 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
   k_phase_a_rows<<<nrg * ncg, 64 * std::max(cw, PR_MINW), 0, st>>>(
       W, ldw, R, nc, U, ldu, metric, ncand, up_lim, ncg, cw, s, tr);
   k_qpass1<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  k_qscan1<<<1, 256, 0, st>>>((int64_t)R * nc, s);
   k_qlist<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
   k_qselect<<<NT, QS_T, 0, st>>>(R, nc, s);
   k_phase_c<<<nwg_c, 64 * PC_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s, tr);
