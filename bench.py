@@ -578,7 +578,7 @@ def main():
         out["roofline"]["clock_ghz_under_load"] = pv.get("syrk_fc2_clock_ghz")
     if not args.no_kernels:
         out["kernels"] = kernel_rooflines(dev)
-    print(f"[bench] kernels: {out['kernels']}", file=sys.stderr, flush=True)
+        print(f"[bench] kernels: {out['kernels']}", file=sys.stderr, flush=True)
     if args.stack_layers > 0:
         del X
         torch.cuda.empty_cache()
