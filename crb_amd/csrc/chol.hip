@@ -77,17 +77,45 @@ static inline dim3 rows_grid(int64_t C) {
   return dim3((unsigned)C, (unsigned)((C + 1023) / 1024));
 }
 
-// A[i][j] = H[C-1-i][C-1-j] in the lower triangle, 0 above it (rows_grid)
-__global__ __launch_bounds__(256) void k_reverse_lower(const float* __restrict__ H, int64_t ldh,
-                                                       int C, float* A, int64_t lda) {
+// Row i of the index-reversed copy: Y[i][j] = X[C-1-i][C-1-j] where keep(i, j)
+// holds, 0 elsewhere (rows_grid).  With vec (C, the row strides and both
+// bases multiples of 4 floats) each thread moves 4 consecutive j with one
+// 16-byte load of the source row (columns C-4-j .. C-1-j, reversed) and one
+// 16-byte store; runs wholly outside keep skip the load.
+template <bool LOWER>
+__device__ __forceinline__ void reverse_row(const float* __restrict__ X, int64_t ldx, int C,
+                                            float* Y, int64_t ldy, bool vec) {
   const int i = blockIdx.x;
-  const float* h = H + (int64_t)(C - 1 - i) * ldh + (C - 1);
-  float* a = A + (int64_t)i * lda;
+  const float* x = X + (int64_t)(C - 1 - i) * ldx;
+  float* y = Y + (int64_t)i * ldy;
+  auto keep = [i](int j) { return LOWER ? j <= i : j >= i; };
+  if (vec) {
+    const int j0 = blockIdx.y * 1024 + threadIdx.x * 4;
+    if (j0 >= C) return;
+    float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (keep(j0) || keep(j0 + 3)) {
+      const float4 v = *(const float4*)(x + (C - 4 - j0));
+      q = make_float4(keep(j0) ? v.w : 0.f, keep(j0 + 1) ? v.z : 0.f, keep(j0 + 2) ? v.y : 0.f,
+                      keep(j0 + 3) ? v.x : 0.f);
+    }
+    *(float4*)(y + j0) = q;
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int j = blockIdx.y * 1024 + k * 256 + threadIdx.x;
-    if (j < C) a[j] = j <= i ? h[-j] : 0.f;
+    if (j < C) y[j] = keep(j) ? x[C - 1 - j] : 0.f;
   }
+}
+static inline bool reverse_vec(const float* X, int64_t ldx, int64_t C, const float* Y,
+                               int64_t ldy) {
+  return (C & 3) == 0 && ((ldx | ldy) & 3) == 0 && ((((uintptr_t)X) | ((uintptr_t)Y)) & 15) == 0;
+}
+
+// A[i][j] = H[C-1-i][C-1-j] in the lower triangle, 0 above it (rows_grid)
+__global__ __launch_bounds__(256) void k_reverse_lower(const float* __restrict__ H, int64_t ldh,
+                                                       int C, float* A, int64_t lda, int vec) {
+  reverse_row<true>(H, ldh, C, A, lda, vec != 0);
 }
 
 // Y[r][c] = X[r][c] for an M x N block (row strides ldx, ldy)
@@ -103,15 +131,8 @@ __global__ __launch_bounds__(256) void k_copy2d(const float* __restrict__ X, int
 
 // U[i][j] = X[C-1-i][C-1-j] for j >= i, 0 below the diagonal (rows_grid)
 __global__ __launch_bounds__(256) void k_reverse_to_u(const float* __restrict__ X, int64_t ldx,
-                                                      int C, float* U, int64_t ldu) {
-  const int i = blockIdx.x;
-  const float* x = X + (int64_t)(C - 1 - i) * ldx + (C - 1);
-  float* u = U + (int64_t)i * ldu;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int j = blockIdx.y * 1024 + k * 256 + threadIdx.x;
-    if (j < C) u[j] = j >= i ? x[-j] : 0.f;
-  }
+                                                      int C, float* U, int64_t ldu, int vec) {
+  reverse_row<false>(X, ldx, C, U, ldu, vec != 0);
 }
 
 // Last resort (bigptq.py:124-128): L = diag(sqrt(clamp(diag H, 1e-8))),
@@ -563,11 +584,13 @@ extern "C" int crbq_hinv_upper_async(float* H, int64_t ldh, int64_t C, float* W,
   k_damp<<<1, 1024, 0, s>>>(H, ldh, Ci, percdamp, 0, w.scal);      // bigptq.py:109-111
   CRBQ_LAUNCH_CHECK();
   k_set_int<<<1, 1, 0, s>>>(w.info, 0);
-  k_reverse_lower<<<rows_grid(C), 256, 0, s>>>(H, ldh, Ci, w.A, C);
+  k_reverse_lower<<<rows_grid(C), 256, 0, s>>>(H, ldh, Ci, w.A, C,
+                                                reverse_vec(H, ldh, C, w.A, C));
   CRBQ_LAUNCH_CHECK();
   st = chol_inv_sweep(w.A, C, Ci, w, s);
   if (st) return st;
-  k_reverse_to_u<<<rows_grid(C), 256, 0, s>>>(w.A, C, Ci, U, ldu);
+  k_reverse_to_u<<<rows_grid(C), 256, 0, s>>>(w.A, C, Ci, U, ldu,
+                                               reverse_vec(w.A, C, C, U, ldu));
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }
@@ -597,7 +620,8 @@ extern "C" int crbq_hinv_upper_finish(float* H, int64_t ldh, int64_t C, float* U
     CRBQ_LAUNCH_CHECK();
     if (attempt == 10) break;                                       // 10 attempts in all
     k_set_int<<<1, 1, 0, s>>>(w.info, 0);
-    k_reverse_lower<<<rows_grid(C), 256, 0, s>>>(H, ldh, Ci, w.A, C);
+    k_reverse_lower<<<rows_grid(C), 256, 0, s>>>(H, ldh, Ci, w.A, C,
+                                                reverse_vec(H, ldh, C, w.A, C));
     CRBQ_LAUNCH_CHECK();
     st = chol_inv_sweep(w.A, C, Ci, w, s);
     if (st) return st;
@@ -605,7 +629,8 @@ extern "C" int crbq_hinv_upper_finish(float* H, int64_t ldh, int64_t C, float* U
     CRBQ_HIP(hipStreamSynchronize(s));
     ok = hinfo == 0;
     if (ok) {
-      k_reverse_to_u<<<rows_grid(C), 256, 0, s>>>(w.A, C, Ci, U, ldu);
+      k_reverse_to_u<<<rows_grid(C), 256, 0, s>>>(w.A, C, Ci, U, ldu,
+                                               reverse_vec(w.A, C, C, U, ldu));
       CRBQ_LAUNCH_CHECK();
     }
   }

@@ -531,17 +531,65 @@ __global__ __launch_bounds__(256) void k_syrk32(const float* __restrict__ X, int
 
 // H = scale * sym(S) from the upper triangle of S, in 64 x 64 tiles: the
 // workgroup of upper tile (ti, tj) stages it in LDS and writes it and its
-// mirror (tj, ti) with row-contiguous stores.  Grid: x = tj, y = ti;
-// workgroups below the diagonal exit.  H may alias S: a workgroup reads
-// only its own upper tile, and lower tiles are never read.
+// mirror (tj, ti) with row-contiguous stores (16-byte accesses when rows
+// are 16-byte aligned and the tile lies inside the matrix).  Grid: the
+// nt (nt + 1) / 2 upper tiles, row by row from the last.  H may alias S: a
+// workgroup reads only its own upper tile, all of it before any store, and
+// lower tiles are never read.
 constexpr int FT = 64;
+__device__ __forceinline__ void upper_tile(int id, int nt, int& ti, int& tj) {
+  const int k = nt * (nt + 1) / 2 - 1 - id;          // lower-triangle index (r >= b)
+  int r = (int)((sqrtf(8.f * (float)k + 1.f) - 1.f) * 0.5f);
+  while ((r + 1) * (r + 2) / 2 <= k) ++r;
+  while (r * (r + 1) / 2 > k) --r;
+  const int b = k - r * (r + 1) / 2;
+  ti = nt - 1 - r;
+  tj = nt - 1 - b;
+}
+
 __global__ __launch_bounds__(256) void k_finalize(const float* S, int64_t lds, int C,
-                                                  float scale, float* H, int64_t ldh) {
-  const int tj = blockIdx.x, ti = blockIdx.y;
-  if (ti > tj) return;
+                                                  float scale, float* H, int64_t ldh, int nt,
+                                                  int vec) {
+  int ti, tj;
+  upper_tile(blockIdx.x, nt, ti, tj);
   __shared__ float T[FT][FT + 1];
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
   const int r0 = ti * FT, c0 = tj * FT;
+  const bool diag = ti == tj;
+  if (vec && r0 + FT <= C && c0 + FT <= C) {
+    // thread: rows tid / 16 + 16 k, columns 4 (tid % 16) .. + 3
+    const int rr = tid >> 4, cc = (tid & 15) * 4;
+    float4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      v[k] = *(const float4*)(S + (int64_t)(r0 + rr + 16 * k) * lds + c0 + cc);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = rr + 16 * k;
+      T[r][cc] = scale * v[k].x;
+      T[r][cc + 1] = scale * v[k].y;
+      T[r][cc + 2] = scale * v[k].z;
+      T[r][cc + 3] = scale * v[k].w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = rr + 16 * k;
+      float q[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q[e] = (!diag || r <= cc + e) ? T[r][cc + e] : T[cc + e][r];
+      *(float4*)(H + (int64_t)(r0 + r) * ldh + c0 + cc) = make_float4(q[0], q[1], q[2], q[3]);
+    }
+    if (diag) return;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = rr + 16 * k;
+      *(float4*)(H + (int64_t)(c0 + r) * ldh + r0 + cc) =
+          make_float4(T[cc][r], T[cc + 1][r], T[cc + 2][r], T[cc + 3][r]);
+    }
+    return;
+  }
+  const int tx = tid & 63, ty = tid >> 6;
 #pragma unroll
   for (int k = 0; k < FT; k += 4) {
     const int r = r0 + ty + k, c = c0 + tx;
@@ -550,7 +598,7 @@ __global__ __launch_bounds__(256) void k_finalize(const float* S, int64_t lds, i
     T[ty + k][tx] = v;
   }
   __syncthreads();
-  if (ti == tj) {
+  if (diag) {
 #pragma unroll
     for (int k = 0; k < FT; k += 4) {
       const int r = ty + k, c = tx;
@@ -804,9 +852,10 @@ extern "C" int crbq_syrk_timing_collect(float* ms, int64_t* C, int max, int* n) 
 extern "C" int crbq_hessian_finalize(const float* S, int64_t lds, int64_t C, float scale,
                                      float* H, int64_t ldh, void* stream) {
   if (!S || !H || C <= 0 || C > (1 << 20) || lds < C || ldh < C) return CRBQ_ERR_ARG;
-  const unsigned nt = (unsigned)((C + crbq::FT - 1) / crbq::FT);
-  crbq::k_finalize<<<dim3(nt, nt), 256, 0, (hipStream_t)stream>>>(S, lds, (int)C, scale, H,
-                                                                    ldh);
+  const int nt = (int)((C + crbq::FT - 1) / crbq::FT);
+  const int vec = ((lds | ldh) & 3) == 0 && ((((uintptr_t)S) | ((uintptr_t)H)) & 15) == 0;
+  crbq::k_finalize<<<(unsigned)(nt * (nt + 1) / 2), 256, 0, (hipStream_t)stream>>>(
+      S, lds, (int)C, scale, H, ldh, nt, vec);
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }
