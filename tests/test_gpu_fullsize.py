@@ -1,8 +1,8 @@
 """Size-independent properties at the BASELINE configs' full sizes
-(configs[1] OPT-1.3B layer crb vs braq, configs[3] OPT-66B fc2 with a
-36864^2 Hessian, configs[4] Llama-3-8B layer in bf16 with 1 % outlier
-columns, crb with 5 refinement rounds and crbog), where the CPU oracle is
-too slow to run:
+(configs[1] OPT-1.3B layer crb vs braq, configs[3] the whole OPT-66B layer
+with fc2's 36864^2 Hessian, configs[4] Llama-3-8B layer in bf16 with 1 %
+outlier columns, crb with 5 refinement rounds against crbog by per-layer
+reconstruction error), where the CPU oracle is too slow to run:
 
 * Hessian: 256 sampled entries against float64 dot products over all
   128 x 2048 tokens (relative to sqrt(H_ii H_jj)).
@@ -65,9 +65,12 @@ def _hessian(X, nseq=128):
     return H
 
 
-def _quantize_check(name, W16, H, method, refine_iters=1):
+def _quantize_check(name, W16, H, method, refine_iters=1, nseq=128, recon=None):
     """One sublayer through the factor and the block loop; checks the GPTQ
-    identity and the binarization structure.  Returns the layer error."""
+    identity and the binarization structure.  Returns the sublayer's GPTQ
+    loss.  With recon (a dict), also adds the reconstruction error
+    ||(W - Q) X^T||_F^2 over the calibration tokens to recon[method]: with
+    H = (2 / nseq) X^T X (undamped), it is (nseq / 2) sum((D H) * D)."""
     Hd = H.clone()
     W = W16.float().contiguous()
     U, retries, fb = _k().hinv_upper(Hd, W, 0.01)          # Hd is now the damped H
@@ -85,6 +88,10 @@ def _quantize_check(name, W16, H, method, refine_iters=1):
           f"row max {float(rel.max()):.2e}", flush=True)
     assert tot < 1e-3, tot
     assert float(rel.max()) < 1e-2, float(rel.max())
+    if recon is not None:
+        r2 = float((((D @ H) * D).sum(1)).double().sum()) * nseq / 2
+        assert r2 > 0 and r2 == r2
+        recon[method] = recon.get(method, 0.0) + r2
     Wq = W.to(W16.dtype).contiguous()
     codes, lut, sal, ex = _k().pack(Wq, masks)               # raises on a structure violation
     n_ex = int(ex.idx.numel())
@@ -113,12 +120,22 @@ def test_cfg1_opt13b_layer_crb_and_braq():
     print(f"  layer error crb {errs['crb']:.5g} braq {errs['braq']:.5g}", flush=True)
 
 
-def test_cfg3_opt66b_fc2_max_shape():
-    print("cfg3 OPT-66B fc2 (C = 36864)", flush=True)
-    H = _hessian(_acts(36864, 7))
-    W = (torch.randn(9216, 36864, generator=torch.Generator(device=DEV).manual_seed(3),
-                     device=DEV) * 0.02).half()
-    _quantize_check("fc2", W, H, "crb")
+def test_cfg3_opt66b_layer_max_shape():
+    """every sublayer of an OPT-66B-shaped layer, fc2's input
+    giving the 36864^2 Hessian and fc1 a 36864-row block loop."""
+    print("cfg3 OPT-66B layer (fc2 C = 36864, fc1 36864 rows)", flush=True)
+    subs = synth.opt_sublayers("opt-66b")
+    groups = {}
+    for j, (name, r, c, grp) in enumerate(subs):
+        if grp not in groups:
+            X = _acts(c, 7 + j)
+            groups[grp] = _hessian(X)
+            del X
+            torch.cuda.empty_cache()
+    for j, (name, r, c, grp) in enumerate(subs):
+        W = (torch.randn(r, c, generator=torch.Generator(device=DEV).manual_seed(3 + j),
+                         device=DEV) * 0.02).half()
+        _quantize_check(name, W, groups[grp], "crb")
 
 
 def test_cfg4_llama3_8b_layer_bf16():
@@ -128,12 +145,16 @@ def test_cfg4_llama3_8b_layer_bf16():
     for j, (name, r, c, grp) in enumerate(subs):
         if grp not in groups:
             groups[grp] = _hessian(_acts(c, 200 + j))
-    errs = {}
+    errs, recon = {}, {}
     for method, it in (("crb", 5), ("crbog", 1)):
         tot = 0.0
         for j, (name, r, c, grp) in enumerate(subs):
             W = synth.weight(r, c, 300 + j, outlier_frac=0.01, outlier_scale=10.0,
                              dtype=torch.bfloat16, device=DEV)
-            tot += _quantize_check(name, W, groups[grp], method, refine_iters=it)
+            tot += _quantize_check(name, W, groups[grp], method, refine_iters=it, recon=recon)
         errs[method] = tot
-    print(f"  layer error crb(refine 5) {errs['crb']:.5g} crbog {errs['crbog']:.5g}", flush=True)
+    print(f"  layer GPTQ loss crb(refine 5) {errs['crb']:.5g} crbog {errs['crbog']:.5g}",
+          flush=True)
+    print(f"  layer reconstruction error ||(W - Q) X^T||_F: crb(refine 5) "
+          f"{recon['crb'] ** 0.5:.5g} crbog {recon['crbog'] ** 0.5:.5g} "
+          f"(ratio {(recon['crb'] / recon['crbog']) ** 0.5:.4f})", flush=True)
