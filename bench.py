@@ -478,8 +478,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=128 * 2048)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-packed", action="store_true", help="skip the packed GEMV timing")
-    ap.add_argument("--stack-layers", type=int, default=3,
-                    help="layers of the OPT-6.7B-shaped stack run (0: skip)")
+    ap.add_argument("--stack-layers", type=int, default=32,
+                    help="layers of the OPT-6.7B-shaped stack run (0: skip); the default "
+                         "is the whole 32-layer stack of BASELINE configs[2]")
     ap.add_argument("--fc2-last", action="store_true",
                     help="accumulate the fc2 input's Hessian last (forward order)")
     ap.add_argument("--no-kernels", action="store_true",
