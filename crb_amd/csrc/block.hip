@@ -29,6 +29,7 @@
 //
 // T = W^2 / diag(U_blk)^2 (hessian metric) or W (magnitude) is recomputed
 // from W on every pass instead of being stored.
+#include <atomic>
 #include <mutex>
 
 #include "binarize.h"
@@ -1338,14 +1339,18 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
 }
 
 // c_q lives in every device's copy of the code object, so "uploaded" is
-// tracked per device (the current device of the call).
+// tracked per device (the current device of the call).  Host threads may
+// call concurrently: the flags are atomics and the upload is serialized.
 constexpr int MAXDEV = 64;
-static bool q_table_ready[MAXDEV] = {};
+static std::atomic<bool> q_table_ready[MAXDEV] = {};
+static std::mutex g_q_mu;
 static int ensure_q_table() {
   int dev = 0;
   CRBQ_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= MAXDEV) return CRBQ_ERR_ARG;
-  if (q_table_ready[dev]) return CRBQ_OK;
+  if (q_table_ready[dev].load(std::memory_order_acquire)) return CRBQ_OK;
+  std::lock_guard<std::mutex> g(g_q_mu);
+  if (q_table_ready[dev].load(std::memory_order_relaxed)) return CRBQ_OK;
   // torch.linspace(0.10, 0.90, 81) (float32, CPU): start + i*step for the
   // first half, end - (steps-1-i)*step for the second, step in float32.
   float q[NQ];
@@ -1355,7 +1360,7 @@ static int ensure_q_table() {
   for (int i = 0; i < NQ; ++i)
     q[i] = i < half ? start + step * (float)i : end - step * (float)(NQ - 1 - i);
   CRBQ_HIP(hipMemcpyToSymbol(HIP_SYMBOL(c_q), q, sizeof(q)));
-  q_table_ready[dev] = true;
+  q_table_ready[dev].store(true, std::memory_order_release);
   return CRBQ_OK;
 }
 
@@ -1363,8 +1368,9 @@ int set_q_table(const float* q) {
   int dev = 0;
   CRBQ_HIP(hipGetDevice(&dev));
   if (dev < 0 || dev >= MAXDEV) return CRBQ_ERR_ARG;
+  std::lock_guard<std::mutex> g(g_q_mu);
   CRBQ_HIP(hipMemcpyToSymbol(HIP_SYMBOL(c_q), q, NQ * sizeof(float)));
-  q_table_ready[dev] = true;
+  q_table_ready[dev].store(true, std::memory_order_release);
   return CRBQ_OK;
 }
 

@@ -18,6 +18,7 @@
 //    with v_perm_b32 before one 8-byte LDS store per channel.
 #include <stdlib.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -622,17 +623,19 @@ __global__ __launch_bounds__(256) void k_finalize(const float* S, int64_t lds, i
 }  // namespace crbq
 
 namespace crbq {
+// CUs of the current device, per device (thread-safe: one query each)
 static int num_cus() {
-  static int cus = 0;
-  if (!cus) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-      cus = v;
-    else
-      cus = 256;
-  }
-  return cus;
+  constexpr int MAXDEV = 64;
+  static std::atomic<int> cus[MAXDEV] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) return 256;
+  int v = cus[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      v <= 0)
+    v = 256;
+  cus[dev].store(v, std::memory_order_relaxed);
+  return v;
 }
 
 // Split count for the 16-bit kernel: minimise the modelled time of
