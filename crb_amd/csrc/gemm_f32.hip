@@ -124,6 +124,137 @@ __device__ __forceinline__ void gemm_tile(int id, int nwg, int TM, int TN, int t
   tn = lin % TN;
 }
 
+// K loop of an interior 128 x 128 tile (A not transposed) as one asm block.
+// Left to the compiler, each 4-deep k-step's fragment reads were issued two
+// MFMAs before their first use, so every step waited out the LDS latency
+// (~0.8 of the matrix units busy); and once the accumulators are asm
+// operands, any asm statement inside a compiler-visible loop makes the
+// register allocator carry them in VGPRs and copy them in and out of the
+// AGPRs around it.  So the whole loop is one block with a fixed schedule:
+//  * chunk c (32 deep) runs from LDS buffer c & 1: 8 k-steps of 4, each
+//    waiting for the fragments the previous step read and issuing its 16
+//    MFMAs (v_mfma_f32_16x16x4_f32, 4 x 4 tiles of 16 x 16) with the 8
+//    ds_read_b32 of the next step between the first 8 of them (two
+//    fragment sets in alternation);
+//  * at its start the 8 buffer loads of chunk c + 1 (4 float4 per operand
+//    and thread) go into staging registers; after 5 k-steps they are
+//    written to the other buffer (its last reader, chunk c - 1, finished
+//    before the previous barrier) between MFMAs;
+//  * the chunk ends with one barrier, then the next chunk's first reads.
+// Past the last chunk the loads run beyond kend; the buffer descriptors'
+// record counts end at the operands' last elements, so those loads return
+// zeros or in-range elements, and their LDS copy is never read.
+// A is [m][k] in LDS (pitch P_MK = 36), B [k][n] (pitch BT + 16 = 144) when
+// BK, else [n][k] (pitch 36); a buffer is 4608 floats.  ab / bb: this lane's
+// byte address of A[wm + lane % 16][lane / 16] and of B's first fragment in
+// buffer 0; wa / wb: the byte address of this thread's first float4 of the
+// staged tile (float4 e at + 4608 e bytes).
+#define SG_BUF "18432"
+#define SG_MF(i, j, s)                                                                    \
+  "v_mfma_f32_16x16x4_f32 %[c" #i #j "], %[f" #s "a" #i "], %[f" #s "b" #j "], %[c" #i #j "]\n"
+#define SG_RA(s, i, kk, b)                                                                \
+  "ds_read_b32 %[f" #s "a" #i "], %[ab] offset:((" #i ")*576+(" #kk "))*4+(" #b ")*" SG_BUF "\n"
+#define SG_RBK(s, j, kk, b)                                                               \
+  "ds_read_b32 %[f" #s "b" #j "], %[bb] offset:((" #kk ")*144+(" #j ")*16)*4+(" #b ")*" SG_BUF "\n"
+#define SG_RBN(s, j, kk, b)                                                               \
+  "ds_read_b32 %[f" #s "b" #j "], %[bb] offset:((" #j ")*576+(" #kk "))*4+(" #b ")*" SG_BUF "\n"
+#define SG_WA(e, w) "ds_write_b128 %[wa], %[r" #e "] offset:" #e "*4608+(" #w ")*" SG_BUF "\n"
+#define SG_WB(e, w) "ds_write_b128 %[wb], %[r" #e "b] offset:" #e "*4608+(" #w ")*" SG_BUF "\n"
+#define SG_ROW(i, s) SG_MF(i, 0, s) SG_MF(i, 1, s) SG_MF(i, 2, s) SG_MF(i, 3, s)
+// 8 MFMAs (rows 0, 1 of set s) with the reads of step nk (buffer b) into set n
+#define SG_HR(s, n, nk, RB, b)                                                            \
+  SG_MF(0, 0, s) SG_RA(n, 0, nk, b) SG_MF(0, 1, s) SG_RA(n, 1, nk, b) SG_MF(0, 2, s)     \
+  SG_RA(n, 2, nk, b) SG_MF(0, 3, s) SG_RA(n, 3, nk, b) SG_MF(1, 0, s) RB(n, 0, nk, b)    \
+  SG_MF(1, 1, s) RB(n, 1, nk, b) SG_MF(1, 2, s) RB(n, 2, nk, b) SG_MF(1, 3, s)           \
+  RB(n, 3, nk, b)
+#define SG_STEP(s, n, nk, RB, b)                                                          \
+  "s_waitcnt lgkmcnt(0)\n" SG_HR(s, n, nk, RB, b) SG_ROW(2, s) SG_ROW(3, s)
+// the same with the staged chunk written to buffer w between rows 2 and 3
+#define SG_STEPW(s, n, nk, RB, b, w)                                                      \
+  "s_waitcnt lgkmcnt(0)\n" SG_HR(s, n, nk, RB, b)                                        \
+  SG_MF(2, 0, s) SG_WA(0, w) SG_MF(2, 1, s) SG_WA(1, w) SG_MF(2, 2, s) SG_WA(2, w)       \
+  SG_MF(2, 3, s) SG_WA(3, w) SG_MF(3, 0, s) SG_WB(0, w) SG_MF(3, 1, s) SG_WB(1, w)       \
+  SG_MF(3, 2, s) SG_WB(2, w) SG_MF(3, 3, s) SG_WB(3, w)
+#define SG_FIRST(RB, b)                                                                   \
+  SG_RA(0, 0, 0, b) SG_RA(0, 1, 0, b) SG_RA(0, 2, 0, b) SG_RA(0, 3, 0, b)                \
+  RB(0, 0, 0, b) RB(0, 1, 0, b) RB(0, 2, 0, b) RB(0, 3, 0, b)
+#define SG_LOADS                                                                          \
+  "buffer_load_dwordx4 %[r0], %[va], %[rsa], %[sa0] offen\n"                             \
+  "buffer_load_dwordx4 %[r1], %[va], %[rsa], %[sa1] offen\n"                             \
+  "buffer_load_dwordx4 %[r2], %[va], %[rsa], %[sa2] offen\n"                             \
+  "buffer_load_dwordx4 %[r3], %[va], %[rsa], %[sa3] offen\n"                             \
+  "buffer_load_dwordx4 %[r0b], %[vb], %[rsb], %[sb0] offen\n"                            \
+  "buffer_load_dwordx4 %[r1b], %[vb], %[rsb], %[sb1] offen\n"                            \
+  "buffer_load_dwordx4 %[r2b], %[vb], %[rsb], %[sb2] offen\n"                            \
+  "buffer_load_dwordx4 %[r3b], %[vb], %[rsb], %[sb3] offen\n"                            \
+  "v_add_u32 %[va], %[ka], %[va]\n"                                                      \
+  "v_add_u32 %[vb], %[kb], %[vb]\n"
+// chunk from buffer b, staging the next one into buffer w
+#define SG_CHUNK(RB, b, w)                                                                \
+  SG_LOADS                                                                               \
+  SG_STEP(0, 1, 4, RB, b) SG_STEP(1, 0, 8, RB, b) SG_STEP(0, 1, 12, RB, b)               \
+  SG_STEP(1, 0, 16, RB, b) "s_waitcnt vmcnt(0)\n" SG_STEPW(0, 1, 20, RB, b, w)           \
+  SG_STEP(1, 0, 24, RB, b) SG_STEP(0, 1, 28, RB, b)                                      \
+  "s_waitcnt lgkmcnt(0)\n" SG_ROW(0, 1) SG_ROW(1, 1) SG_ROW(2, 1) SG_ROW(3, 1)          \
+  "s_barrier\n"                                                                          \
+  "s_add_u32 %[cnt], %[cnt], 1\n"                                                        \
+  "s_cmp_ge_u32 %[cnt], %[n]\n"                                                          \
+  "s_cbranch_scc1 .Lsgend%=\n"                                                           \
+  SG_FIRST(RB, w)
+#define SG_LOOP(RB)                                                                       \
+  "s_mov_b32 %[cnt], 0\n" SG_FIRST(RB, 0)                                                \
+  ".Lsgloop%=:\n" SG_CHUNK(RB, 0, 1) SG_CHUNK(RB, 1, 0) "s_branch .Lsgloop%=\n"          \
+  ".Lsgend%=:\n"                                                                         \
+  "s_waitcnt vmcnt(0) lgkmcnt(0)\n"                                                      \
+  "s_nop 7\ns_nop 7\ns_nop 7\n"
+#define SG_OPERANDS                                                                       \
+  : [c00] "+{a[0:3]}"(acc[0][0]), [c01] "+{a[4:7]}"(acc[0][1]),                          \
+    [c02] "+{a[8:11]}"(acc[0][2]), [c03] "+{a[12:15]}"(acc[0][3]),                       \
+    [c10] "+{a[16:19]}"(acc[1][0]), [c11] "+{a[20:23]}"(acc[1][1]),                      \
+    [c12] "+{a[24:27]}"(acc[1][2]), [c13] "+{a[28:31]}"(acc[1][3]),                      \
+    [c20] "+{a[32:35]}"(acc[2][0]), [c21] "+{a[36:39]}"(acc[2][1]),                      \
+    [c22] "+{a[40:43]}"(acc[2][2]), [c23] "+{a[44:47]}"(acc[2][3]),                      \
+    [c30] "+{a[48:51]}"(acc[3][0]), [c31] "+{a[52:55]}"(acc[3][1]),                      \
+    [c32] "+{a[56:59]}"(acc[3][2]), [c33] "+{a[60:63]}"(acc[3][3]),                      \
+    [f0a0] "=&v"(t[0]), [f0a1] "=&v"(t[1]), [f0a2] "=&v"(t[2]), [f0a3] "=&v"(t[3]),      \
+    [f0b0] "=&v"(t[4]), [f0b1] "=&v"(t[5]), [f0b2] "=&v"(t[6]), [f0b3] "=&v"(t[7]),      \
+    [f1a0] "=&v"(t[8]), [f1a1] "=&v"(t[9]), [f1a2] "=&v"(t[10]), [f1a3] "=&v"(t[11]),    \
+    [f1b0] "=&v"(t[12]), [f1b1] "=&v"(t[13]), [f1b2] "=&v"(t[14]), [f1b3] "=&v"(t[15]),  \
+    [r0] "=&v"(r[0]), [r1] "=&v"(r[1]), [r2] "=&v"(r[2]), [r3] "=&v"(r[3]),              \
+    [r0b] "=&v"(r[4]), [r1b] "=&v"(r[5]), [r2b] "=&v"(r[6]), [r3b] "=&v"(r[7]),          \
+    [cnt] "=&s"(cnt), [va] "+v"(va), [vb] "+v"(vb)                                       \
+  : [ab] "v"(ab), [bb] "v"(bb), [wa] "v"(wa), [wb] "v"(wb), [rsa] "s"(rsa),              \
+    [rsb] "s"(rsb), [sa0] "s"(sa[0]), [sa1] "s"(sa[1]), [sa2] "s"(sa[2]),                \
+    [sa3] "s"(sa[3]), [sb0] "s"(sb[0]), [sb1] "s"(sb[1]), [sb2] "s"(sb[2]),              \
+    [sb3] "s"(sb[3]), [ka] "s"(ka), [kb] "s"(kb), [n] "s"(n)                             \
+  : "memory", "scc"
+
+typedef int sg_i4_t __attribute__((ext_vector_type(4)));
+// Raw buffer descriptor: 48-bit base, stride 0, nrec bytes.
+__device__ __forceinline__ sg_i4_t sg_rsrc(const float* base, unsigned nrec) {
+  const uint64_t a = (uint64_t)base;
+  return sg_i4_t{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                 __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffff)),
+                 __builtin_amdgcn_readfirstlane((int)nrec), 0x00020000};
+}
+
+// The K loop over n chunks (chunk 0 already in LDS buffer 0).
+template <bool BK>
+__device__ __forceinline__ void sg_loop128(f4_t (&acc)[4][4], unsigned ab, unsigned bb,
+                                           unsigned wa, unsigned wb, sg_i4_t rsa, sg_i4_t rsb,
+                                           int va, int vb, const int (&sa)[4],
+                                           const int (&sb)[4], int ka, int kb, int n) {
+  float t[16];
+  f4_t r[8];
+  int cnt;
+  if constexpr (BK) asm volatile(SG_LOOP(SG_RBK) SG_OPERANDS);
+  else asm volatile(SG_LOOP(SG_RBN) SG_OPERANDS);
+}
+
+__device__ __forceinline__ unsigned lds_addr(const float* p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 template <int BT, bool TA, bool TB, bool LOWER>
 __global__ __launch_bounds__(256) void k_sgemm(
     int M, int N, int K, float alpha, const float* A, int64_t lda,
@@ -166,7 +297,46 @@ __global__ __launch_bounds__(256) void k_sgemm(
     store_tile<BT, BK>(Bs[0], rb);
   }
   __syncthreads();
-  for (int c = 0; c < nch; ++c) {
+  bool done = false;
+  if constexpr (BT == 128 && !AK) {
+    // the asm K loop: interior tiles whose chunks are all full, with every
+    // byte offset of both operand regions below 2^31
+    const int64_t ea = ((int64_t)(M - m0) * lda + K) * 4;
+    const int64_t eb = BK ? ((int64_t)(K - kbeg + 2 * GB_K) * ldb + N) * 4
+                          : ((int64_t)(N - n0) * ldb + K) * 4;
+    if (nch > 0 && nfull == nch && ea < ((int64_t)1 << 31) && eb < ((int64_t)1 << 31)) {
+      static_assert(P_MK == 36 && P_KM == 144 && Cfg::ELEMS == 4608, "offsets in the asm");
+      const unsigned ab = lds_addr(As[0]) + (unsigned)(((wm + c16) * P_MK + kq) * 4);
+      const unsigned bb = lds_addr(Bs[0]) + (unsigned)((BK ? kq * P_KM + wn + c16
+                                                           : (wn + c16) * P_MK + kq) * 4);
+      const unsigned wa = lds_addr(As[0]) + (unsigned)(((tid >> 3) * P_MK + (tid & 7) * 4) * 4);
+      const unsigned wb = lds_addr(Bs[0]) + (unsigned)((BK ? (tid >> 5) * P_KM + (tid & 31) * 4
+                                                           : (tid >> 3) * P_MK + (tid & 7) * 4) * 4);
+      const int la = (int)lda, lb = (int)ldb;
+      const sg_i4_t rsa = sg_rsrc(A + (int64_t)m0 * lda + kbeg,
+                                  (unsigned)(((int64_t)(M - m0 - 1) * lda + (K - kbeg)) * 4));
+      const sg_i4_t rsb =
+          BK ? sg_rsrc(B + (int64_t)kbeg * ldb + n0,
+                       (unsigned)(((int64_t)(K - kbeg - 1) * ldb + (N - n0)) * 4))
+             : sg_rsrc(B + (int64_t)n0 * ldb + kbeg,
+                       (unsigned)(((int64_t)(N - n0 - 1) * ldb + (K - kbeg)) * 4));
+      // chunk 1's offsets (chunk 0 is in LDS); float4 e of a thread at + s[e]
+      const int va0 = ((tid >> 3) * la + (tid & 7) * 4) * 4 + GB_K * 4;
+      const int vb0 = BK ? ((tid >> 5) * lb + (tid & 31) * 4) * 4 + GB_K * lb * 4
+                         : ((tid >> 3) * lb + (tid & 7) * 4) * 4 + GB_K * 4;
+      int sa[4], sb[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sa[e] = __builtin_amdgcn_readfirstlane(e * 32 * la * 4);
+        sb[e] = __builtin_amdgcn_readfirstlane(BK ? e * 8 * lb * 4 : e * 32 * lb * 4);
+      }
+      const int ka = GB_K * 4;
+      const int kb = __builtin_amdgcn_readfirstlane(BK ? GB_K * lb * 4 : GB_K * 4);
+      sg_loop128<BK>(acc, ab, bb, wa, wb, rsa, rsb, va0, vb0, sa, sb, ka, kb, nch);
+      done = true;
+    }
+  }
+  for (int c = 0; !done && c < nch; ++c) {
     const int buf = c & 1;
     if (c + 1 < nfull) {
       load_tile_in<BT, AK>(A, lda, m0, kbeg + (c + 1) * GB_K, ra);
