@@ -118,17 +118,6 @@ __global__ __launch_bounds__(256) void k_reverse_lower(const float* __restrict__
   reverse_row<true>(H, ldh, C, A, lda, vec != 0);
 }
 
-// Y[r][c] = X[r][c] for an M x N block (row strides ldx, ldy)
-__global__ __launch_bounds__(256) void k_copy2d(const float* __restrict__ X, int64_t ldx, int M,
-                                                int N, float* Y, int64_t ldy,
-                                                const int* __restrict__ stop) {
-  if (*stop) return;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int r = (int)(idx / N), c = (int)(idx % N);
-  if (r >= M) return;
-  Y[(int64_t)r * ldy + c] = X[(int64_t)r * ldx + c];
-}
-
 // U[i][j] = X[C-1-i][C-1-j] for j >= i, 0 below the diagonal (rows_grid)
 __global__ __launch_bounds__(256) void k_reverse_to_u(const float* __restrict__ X, int64_t ldx,
                                                       int C, float* U, int64_t ldu, int vec) {
@@ -479,6 +468,7 @@ static inline unsigned nblocks(int64_t n) { return (unsigned)((n + 255) / 256); 
 struct HinvWs {
   float* A;        // C x C (ld = C)
   float* T;        // panel of the recursion: half x half (ld = half)
+  float* Q;        // A21 X11 of every node on the current recursion path (q_floats)
   int* info;
   float* scal;
   uint8_t* dead;   // C
@@ -490,19 +480,30 @@ static inline int split_rows(int n) {
   return (nblk + 1) / 2 * NB;
 }
 
+// Floats of Q an n-row node needs: its own n2 x m product, held while the
+// X22 recursion runs, stacked on what that recursion needs (the X11
+// recursion runs before it and reuses the same space).
+static int64_t q_floats(int64_t n) {
+  if (n <= NB) return 0;
+  const int64_t m = split_rows((int)n), n2 = n - m;
+  return std::max(q_floats(m), n2 * m + q_floats(n2));
+}
+
 static void carve_hinv(WsCarver& c, int64_t C, HinvWs& w) {
   const int64_t h = C > NB ? split_rows((int)C) : 0;
   w.A = c.take<float>((size_t)C * C);
   w.T = c.take<float>((size_t)std::max<int64_t>(h * h, 1));
+  w.Q = c.take<float>((size_t)std::max<int64_t>(q_floats(C), 1));
   w.info = c.take<int>(4);
   w.scal = c.take<float>(4);
   w.dead = c.take<uint8_t>((size_t)C);
 }
 
 // X = L^-1 of the n x n diagonal block at offset o of A (lda), in place.
-// The factorization outcome is in *w.info; after a failure every later
-// kernel returns at once.
-static int chol_inv_rec(float* A, int64_t lda, int o, int n, HinvWs& w, hipStream_t s) {
+// Q: q_floats(n) floats of scratch.  The factorization outcome is in
+// *w.info; after a failure every later kernel returns at once.
+static int chol_inv_rec(float* A, int64_t lda, int o, int n, HinvWs& w, float* Q,
+                        hipStream_t s) {
   if (n <= NB) {
     k_chol_inv_diag<<<1, 256, 0, s>>>(A, lda, o, n, w.info);
     CRBQ_LAUNCH_CHECK();
@@ -513,7 +514,7 @@ static int chol_inv_rec(float* A, int64_t lda, int o, int n, HinvWs& w, hipStrea
   float* A21 = A11 + (int64_t)m * lda;
   float* A22 = A21 + m;
   const int* stop = w.info;
-  int st = chol_inv_rec(A, lda, o, m, w, s);
+  int st = chol_inv_rec(A, lda, o, m, w, Q, s);
   if (st) return st;
   // T = A21 X11^T
   st = sgemm_launch(false, true, false, n2, m, m, 1.f, A21, lda, A11, lda, 0.f, w.T, m, stop, s,
@@ -522,25 +523,21 @@ static int chol_inv_rec(float* A, int64_t lda, int o, int n, HinvWs& w, hipStrea
   // A22 -= T T^T (lower tiles)
   st = sgemm_launch(false, true, true, n2, n2, m, -1.f, w.T, m, w.T, m, 1.f, A22, lda, stop, s);
   if (st) return st;
-  // A21 = T X11
-  st = sgemm_launch(false, false, false, n2, m, m, 1.f, w.T, m, A11, lda, 0.f, A21, lda, stop, s,
+  // Q = T X11 (A21 is dead after T; X21 will go there)
+  st = sgemm_launch(false, false, false, n2, m, m, 1.f, w.T, m, A11, lda, 0.f, Q, m, stop, s,
                     GEMM_TRI_KBEG_N);
   if (st) return st;
-  st = chol_inv_rec(A, lda, o + m, n2, w, s);
+  st = chol_inv_rec(A, lda, o + m, n2, w, Q + (int64_t)n2 * m, s);
   if (st) return st;
-  // X21 = -X22 A21, through T
-  st = sgemm_launch(false, false, false, n2, m, n2, -1.f, A22, lda, A21, lda, 0.f, w.T, m, stop,
-                    s, GEMM_TRI_KEND_M);
-  if (st) return st;
-  k_copy2d<<<nblocks((int64_t)n2 * m), 256, 0, s>>>(w.T, m, n2, m, A21, lda, stop);
-  CRBQ_LAUNCH_CHECK();
-  return CRBQ_OK;
+  // X21 = -X22 Q
+  return sgemm_launch(false, false, false, n2, m, n2, -1.f, A22, lda, Q, m, 0.f, A21, lda, stop,
+                      s, GEMM_TRI_KEND_M);
 }
 
 // One full attempt: factor and invert A in place.  Returns a launch status;
 // the factorization outcome is in *w.info.
 static int chol_inv_sweep(float* A, int64_t lda, int C, HinvWs& w, hipStream_t s) {
-  return chol_inv_rec(A, lda, 0, C, w, s);
+  return chol_inv_rec(A, lda, 0, C, w, w.Q, s);
 }
 
 }  // namespace crbq
