@@ -50,6 +50,29 @@ def test_sgemm(ta, tb, M, N, K):
     assert rel(Cd, want) < 1e-5
 
 
+@pytest.mark.parametrize("tb", [False, True])
+@pytest.mark.parametrize("M,N,K,pad", [(2100, 2052, 160, 0), (2100, 2052, 170, 0),
+                                       (2048, 2176, 96, 12), (1920, 2304, 1024, 4)])
+def test_sgemm_large_tiles(tb, M, N, K, pad):
+    """Products with >= 256 tiles of 128 x 128: interior tiles whose chunks
+    are all full run the asm K loop, edge tiles and ragged K the compiled
+    one; both against float64, on row strides padded by `pad` floats."""
+    print(f"sgemm large tb={tb} M={M} N={N} K={K} pad={pad}", flush=True)
+    g = torch.Generator().manual_seed(M + N + K + pad)
+    Af = torch.randn(M, K + pad, generator=g)
+    Bf = torch.randn(N, K + pad, generator=g) if tb else torch.randn(K, N + pad, generator=g)
+    C = torch.randn(M, N, generator=g)
+    A, B = Af[:, :K], (Bf[:, :K] if tb else Bf[:, :N])
+    want = 0.75 * C.double() + (-1.5) * (A.double() @ (B.double().t() if tb else B.double()))
+    Cd = C.to(DEV)
+    # slices of device tensors keep the padded row strides
+    Ad = Af.to(DEV)[:, :K]
+    Bd = Bf.to(DEV)[:, :K] if tb else Bf.to(DEV)[:, :N]
+    _k().sgemm(Ad, Bd, Cd, alpha=-1.5, beta=0.75, transb=tb)
+    torch.cuda.synchronize()
+    assert rel(Cd, want) < 1e-6
+
+
 def test_sgemm_trailing_update_shape():
     """W[:, ed:] -= Err @ U[st:ed, ed:] on strided views (bigptq.py:264)."""
     print("sgemm trailing", flush=True)
