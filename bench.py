@@ -342,6 +342,30 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
     out["block_loop_fc1_alone_ms"] = round(_ev_ms(loop1, 2), 3)
     del W1, U1, Wq
     torch.cuda.empty_cache()
+    # inverse factor alone (crbq_hinv_upper: damping, Cholesky-inverse of the
+    # index-reversed H, U) on a well-conditioned H of the fc2 input's size and
+    # of the other inputs'; 2C^3/3 flop against the fp32 MFMA peak.  H is
+    # refreshed before each call (the call damps it in place); that copy is
+    # timed on its own and subtracted.  The calls are enqueued back to back
+    # (hinv_upper_async); the last one's status is checked afterwards.
+    out["inverse_factor"] = {}
+    for Cf in (C, C // 4):
+        Xf = torch.randn(2 * Cf, Cf, device=dev, generator=g)
+        H0 = (Xf.t() @ Xf) / (2 * Cf)
+        del Xf
+        H = torch.empty_like(H0)
+        jobs = []
+        ms_copy = _ev_ms(lambda: H.copy_(H0), 3)
+        ms = _ev_ms(lambda: jobs.append(kernels.hinv_upper_async(H.copy_(H0), None)), 3) - ms_copy
+        _, retries, fallback = kernels.hinv_upper_finish(jobs[-1])
+        fl = 2.0 * Cf ** 3 / 3
+        out["inverse_factor"][f"C{Cf}"] = {
+            "kernels": "k_chol_inv_diag + k_sgemm (recursive Cholesky-inverse)",
+            "ms": round(ms, 3), "achieved": round(fl / ms / 1e9, 1), "peak": PEAK_F32 / 1e12,
+            "unit": "TFLOP/s", "frac": round(fl / ms / 1e9 / (PEAK_F32 / 1e12), 3),
+            "retries": retries, "fallback": fallback}
+        del H, H0, jobs
+        torch.cuda.empty_cache()
     return out
 
 
