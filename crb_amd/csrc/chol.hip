@@ -178,10 +178,12 @@ __device__ __forceinline__ f4_t mfma4(float a, float b, f4_t c) {
 // Value of lane L of each 16-lane row in every lane of that row (DPP
 // row_newbcast).  In the leaves the four rows of a wavefront hold the same
 // data, so this is lane L's value in VGPRs, with no scalar registers.
+// bound_ctrl set: every lane's source lane is valid, so the old value is
+// never read and no zero needs to be moved into the destination first.
 template <int L>
 __device__ __forceinline__ float row_bcast(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xf, 0xf,
-                                                    false));
+                                                    true));
 }
 __device__ __forceinline__ float row_bcast(float v, int l) {   // l is a constant after unrolling
   switch (l) {
@@ -193,6 +195,51 @@ __device__ __forceinline__ float row_bcast(float v, int l) {   // l is a constan
     case 10: return row_bcast<10>(v); case 11: return row_bcast<11>(v);
     case 12: return row_bcast<12>(v); case 13: return row_bcast<13>(v);
     case 14: return row_bcast<14>(v); default: return row_bcast<15>(v);
+  }
+}
+
+// d - (lane L of s's row) * m as one v_fmac_f32 whose first source is the
+// row broadcast (DPP row_newbcast, negated): the same fma as
+// fmaf(-row_bcast<L>(s), m, d), one instruction instead of two.  A DPP
+// read of a VGPR needs two wait states after the VALU instruction that
+// wrote it, and the compiler's hazard recognizer does not look inside asm:
+// NB puts them before the instruction (s was just written), NA after it (a
+// compiler-generated DPP read of d follows).
+// The wait states sit in the same asm statement as the DPP instruction, so
+// the scheduler cannot move the write in between.
+#define CRBQ_FMAC_BCAST "v_fmac_f32_dpp %0, -%1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf bound_ctrl:1"
+template <int L, bool NB, bool NA>
+__device__ __forceinline__ float fnma_row_bcast(float d, float s, float m) {
+  if (NB && NA)
+    asm volatile("s_nop 1\n\t" CRBQ_FMAC_BCAST "\n\ts_nop 1" : "+v"(d) : "v"(s), "v"(m), "n"(L));
+  else if (NB)
+    asm volatile("s_nop 1\n\t" CRBQ_FMAC_BCAST : "+v"(d) : "v"(s), "v"(m), "n"(L));
+  else if (NA)
+    asm volatile(CRBQ_FMAC_BCAST "\n\ts_nop 1" : "+v"(d) : "v"(s), "v"(m), "n"(L));
+  else
+    asm volatile(CRBQ_FMAC_BCAST : "+v"(d) : "v"(s), "v"(m), "n"(L));
+  return d;
+}
+#undef CRBQ_FMAC_BCAST
+template <bool NB, bool NA>
+__device__ __forceinline__ float fnma_row_bcast(float d, float s, float m, int l) {
+  switch (l) {   // l is a constant after unrolling
+    case 0: return fnma_row_bcast<0, NB, NA>(d, s, m);
+    case 1: return fnma_row_bcast<1, NB, NA>(d, s, m);
+    case 2: return fnma_row_bcast<2, NB, NA>(d, s, m);
+    case 3: return fnma_row_bcast<3, NB, NA>(d, s, m);
+    case 4: return fnma_row_bcast<4, NB, NA>(d, s, m);
+    case 5: return fnma_row_bcast<5, NB, NA>(d, s, m);
+    case 6: return fnma_row_bcast<6, NB, NA>(d, s, m);
+    case 7: return fnma_row_bcast<7, NB, NA>(d, s, m);
+    case 8: return fnma_row_bcast<8, NB, NA>(d, s, m);
+    case 9: return fnma_row_bcast<9, NB, NA>(d, s, m);
+    case 10: return fnma_row_bcast<10, NB, NA>(d, s, m);
+    case 11: return fnma_row_bcast<11, NB, NA>(d, s, m);
+    case 12: return fnma_row_bcast<12, NB, NA>(d, s, m);
+    case 13: return fnma_row_bcast<13, NB, NA>(d, s, m);
+    case 14: return fnma_row_bcast<14, NB, NA>(d, s, m);
+    default: return fnma_row_bcast<15, NB, NA>(d, s, m);
   }
 }
 
@@ -210,18 +257,27 @@ __device__ __forceinline__ void leaf16(DiagSmem& sm, int o, int lane, int off, i
   float a[16], rdg[16];
 #pragma unroll
   for (int c = 0; c < 16; ++c) a[c] = sm.Ls[o + i][o + c];
-  int badl = 16;   // first bad pivot (the same in every lane)
+  unsigned badm = 0u;   // bad pivots as bits (the same in every lane)
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const float piv = row_bcast(a[j], j);
-    badl = (!(piv > 0.f) && o + j < bj && badl == 16) ? j : badl;
+    badm |= (!(piv > 0.f) && o + j < bj) ? (1u << j) : 0u;
     const float rd = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(piv));
     rdg[j] = rd;
     a[j] *= rd;
+    // a[k] -= L[i][j] L[k][j]; the first update reads a[j] right after its
+    // scaling, and the next column's pivot reads a[j + 1] (written by the
+    // first update) at most two updates later
 #pragma unroll
-    for (int k = j + 1; k < 16; ++k) a[k] = fmaf(-a[j], row_bcast(a[j], k), a[k]);
+    for (int k = j + 1; k < 16; ++k) {
+      if (k == j + 1 && k == 15) a[k] = fnma_row_bcast<true, true>(a[k], a[j], a[j], k);
+      else if (k == j + 1) a[k] = fnma_row_bcast<true, false>(a[k], a[j], a[j], k);
+      else if (k == 15) a[k] = fnma_row_bcast<false, true>(a[k], a[j], a[j], k);
+      else a[k] = fnma_row_bcast<false, false>(a[k], a[j], a[j], k);
+    }
   }
-  const int bad = __builtin_amdgcn_readfirstlane(badl);
+  const unsigned bm = __builtin_amdgcn_readfirstlane(badm);
+  const int bad = bm ? __builtin_ctz(bm) : 16;   // first bad pivot
   if (bad < 16 && lane == 0) {
     sm.fail = 1;
     atomicCAS(info, 0, off + o + bad + 1);
@@ -231,7 +287,7 @@ __device__ __forceinline__ void leaf16(DiagSmem& sm, int o, int lane, int off, i
   for (int r = 0; r < 16; ++r) {
     float acc = i == r ? 1.f : 0.f;
 #pragma unroll
-    for (int k = 0; k < r; ++k) acc = fmaf(-row_bcast(a[k], r), y[k], acc);
+    for (int k = 0; k < r; ++k) acc = fnma_row_bcast<false, false>(acc, a[k], y[k], r);
     y[r] = acc * rdg[r];
   }
   if (lane < 16) {
