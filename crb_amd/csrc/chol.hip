@@ -282,13 +282,18 @@ __device__ __forceinline__ void leaf16(DiagSmem& sm, int o, int lane, int off, i
     sm.fail = 1;
     atomicCAS(info, 0, off + o + bad + 1);
   }
-  float y[16];
+  // right-looking: once y[r] is known every later row's accumulator takes
+  // its term, so each accumulator receives k = 0, 1, ... in the same order
+  // as a row-by-row dot product would, while the dependent chain is one
+  // multiply and one fma per row
+  float y[16], acc[16];
+#pragma unroll
+  for (int s = 0; s < 16; ++s) acc[s] = i == s ? 1.f : 0.f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    float acc = i == r ? 1.f : 0.f;
+    y[r] = acc[r] * rdg[r];
 #pragma unroll
-    for (int k = 0; k < r; ++k) acc = fnma_row_bcast<false, false>(acc, a[k], y[k], r);
-    y[r] = acc * rdg[r];
+    for (int s = r + 1; s < 16; ++s) acc[s] = fnma_row_bcast<false, false>(acc[s], a[r], y[r], s);
   }
   if (lane < 16) {
 #pragma unroll
