@@ -12,7 +12,8 @@
 //   X11 = chol_inv(A11)                     (L11^-1, recursively)
 //   T   = A21 X11^T                         (= L21, the panel of L')
 //   A22 = A22 - T T^T      (lower tiles)    (Schur complement)
-//   A21 = T X11                             (= L21 L11^-1)
+//   A21 = T X11                             (= L21 L11^-1; one launch with
+//                                            the Schur update)
 //   X22 = chol_inv(A22)                     (recursively)
 //   X21 = -X22 A21
 // so X = [X11 0; X21 X22] = L'^-1 overwrites A.  Blocks of NB or fewer
@@ -146,9 +147,9 @@ __global__ __launch_bounds__(256) void k_fallback_u(const float* __restrict__ H,
 // recursively like the whole matrix (X11, T = A21 X11^T, A22 -= T T^T,
 // A21 = T X11, X22, X21 = -X22 A21):
 //  * 16 x 16 leaves: one wavefront, lane i & 15 holding row i in
-//    registers; Cholesky by columns and the inverse by forward
-//    substitution over rows, the values other lanes need broadcast with
-//    readlane.
+//    registers; Cholesky by columns and the inverse by right-looking
+//    forward substitution, the values other lanes hold taken by DPP row
+//    broadcasts fused into the fma (v_fmac_f32_dpp).
 //  * 32 x 32 blocks: one wavefront runs both leaves and the four 16 x 16
 //    products (v_mfma_f32_16x16x4f32), so no workgroup barrier is needed.
 //  * the 64 and 128 levels: the products' 16 x 16 output tiles are spread
@@ -581,13 +582,16 @@ static int chol_inv_rec(float* A, int64_t lda, int o, int n, HinvWs& w, float* Q
   st = sgemm_launch(false, true, false, n2, m, m, 1.f, A21, lda, A11, lda, 0.f, w.T, m, stop, s,
                     GEMM_TRI_KEND_N);
   if (st) return st;
-  // A22 -= T T^T (lower tiles)
-  st = sgemm_launch(false, true, true, n2, n2, m, -1.f, w.T, m, w.T, m, 1.f, A22, lda, stop, s);
-  if (st) return st;
-  // Q = T X11 (A21 is dead after T; X21 will go there)
-  st = sgemm_launch(false, false, false, n2, m, m, 1.f, w.T, m, A11, lda, 0.f, Q, m, stop, s,
-                    GEMM_TRI_KBEG_N);
-  if (st) return st;
+  // A22 -= T T^T (lower tiles) and Q = T X11 (A21 is dead after T; X21
+  // will go there), in one launch: both only read T and X11
+  {
+    const GemmArgs schur = {false, true, true, n2, n2, m, -1.f, w.T, m, w.T, m, 1.f, A22, lda,
+                            GEMM_TRI_NONE};
+    const GemmArgs q = {false, false, false, n2, m, m, 1.f, w.T, m, A11, lda, 0.f, Q, m,
+                        GEMM_TRI_KBEG_N};
+    st = sgemm2_launch(schur, q, stop, s);
+    if (st) return st;
+  }
   st = chol_inv_rec(A, lda, o + m, n2, w, Q + (int64_t)n2 * m, s);
   if (st) return st;
   // X21 = -X22 Q

@@ -15,4 +15,24 @@ int sgemm_launch(bool ta, bool tb, bool lower, int64_t M, int64_t N, int64_t K,
                  float alpha, const float* A, int64_t lda, const float* B,
                  int64_t ldb, float beta, float* C, int64_t ldc,
                  const int* stop, hipStream_t s, int tri = GEMM_TRI_NONE);
+
+// One product for sgemm2_launch.
+struct GemmArgs {
+  bool ta, tb, lower;
+  int64_t M, N, K;
+  float alpha;
+  const float* A;
+  int64_t lda;
+  const float* B;
+  int64_t ldb;
+  float beta;
+  float* C;
+  int64_t ldc;
+  int tri;
+};
+// Two independent products (neither writes what the other reads): x a
+// lower-tile product op(A) B^T with M == N, y a plain op(A) B (triangular K
+// allowed).  One launch when both pick the same tile size, with x's tiles
+// first; otherwise the two launches of sgemm_launch in order.
+int sgemm2_launch(const GemmArgs& x, const GemmArgs& y, const int* stop, hipStream_t s);
 }  // namespace crbq

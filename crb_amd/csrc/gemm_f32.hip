@@ -255,16 +255,18 @@ __device__ __forceinline__ unsigned lds_addr(const float* p) {
   return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// One BT x BT output tile (number bid of the product's nwg tiles) of
+// C = beta C + alpha op(A) op(B), staged through the LDS buffers As, Bs.
 template <int BT, bool TA, bool TB, bool LOWER>
-__global__ __launch_bounds__(256) void k_sgemm(
+__device__ __forceinline__ void sgemm_tile(
     int M, int N, int K, float alpha, const float* A, int64_t lda,
     const float* B, int64_t ldb, float beta, float* C,
-    int64_t ldc, const int* __restrict__ stop, int va, int vb, int tri) {
+    int64_t ldc, int va, int vb, int tri, float (*As)[TileCfg<BT>::ELEMS],
+    float (*Bs)[TileCfg<BT>::ELEMS], int bid, int nwg) {
   using Cfg = TileCfg<BT>;
   constexpr int P_KM = Cfg::P_KM, WT = Cfg::WT, MT = Cfg::MT, NE = Cfg::NE;
-  if (stop && *stop) return;
   int tm, tn;
-  gemm_tile(blockIdx.x, gridDim.x, (M + BT - 1) / BT, (N + BT - 1) / BT, tri, LOWER, tm, tn);
+  gemm_tile(bid, nwg, (M + BT - 1) / BT, (N + BT - 1) / BT, tri, LOWER, tm, tn);
   const int m0 = tm * BT, n0 = tn * BT;
   // K range of this tile when one operand is triangular (its zero part is
   // skipped; the products skipped are exact zeros)
@@ -272,8 +274,6 @@ __global__ __launch_bounds__(256) void k_sgemm(
   if (tri == GEMM_TRI_KEND_N) kend = min(K, n0 + BT);
   else if (tri == GEMM_TRI_KBEG_N) kbeg = min(K, n0) / GB_K * GB_K;
   else if (tri == GEMM_TRI_KEND_M) kend = min(K, m0 + BT);
-  __shared__ __attribute__((aligned(16))) float As[2][Cfg::ELEMS];
-  __shared__ __attribute__((aligned(16))) float Bs[2][Cfg::ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = (wave >> 1) * WT, wn = (wave & 1) * WT;
   const int c16 = lane & 15, kq = lane >> 4;
@@ -391,6 +391,51 @@ __global__ __launch_bounds__(256) void k_sgemm(
       }
 }
 
+// operands of one product (the arguments of sgemm_tile)
+struct SgP {
+  int M, N, K;
+  float alpha, beta;
+  const float* A;
+  const float* B;
+  float* C;
+  int64_t lda, ldb, ldc;
+  int va, vb, tri;
+};
+
+template <int BT, bool TA, bool TB, bool LOWER>
+__device__ __forceinline__ void sgemm_tile(const SgP& p, float (*As)[TileCfg<BT>::ELEMS],
+                                           float (*Bs)[TileCfg<BT>::ELEMS], int bid, int nwg) {
+  sgemm_tile<BT, TA, TB, LOWER>(p.M, p.N, p.K, p.alpha, p.A, p.lda, p.B, p.ldb, p.beta, p.C,
+                                p.ldc, p.va, p.vb, p.tri, As, Bs, bid, nwg);
+}
+
+template <int BT, bool TA, bool TB, bool LOWER>
+__global__ __launch_bounds__(256) void k_sgemm(SgP p, const int* __restrict__ stop) {
+  if (stop && *stop) return;
+  __shared__ __attribute__((aligned(16))) float As[2][TileCfg<BT>::ELEMS];
+  __shared__ __attribute__((aligned(16))) float Bs[2][TileCfg<BT>::ELEMS];
+  sgemm_tile<BT, TA, TB, LOWER>(p, As, Bs, blockIdx.x, gridDim.x);
+}
+
+// Two independent products in one grid: workgroups [0, n1) compute p1's
+// tiles, the others p2's, in one set of LDS buffers.  The factorization's
+// Schur update A22 -= T T^T (p1, full K on every tile) and Q = T X11 (p2,
+// tiles in decreasing K) both only read T; launched together, the Schur
+// update's last round of tiles shares the CUs with the start of the other
+// product instead of running alone, and one launch of the dependent chain
+// goes away.
+template <int BT, bool TA1, bool TB1, bool LO1, bool TA2, bool TB2, bool LO2>
+__global__ __launch_bounds__(256) void k_sgemm2(SgP p1, int n1, SgP p2,
+                                                const int* __restrict__ stop) {
+  if (stop && *stop) return;
+  __shared__ __attribute__((aligned(16))) float As[2][TileCfg<BT>::ELEMS];
+  __shared__ __attribute__((aligned(16))) float Bs[2][TileCfg<BT>::ELEMS];
+  if ((int)blockIdx.x < n1)
+    sgemm_tile<BT, TA1, TB1, LO1>(p1, As, Bs, blockIdx.x, n1);
+  else
+    sgemm_tile<BT, TA2, TB2, LO2>(p2, As, Bs, (int)blockIdx.x - n1, (int)gridDim.x - n1);
+}
+
 static inline bool vec_ok(const float* p, int64_t ld) {
   return ((((uintptr_t)p) & 15) == 0) && ((ld & 3) == 0);
 }
@@ -406,14 +451,17 @@ static int sgemm_go(bool ta, bool tb, bool lower, int64_t M, int64_t N, int64_t 
   const int64_t nwg = lower ? TM * (TM + 1) / 2 : TM * TN;
   if (nwg > 0x7fffffff) return CRBQ_ERR_ARG;
   const dim3 grid((unsigned)nwg);
-  const int m = (int)M, n = (int)N, k = (int)K;
-  const int va = vec_ok(A, lda), vb = vec_ok(B, ldb);
-#define CRBQ_GEMM_CASE(TA_, TB_, LO_)                                                  \
-  if (ta == TA_ && tb == TB_ && lower == LO_) {                                        \
-    k_sgemm<BT, TA_, TB_, LO_><<<grid, 256, 0, s>>>(m, n, k, alpha, A, lda, B, ldb,    \
-                                                    beta, C, ldc, stop, va, vb, tri);  \
-    CRBQ_LAUNCH_CHECK();                                                               \
-    return CRBQ_OK;                                                                    \
+  SgP p;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  p.alpha = alpha; p.beta = beta;
+  p.A = A; p.B = B; p.C = C;
+  p.lda = lda; p.ldb = ldb; p.ldc = ldc;
+  p.va = vec_ok(A, lda); p.vb = vec_ok(B, ldb); p.tri = tri;
+#define CRBQ_GEMM_CASE(TA_, TB_, LO_)                                 \
+  if (ta == TA_ && tb == TB_ && lower == LO_) {                       \
+    k_sgemm<BT, TA_, TB_, LO_><<<grid, 256, 0, s>>>(p, stop);         \
+    CRBQ_LAUNCH_CHECK();                                              \
+    return CRBQ_OK;                                                   \
   }
   CRBQ_GEMM_CASE(false, false, false)
   CRBQ_GEMM_CASE(false, true, false)
@@ -432,22 +480,69 @@ static int sgemm_go(bool ta, bool tb, bool lower, int64_t M, int64_t N, int64_t 
 // latency chains of one or two rounds of workgroups, which smaller tiles
 // shorten (factor at C = 16384: 33.2 -> 31.4 ms; the sums are unchanged,
 // since every tile size adds the k-steps of an element in the same order).
+static int tile_of(int64_t M, int64_t N) {
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  const int64_t t64 = ((M + 63) / 64) * ((N + 63) / 64);
+  return t64 < 512 ? 32 : t128 < 512 ? 64 : 128;
+}
+
 int sgemm_launch(bool ta, bool tb, bool lower, int64_t M, int64_t N, int64_t K,
                  float alpha, const float* A, int64_t lda, const float* B,
                  int64_t ldb, float beta, float* C, int64_t ldc,
                  const int* stop, hipStream_t s, int tri) {
   if (M <= 0 || N <= 0) return CRBQ_OK;
   if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30) || K < 0) return CRBQ_ERR_ARG;
-  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
-  const int64_t t64 = ((M + 63) / 64) * ((N + 63) / 64);
-  if (t64 < 512)
+  const int bt = tile_of(M, N);
+  if (bt == 32)
     return sgemm_go<32>(ta, tb, lower, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stop, s,
                         tri);
-  if (t128 < 512)
+  if (bt == 64)
     return sgemm_go<64>(ta, tb, lower, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stop, s,
                         tri);
   return sgemm_go<128>(ta, tb, lower, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stop, s,
                        tri);
+}
+
+static SgP sg_params(const GemmArgs& g) {
+  SgP p;
+  p.M = (int)g.M; p.N = (int)g.N; p.K = (int)g.K;
+  p.alpha = g.alpha; p.beta = g.beta;
+  p.A = g.A; p.B = g.B; p.C = g.C;
+  p.lda = g.lda; p.ldb = g.ldb; p.ldc = g.ldc;
+  p.va = vec_ok(g.A, g.lda); p.vb = vec_ok(g.B, g.ldb); p.tri = g.tri;
+  return p;
+}
+
+template <int BT>
+static int sgemm2_go(const GemmArgs& x, const GemmArgs& y, const int* stop, hipStream_t s) {
+  const int64_t TX = (x.M + BT - 1) / BT;
+  const int64_t n1 = TX * (TX + 1) / 2;
+  const int64_t n2 = ((y.M + BT - 1) / BT) * ((y.N + BT - 1) / BT);
+  if (n1 + n2 > 0x7fffffff) return CRBQ_ERR_ARG;
+  k_sgemm2<BT, false, true, true, false, false, false>
+      <<<(unsigned)(n1 + n2), 256, 0, s>>>(sg_params(x), (int)n1, sg_params(y), stop);
+  CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}
+
+int sgemm2_launch(const GemmArgs& x, const GemmArgs& y, const int* stop, hipStream_t s) {
+  const auto one = [&](const GemmArgs& g) {
+    return sgemm_launch(g.ta, g.tb, g.lower, g.M, g.N, g.K, g.alpha, g.A, g.lda, g.B, g.ldb,
+                        g.beta, g.C, g.ldc, stop, s, g.tri);
+  };
+  const bool pair = !x.ta && x.tb && x.lower && x.M == x.N && x.tri == GEMM_TRI_NONE &&
+                    !y.ta && !y.tb && !y.lower;
+  const bool sizes = x.M > 0 && x.N > 0 && y.M > 0 && y.N > 0 && x.K >= 0 && y.K >= 0 &&
+                     x.M <= (1 << 30) && x.K <= (1 << 30) && y.M <= (1 << 30) &&
+                     y.N <= (1 << 30) && y.K <= (1 << 30);
+  const int bt = sizes ? tile_of(x.M, x.N) : 0;
+  if (!pair || !sizes || bt != tile_of(y.M, y.N)) {
+    const int st = one(x);
+    return st ? st : one(y);
+  }
+  if (bt == 32) return sgemm2_go<32>(x, y, stop, s);
+  if (bt == 64) return sgemm2_go<64>(x, y, stop, s);
+  return sgemm2_go<128>(x, y, stop, s);
 }
 
 }  // namespace crbq
