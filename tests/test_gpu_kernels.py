@@ -282,6 +282,27 @@ def test_hinv_upper_matches_oracle(C):
     assert float((Ud.t() @ Ud @ Hdamp - torch.eye(C, dtype=torch.float64)).abs().max()) < 1e-3
 
 
+@pytest.mark.parametrize("C", [1000, 2900])
+def test_hinv_upper_ragged_levels(C):
+    """Sizes whose recursion splits unevenly at several levels (node halves of
+    different sizes, so the one-launch Schur update + Q product pairs grids of
+    different shapes or falls back to two launches): U against the fp64
+    Cholesky factor of the damped inverse (bigptq.py:111-129) and the
+    U^T U (H + damp I) = I invariant."""
+    print(f"hinv ragged C={C}", flush=True)
+    H = _spd(C, C + 7).float()
+    U, retries, fb = _k().hinv_upper(H.to(DEV), None, 0.01)
+    torch.cuda.synchronize()
+    assert retries == 0 and not fb
+    Hdamp = H.double() + 0.01 * torch.diag(H.double()).mean() * torch.eye(C, dtype=torch.float64)
+    Uref = torch.linalg.cholesky(torch.linalg.inv(Hdamp), upper=True)
+    Uc = U.cpu()
+    assert torch.equal(torch.tril(Uc, -1), torch.zeros(C, C))
+    assert rel(Uc, Uref.float()) < 1e-4
+    Ud = Uc.double()
+    assert float((Ud.t() @ Ud @ Hdamp - torch.eye(C, dtype=torch.float64)).abs().max()) < 1e-3
+
+
 def test_hinv_dead_columns():
     print("hinv dead", flush=True)
     C = 160
