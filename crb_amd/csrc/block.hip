@@ -1149,23 +1149,23 @@ __device__ __forceinline__ void row_abs(const float* x, int c0, int c1, float m1
 }
 
 // Residual moments over x[c0, c1) of a group with parameters g.  Each
-// element takes s1 = m1 + (x > m1 ? a1 : -a1), the reference's
-// sign(x - m1) * a1 + m1 (binary.py:26, 32-34; the product is exact, so
-// the add rounds as the reference's does) except where x == m1, whose sign
-// is 0 and s1 = m1.  Those n0 elements (known from the sign counts) all
-// contributed the same e0 = fl(fl(m1 - lo) - m2) here, and their sums are
-// moved to the reference's e = -m2 afterwards, so the loop carries no zero
-// test.  e^2 is accumulated with fma.
+// element takes s1 = x > m1 ? hi : lo with hi = fl(a1 + m1), lo =
+// fl(-a1 + m1): the reference's sign(x - m1) * a1 + m1 (binary.py:26,
+// 32-34; the product is exact, so the add rounds as the reference's does)
+// except where x == m1, whose sign is 0 and s1 = m1.  Those n0 elements
+// (known from the sign counts) all contributed the same e0 = fl(fl(m1 -
+// lo) - m2) here, and their sums are moved to the reference's e = -m2
+// afterwards, so the loop carries no zero test.  e^2 is accumulated with
+// fma.
 __device__ __forceinline__ void row_res(const float* x, int c0, int c1, const ParA& g, int n0,
                                         RowRes& r) {
-  const float na1 = -g.a1;
   int c = c0;
   for (; c + 8 <= c1; c += 8) {
     float p1 = 0.f, p2 = 0.f;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const float v = x[c + u];
-      const float s1 = g.m1 + (v > g.m1 ? g.a1 : na1);
+      const float s1 = v > g.m1 ? g.hi : g.lo;
       const float e = (v - s1) - g.m2;
       p1 += fabsf(e);
       p2 = __builtin_fmaf(e, e, p2);
@@ -1177,7 +1177,7 @@ __device__ __forceinline__ void row_res(const float* x, int c0, int c1, const Pa
   float p1 = 0.f, p2 = 0.f;
   for (; c < c1; ++c) {
     const float v = x[c];
-    const float s1 = g.m1 + (v > g.m1 ? g.a1 : na1);
+    const float s1 = v > g.m1 ? g.hi : g.lo;
     const float e = (v - s1) - g.m2;
     p1 += fabsf(e);
     p2 = __builtin_fmaf(e, e, p2);
