@@ -42,9 +42,12 @@ __device__ __forceinline__ float clamp0(float x) { return x < 0.f ? 0.f : x; }
 // v_j, lane j adds v_i, with all lanes of the partner group already equal),
 // and a swap level returns (lower-group value, upper-group value) in the
 // same order to both lanes of a pair.
+// bound_ctrl set: a lane whose source lies outside its row (row_shl /
+// row_shr) reads 0, the same value the old operand 0 gave it, and no zero
+// has to be moved into the destination first.
 template <int CTRL>
 __device__ __forceinline__ unsigned dpp_u32(unsigned v) {
-  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
 }
 constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
 
