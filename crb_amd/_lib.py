@@ -54,6 +54,7 @@ class CrbqBlockTrace(ctypes.Structure):
 TRACE_BYTES = ctypes.sizeof(CrbqBlockTrace)
 NOALLOC_SCRATCH_BYTES = 80 << 20      # CRBQ_NOALLOC_SCRATCH_BYTES (include/crbq.h)
 ERR_TOO_LARGE = -5                    # CRBQ_ERR_TOO_LARGE
+ERR_CAPTURE = -6                      # CRBQ_ERR_CAPTURE
 
 _SIGS = {
     "crbq_version": (c_i32, []),
@@ -86,6 +87,9 @@ _SIGS = {
                                   c_i64, c_vp, c_vp, c_size, c_vp]),
     "crbq_binarize": (c_i32, [c_vp, c_i64, c_i32, c_i64, c_vp, c_i64, c_i32, c_i32,
                               ctypes.c_float, ctypes.c_float, c_i32, c_vp, c_i64, c_vp]),
+    "crbq_binarize_scales": (c_i32, [c_vp, c_i64, c_i32, c_i64, c_vp, c_i64, c_i32, c_i32,
+                                     ctypes.c_float, ctypes.c_float, c_i32, c_vp, c_i64, c_vp,
+                                     c_i64, c_vp]),
     "crbq_sgemm": (c_i32, [c_i32, c_i32, c_i64, c_i64, c_i64, ctypes.c_float, c_vp, c_i64,
                            c_vp, c_i64, ctypes.c_float, c_vp, c_i64, c_vp]),
     "crbq_pack": (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp,

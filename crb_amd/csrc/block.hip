@@ -155,7 +155,13 @@ __device__ __forceinline__ double pload(const double* p) {
 
 __device__ __forceinline__ bool last_block(uint32_t* cnt) {
   __shared__ bool last;
+  // The waitcnt builtin is no memory access, so a compiler barrier keeps
+  // every partial store of this thread ahead of it; the hardware then waits
+  // until those stores are acknowledged (vmcnt counts them: they are vector
+  // memory stores), i.e. written through to the coherence point.
+  asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this thread's stores acknowledged
+  asm volatile("" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev = atomicAdd(cnt, 1u);
@@ -1565,6 +1571,14 @@ static __device__ __align__(256) unsigned char scratch[CRBQ_NOALLOC_SCRATCH_BYTE
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[MAXDEV] = {};
 
+static bool noalloc_ready_on_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) return false;
+  if (!q_table_ready[dev].load(std::memory_order_acquire)) return false;
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  return g_scratch_ptr[dev] != nullptr;
+}
+
 static int scratch_of_current_device(void** out) {
   int dev = 0;
   CRBQ_HIP(hipGetDevice(&dev));
@@ -1598,6 +1612,15 @@ extern "C" int crbq_fasterquant_noalloc(float* W, int64_t R, int64_t C, int64_t 
   if (R <= 0 || C <= 0) return CRBQ_ERR_ARG;
   if (crbq_fasterquant_workspace_size(R, C, p) > CRBQ_NOALLOC_SCRATCH_BYTES)
     return CRBQ_ERR_TOO_LARGE;
+  {
+    // The per-device set-up (the percentile table's copy to the device and
+    // the scratch address query) happens on a device's first call and
+    // cannot be recorded into a graph: under capture it must already be done.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    CRBQ_HIP(hipStreamIsCapturing((hipStream_t)stream, &cs));
+    if (cs != hipStreamCaptureStatusNone && !crbq::noalloc_ready_on_current_device())
+      return CRBQ_ERR_CAPTURE;
+  }
   void* ws = nullptr;
   const int sst = crbq::scratch_of_current_device(&ws);
   if (sst) return sst;
@@ -1633,6 +1656,41 @@ __global__ __launch_bounds__(256) void k_binarize(const float* x, int R, int nc,
     if (c < nc) out[(int64_t)row * ldo + c] = o[e];
   }
 }
+// The same with the row's scales written to scales[row * lds ..] by lane 0
+// (a check of the per-row scales, so one wavefront per row and no
+// tuning: rows of up to 64 * EPL columns).
+template <int MF, int EPL>
+__global__ __launch_bounds__(256) void k_binarize_scales(const float* x, int R, int nc,
+                                                         int64_t ldx,
+                                                         const uint8_t* __restrict__ mask,
+                                                         int64_t ldm, int order, int method,
+                                                         CrbConsts k, float* out, int64_t ldo,
+                                                         float* scales, int64_t lds, int nsc) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= R) return;
+  float v[EPL], o[EPL];
+  bool m[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int c = lane + 64 * e;
+    const bool ok = c < nc;
+    v[e] = ok ? x[(int64_t)row * ldx + c] : 0.f;
+    m[e] = ok && mask[(int64_t)row * ldm + c] != 0;
+  }
+  float sc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) sc[i] = 0.f;
+  binarize_row<MF, EPL>(method, v, m, order, k, o, sc);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int c = lane + 64 * e;
+    if (c < nc) out[(int64_t)row * ldo + c] = o[e];
+  }
+  if (lane == 0)
+    for (int i = 0; i < nsc; ++i) scales[(int64_t)row * lds + i] = sc[i];
+}
+
 // Rows of at most EPL * LPR columns, LPR lanes per row (256 / LPR rows per
 // workgroup), EPL elements per lane: lane r of a row holds columns
 // h * 4 LPR + 4r .. h * 4 LPR + 4r + 3 for h < EPL / 4, moved with 16-byte
@@ -1736,6 +1794,48 @@ extern "C" int crbq_binarize(const float* x, int64_t R, int32_t ncols, int64_t l
   else if (mf == MF_CRBOG) CRBQ_BIN_GO(MF_CRBOG);
   else CRBQ_BIN_GO(MF_CRB);
 #undef CRBQ_BIN_GO
+  CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}
+
+extern "C" int crbq_binarize_scales(const float* x, int64_t R, int32_t ncols, int64_t ldx,
+                                    const uint8_t* mask, int64_t ldm, int32_t order,
+                                    int32_t method, float lam, float corr_damp,
+                                    int32_t refine_iters, float* out, int64_t ldo,
+                                    float* scales, int64_t lds, void* stream) {
+  if (!x || !mask || !out || !scales || R <= 0 || ncols <= 0 || ncols > 1024)
+    return CRBQ_ERR_ARG;
+  if (order < 1 || order > 8 || refine_iters < 0 || refine_iters > 64) return CRBQ_ERR_ARG;
+  if (method < CRBQ_BRAQ || method > CRBQ_CRB_SYMDAMP_NOREFINE) return CRBQ_ERR_ARG;
+  if (R > (int64_t)4 * 65535 * 1024) return CRBQ_ERR_ARG;
+  const int mf = method_family(method);
+  const bool passes = mf == MF_BRAQ || (mf == MF_CRBOG && order == 1);
+  const int nsc = passes ? 2 * order : 4;
+  if (lds < nsc) return CRBQ_ERR_ARG;
+  CrbConsts k;
+  k.lam = lam;
+  k.omg = (float)(1.0 - (double)corr_damp);
+  k.sym = false;
+  k.skip = false;
+  k.iters = refine_iters;
+  hipStream_t hs = (hipStream_t)stream;
+  const unsigned g4 = (unsigned)cdiv(R, 4);
+  const int r = (int)R;
+#define CRBQ_BSC_GO(MF_, EPL_)                                                               \
+  k_binarize_scales<MF_, EPL_><<<g4, 256, 0, hs>>>(x, r, ncols, ldx, mask, ldm, order, method, \
+                                                   k, out, ldo, scales, lds, nsc)
+#define CRBQ_BSC_MF(MF_)                                          \
+  do {                                                            \
+    if (ncols <= 128) CRBQ_BSC_GO(MF_, 2);                        \
+    else if (ncols <= 256) CRBQ_BSC_GO(MF_, 4);                   \
+    else if (ncols <= 512) CRBQ_BSC_GO(MF_, 8);                   \
+    else CRBQ_BSC_GO(MF_, 16);                                    \
+  } while (0)
+  if (mf == MF_BRAQ) CRBQ_BSC_MF(MF_BRAQ);
+  else if (mf == MF_CRBOG) CRBQ_BSC_MF(MF_CRBOG);
+  else CRBQ_BSC_MF(MF_CRB);
+#undef CRBQ_BSC_MF
+#undef CRBQ_BSC_GO
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }

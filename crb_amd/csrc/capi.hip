@@ -14,6 +14,9 @@ extern "C" const char* crbq_status_string(int status) {
     case CRBQ_ERR_TOPK: return "selected index k out of range (block narrower than up_lim)";
     case CRBQ_ERR_TOO_LARGE:
       return "problem larger than the allocation-free entry point's static scratch";
+    case CRBQ_ERR_CAPTURE:
+      return "first call on this device made under stream capture (make one call outside "
+             "capture first)";
     default: return "unknown status";
   }
 }

@@ -41,6 +41,9 @@ extern "C" {
                                     (torch.topk k out of range, utils/autosearch.py:42) */
 #define CRBQ_ERR_TOO_LARGE  -5   /* problem needs more scratch than the
                                     allocation-free entry point holds */
+#define CRBQ_ERR_CAPTURE    -6   /* allocation-free entry point first called on a
+                                    device while its stream is capturing: its
+                                    one-time set-up copies cannot be captured */
 
 /* ---- enums -------------------------------------------------------------- */
 enum crbq_dtype  { CRBQ_F32 = 0, CRBQ_F16 = 1, CRBQ_BF16 = 2 };
@@ -201,6 +204,24 @@ int crbq_binarize(const float* x, int64_t R, int32_t ncols, int64_t ldx,
                   const uint8_t* mask, int64_t ldm, int32_t order,
                   int32_t method, float lam, float corr_damp,
                   int32_t refine_iters, float* out, int64_t ldo, void* stream);
+/* crbq_binarize that also writes each row's scales to scales[row * lds ..]
+ * (fp32; a row of the reference's per-row tensors):
+ *   CRB variants (binary.py:1544-1638), and CRBOG at order >= 2
+ *   (binary.py:635-687): (mean, mu correction, a1, a2), 4 values: the row
+ *   mean (:1599; CRBOG :653), the mean correction of step 7 (:1633-1635;
+ *   0 for CRBOG), the two plane scales after the last solve (:1582-1596,
+ *   1615-1630; CRBOG :656-679); order 1 gives (mean, 0, a1, 0)
+ *   (:1570-1576);
+ *   BRAQ (binary.py:18-39), and CRBOG at order 1 (:595-630): (mu_k, alpha_k)
+ *   for each residual pass k < order, 2 * order values.
+ * lds must hold them (>= 4, >= 2 * order for BRAQ).  Rows are processed
+ * one wavefront each; the values written to out are those of crbq_binarize
+ * up to summation order. */
+int crbq_binarize_scales(const float* x, int64_t R, int32_t ncols, int64_t ldx,
+                         const uint8_t* mask, int64_t ldm, int32_t order,
+                         int32_t method, float lam, float corr_damp,
+                         int32_t refine_iters, float* out, int64_t ldo,
+                         float* scales, int64_t lds, void* stream);
 /* C = beta*C + alpha*op(A)*op(B), fp32 on MFMA (the trailing update uses
  * alpha = -1, beta = 1, bigptq.py:264).  transa/transb: op(X) = X^T. */
 int crbq_sgemm(int transa, int transb, int64_t M, int64_t N, int64_t K,

@@ -51,12 +51,15 @@ def test_sgemm(ta, tb, M, N, K):
 
 
 @pytest.mark.parametrize("tb", [False, True])
-@pytest.mark.parametrize("M,N,K,pad", [(2100, 2052, 160, 0), (2100, 2052, 170, 0),
-                                       (2048, 2176, 96, 12), (1920, 2304, 1024, 4)])
+@pytest.mark.parametrize("M,N,K,pad", [(3000, 2900, 160, 0), (3000, 2900, 170, 0),
+                                       (3072, 2816, 96, 12), (2816, 3072, 1024, 4),
+                                       (2990, 3001, 77, 3)])
 def test_sgemm_large_tiles(tb, M, N, K, pad):
-    """Products with >= 256 tiles of 128 x 128: interior tiles whose chunks
-    are all full run the asm K loop, edge tiles and ragged K the compiled
-    one; both against float64, on row strides padded by `pad` floats."""
+    """Products with >= 512 tiles of 128 x 128 (the size from which the
+    128 x 128 tiles are used; 552 / 528 / 552 tiles here): interior tiles
+    whose chunks are all full run the hand-scheduled asm K loop, edge tiles
+    (ragged M and N) and ragged K the compiled one; both B layouts, against
+    float64, on row strides padded by `pad` floats."""
     print(f"sgemm large tb={tb} M={M} N={N} K={K} pad={pad}", flush=True)
     g = torch.Generator().manual_seed(M + N + K + pad)
     Af = torch.randn(M, K + pad, generator=g)
@@ -301,6 +304,35 @@ def test_hinv_upper_ragged_levels(C):
     assert rel(Uc, Uref.float()) < 1e-4
     Ud = Uc.double()
     assert float((Ud.t() @ Ud @ Hdamp - torch.eye(C, dtype=torch.float64)).abs().max()) < 1e-3
+
+
+@pytest.mark.parametrize("C", [8192, 8320])
+def test_hinv_upper_large_vs_fp64(C):
+    """Factors whose top-level products have >= 512 tiles of 128 x 128, so
+    the triangular-K products (k ranges that skip zero halves) run on the
+    asm K loop: U against the fp64 upper Cholesky factor of the damped
+    inverse, and its backward error U^-1 U^-T = H_d, both in float64 on the
+    GPU.  H = X^T X / T from 2C tokens with log-normal channel scales."""
+    print(f"hinv large C={C}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(C)
+    s = torch.exp(0.5 * torch.randn(C, generator=g, device=DEV, dtype=torch.float64))
+    X = torch.randn(2 * C, C, generator=g, device=DEV, dtype=torch.float64) * s
+    H64 = (X.t() @ X) / (2 * C)
+    del X
+    U, retries, fb = _k().hinv_upper(H64.float(), None, 0.01)
+    torch.cuda.synchronize()
+    assert retries == 0 and not fb
+    Hd = H64.float().double()
+    Hd += 0.01 * torch.diag(Hd).mean() * torch.eye(C, dtype=torch.float64, device=DEV)
+    Uref = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(Hd)), upper=True)
+    assert torch.equal(torch.tril(U, -1), torch.zeros_like(U))
+    r = float((U.double() - Uref).norm() / Uref.norm())
+    I = torch.eye(C, dtype=torch.float64, device=DEV)
+    Ui = torch.linalg.solve_triangular(U.double(), I, upper=True)
+    back = float((Ui @ Ui.t() - Hd).norm() / Hd.norm())
+    print(f"  U rel {r:.2e}, backward {back:.2e}", flush=True)
+    assert r < 1e-4, r
+    assert back < 1e-5, back
 
 
 def test_hinv_dead_columns():

@@ -62,3 +62,40 @@ def test_noalloc_rejects_problems_beyond_its_scratch():
     with pytest.raises(_lib.CrbqError, match="static scratch"):
         kernels.fasterquant_blocks_noalloc(W, U, p, L)
     assert torch.count_nonzero(W) == 0                    # nothing ran
+
+
+def test_noalloc_replays_under_graph_capture():
+    """Captured with torch.cuda.graph after one eager call on the device (the
+    per-device set-up, the percentile table and the scratch address, is done
+    on the first call and cannot be captured: a first call under capture
+    returns CRBQ_ERR_CAPTURE), then replayed three times with eager work and
+    synchronizations between the replays: every replay's weights, losses and
+    masks bitwise equal to the eager call's.  The graph holds kernel nodes
+    only (the library clears its counters with a kernel, not a memset)."""
+    from crb_amd import _lib, kernels
+    print("noalloc under graph capture", flush=True)
+    p = _lib.params("crb")
+    R, C = 2048, 640
+    W0, U = _problem(R, C, 5)
+    We, Le = W0.clone(), torch.zeros(R, device=DEV)
+    me = torch.zeros(R, C, dtype=torch.uint8, device=DEV)
+    kernels.fasterquant_blocks_noalloc(We, U, p, Le, me)      # eager: warm-up and reference
+    Wg, Lg = W0.clone(), torch.zeros(R, device=DEV)
+    mg = torch.zeros_like(me)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        kernels.fasterquant_blocks_noalloc(Wg, U, p, Lg, mg)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        Wg.copy_(W0)
+        Lg.zero_()
+        mg.zero_()
+        a = torch.randn(1024, 1024, device=DEV)
+        (a @ a).sum().item()                                  # eager work in between
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"  replay {rep}: weights equal {torch.equal(Wg, We)}", flush=True)
+        assert torch.equal(Wg, We)
+        assert torch.equal(Lg, Le)
+        assert torch.equal(mg, me)
