@@ -416,6 +416,77 @@ def cfg1_run(dev, method="crb"):
     return best, err
 
 
+def cfg2_full(dev, methods=("crb", "braq"), seed=0):
+    """BASELINE configs[1] in full, on the host cores (the oracle) and on the
+    GPU (the layer driver), for crb and braq: one OPT-1.3B-shaped decoder
+    layer (q/k/v/out_proj 2048 x 2048, fc1 8192 x 2048, fc2 2048 x 8192,
+    fp16 W ~ N(0, 0.02^2)) with 128 x 2048 fp16 tokens per distinct input
+    (Student-t(4) channel scales).  The CPU side feeds one sequence per
+    add_batch (run.py's hooks, bigptq.py:37-53) into one Hessian per
+    distinct input, shared by the two methods as on the GPU, then runs
+    fasterquant (bigptq.py:56-291) per sublayer; the GPU side runs the
+    layer driver on the same tensors.  Seconds and summed errors per method
+    (the two Hessians differ by summation order, so the errors agree to
+    rounding unless a block's search choice sits on a near-tie)."""
+    from crb_amd.driver import LayerQuantizer, Sublayer
+    from oracle import crb_oracle as O
+    subs = synth.opt_sublayers("opt-1.3b")
+    Ws = {}
+    for i, (name, r, c, grp) in enumerate(subs):
+        g = torch.Generator(device=dev).manual_seed(seed * 100 + 50 + i)
+        Ws[name] = (torch.randn(r, c, generator=g, device=dev) * 0.02).half()
+    Cg = {grp: c for (_, _, c, grp) in subs}
+    X = {}
+    for j, (grp, C) in enumerate(Cg.items()):
+        sc = synth.channel_scales(C, seed + 20 + j, kind="student_t4", device=dev)
+        g = torch.Generator(device=dev).manual_seed(seed * 1000 + 20 + j)
+        x = torch.empty(128 * 2048, C, dtype=torch.float16, device=dev)
+        for t0 in range(0, x.shape[0], 8192):
+            x[t0:t0 + 8192] = (torch.randn(8192, C, generator=g, device=dev) * sc).half()
+        X[grp] = x
+    out = {"workload": "BASELINE configs[1] in full (OPT-1.3B layer, 128x2048 fp16 tokens, "
+                       "Student-t(4) channels; crb and braq, blocksize 128, hessian metric)"}
+    # GPU: the layer driver, best of 2 per method
+    for m in methods:
+        best, errs = None, None
+        for _ in range(2):
+            torch.cuda.synchronize()
+            t0 = time.time()
+            lq = LayerQuantizer([Sublayer(n, Ws[n].clone(), gg) for (n, _, _, gg) in subs],
+                                method=m)
+            for grp, x in X.items():
+                lq.add_batch(grp, x.view(128, 2048, -1))
+            e = lq.quantize()
+            torch.cuda.synchronize()
+            dt = time.time() - t0
+            best, errs = (dt, e) if best is None or dt < best else (best, errs)
+        out[m] = {"gpu_s": round(best, 4), "gpu_error": round(sum(errs.values()), 6)}
+    # CPU: the oracle
+    Xc = {grp: x.cpu() for grp, x in X.items()}
+    Wc = {n: w.cpu() for n, w in Ws.items()}
+    del X
+    torch.cuda.empty_cache()
+    t0 = time.time()
+    H = {}
+    for grp, x in Xc.items():
+        h, n = torch.zeros(Cg[grp], Cg[grp]), 0
+        for s in range(128):
+            h, n = O.hessian_add_batch(h, n, x[s * 2048:(s + 1) * 2048].float().unsqueeze(0))
+        H[grp] = h
+    t_h = time.time() - t0
+    out["cpu_hessian_s"] = round(t_h, 2)
+    for m in methods:
+        t0 = time.time()
+        err = 0.0
+        for (n, _, _, grp) in subs:
+            err += O.fasterquant(Wc[n], H[grp], method=m)[2]
+        t_q = time.time() - t0
+        out[m].update({"cpu_s": round(t_h + t_q, 2), "cpu_quantize_s": round(t_q, 2),
+                       "cpu_error": round(err, 6)})
+        out[m]["cpu_over_gpu"] = round(out[m]["cpu_s"] / out[m]["gpu_s"], 1)
+    return out
+
+
 def reference_calibration():
     """Oracle / genuine reference time ratio on configs[0], measured in the
     build container (tests/golden/time_reference.py), or None."""
@@ -428,10 +499,11 @@ def reference_calibration():
             "cpu": d["cpu"], "threads": d["threads"]}
 
 
-def cpu_baseline(nseq=32, nblocks=48, cfg1_gpu=None):
+def cpu_baseline(nseq=32, nblocks=48, cfg1_gpu=None, cfg2=None):
     """Time the test-only CPU oracle (torch-CPU restatement of the reference
     path) on a bounded sample of the workload (about 10-20 s on 16 cores)
-    and extrapolate to one OPT-6.7B layer; also configs[0] in full."""
+    and extrapolate to one OPT-6.7B layer; also configs[0] in full, and
+    configs[1] in full when given (cfg2_full, timed before)."""
     from oracle import crb_oracle as O
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
@@ -486,11 +558,52 @@ def cpu_baseline(nseq=32, nblocks=48, cfg1_gpu=None):
                       "cpu_error": cfg1_err,
                       "gpu_s": None if cfg1_gpu is None else round(cfg1_gpu[0], 4),
                       "gpu_error": None if cfg1_gpu is None else cfg1_gpu[1]},
+        "cfg2_full": cfg2,
         "calibration": reference_calibration(),
         "cpu": cpu_model(),
         "blas": torch.__config__.show().split("BLAS_INFO=")[-1].split(",")[0]
         if "BLAS_INFO=" in torch.__config__.show() else "unknown",
     }
+
+
+def syrk_compare(dev, ntok, reps=2):
+    """The fc2 input's Hessian product two ways on the same data, for counter
+    runs that compare them kernel by kernel: crbq_hessian_accum (transpose
+    into the channel-major copy + k_syrk16k over the upper triangle) and
+    hipBLASLt (torch.mm, fp16 in / fp32 accumulate / fp16 out) on the same
+    channel-major operand, the full C x C product.  Each timed with events
+    on the current stream; prints TFLOP/s of the symmetric half T C (C + 1)
+    for ours and of the full 2 T C^2 for the library."""
+    from crb_amd import kernels
+    C = 16384
+    X = make_inputs(dev, ntok)["fc2"]
+    S = torch.zeros(C, C, device=dev)
+    res = {}
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    for r in range(reps):
+        S.zero_()
+        ev[0].record()
+        kernels.hessian_accum(X, S)
+        ev[1].record()
+        torch.cuda.synchronize()
+        res.setdefault("crbq_hessian_accum_ms", []).append(round(ev[0].elapsed_time(ev[1]), 3))
+    del S
+    Xt = X.t().contiguous()
+    del X
+    torch.cuda.empty_cache()
+    for r in range(reps):
+        ev[0].record()
+        P = torch.mm(Xt, Xt.t())
+        ev[1].record()
+        torch.cuda.synchronize()
+        res.setdefault("torch_mm_channel_major_ms", []).append(round(ev[0].elapsed_time(ev[1]),
+                                                                     3))
+        del P
+    t_ours = min(res["crbq_hessian_accum_ms"]) / 1e3
+    t_lib = min(res["torch_mm_channel_major_ms"]) / 1e3
+    res["crbq_TFLOP_s_symmetric"] = round(ntok * C * (C + 1) / t_ours / 1e12, 1)
+    res["torch_mm_TFLOP_s_full"] = round(2 * ntok * C * C / t_lib / 1e12, 1)
+    return res
 
 
 def main():
@@ -515,7 +628,19 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy a 1 GiB buffer 3 times: the known-size copy kernel that "
                          "calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE for the traffic figure")
+    ap.add_argument("--no-cfg2-full", action="store_true",
+                    help="skip configs[1] in full (OPT-1.3B layer, crb and braq, oracle on "
+                         "the host cores and the GPU) in the CPU baseline")
+    ap.add_argument("--syrk-compare", action="store_true",
+                    help="only the fc2 input's Hessian product through the library and "
+                         "through hipBLASLt (torch.mm) on the same channel-major data, for "
+                         "counter runs comparing the two kernels")
     args = ap.parse_args()
+    if args.syrk_compare:
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        print(json.dumps({"syrk_compare": syrk_compare(dev, args.tokens)}))
+        return
     if args.calibrate_copy:
         x = torch.ones(256 * 1024 * 1024, device="cuda")
         y = torch.empty_like(x)
@@ -627,7 +752,12 @@ def main():
         print(f"[bench] packed gemv: {out['packed_gemv']}", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(cfg1_gpu=cfg1_run(dev))
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        cfg2 = None
+        if not args.no_cfg2_full:
+            cfg2 = cfg2_full(dev)
+            print(f"[bench] configs[1] in full: {cfg2}", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(cfg1_gpu=cfg1_run(dev), cfg2=cfg2)
     print(json.dumps(out))
 
 

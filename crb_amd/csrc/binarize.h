@@ -88,9 +88,10 @@ __device__ __forceinline__ float rcount(const bool (&m)[EPL]) {
 }
 
 // high_order_residual, binary.py:18-39.
+// scales (optional): (mu_k, alpha_k) of each pass k at scales[2k], [2k+1].
 template <int EPL, int LPR = 64>
 __device__ void hor_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
-                        float (&acc)[EPL]) {
+                        float (&acc)[EPL], float* scales = nullptr) {
   const float cnt = rcount<EPL, LPR>(m);
   const float rc = 1.f / fmaxf(cnt, 1.f);
 #pragma unroll
@@ -103,6 +104,7 @@ __device__ void hor_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
 #pragma unroll
     for (int e = 0; e < EPL; ++e) c[e] = c[e] - mu;
     const float alpha = cnt > 0.f ? div_cnt(rsum_abs<EPL, LPR>(c, m), cnt, rc) : 0.f;
+    if (scales) { scales[2 * od] = mu; scales[2 * od + 1] = alpha; }
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
       const float b = __builtin_fmaf(tsign(c[e]), alpha, mu);
@@ -132,6 +134,9 @@ __device__ __forceinline__ void crb_solve(float d, float c12, float c1w, float c
 // either (the reference multiplies them by the mask, giving the same zeros).
 // Only the signs taken of shifted values (B2 and the refined B1) and the
 // output are masked explicitly.
+// scales (optional): (mean, mu correction, a1, a2) of the row (binary.py:
+// 1599 mean, 1582-1596 a1 / a2, 1633-1635 mu correction); order 1 gives
+// (mean, 0, a1, 0).
 template <int EPL, int LPR = 64>
 __device__ void crb_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
                         const CrbConsts& k, float (&out)[EPL],
@@ -207,13 +212,15 @@ __device__ void crb_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
 }
 
 // coupled_residual_binarization (CRBOG), binary.py:577-687.
+// scales (optional): order 1 as hor_row; order 2 (mean, 0, a1, a2).
 template <int EPL, int LPR = 64>
 __device__ void crbog_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
-                          float (&out)[EPL]) {
-  if (order == 1) { hor_row<EPL, LPR>(x, m, 1, out); return; }               // :595-630
+                          float (&out)[EPL], float* scales = nullptr) {
+  if (order == 1) { hor_row<EPL, LPR>(x, m, 1, out, scales); return; }       // :595-630
   const float n = rcount<EPL, LPR>(m);
 #pragma unroll
   for (int e = 0; e < EPL; ++e) out[e] = 0.f;
+  if (scales) { scales[0] = 0.f; scales[1] = 0.f; scales[2] = 0.f; scales[3] = 0.f; }
   if (n == 0.f) return;                                             // :647-649
   const float rn = 1.f / n;
   const float mean = div_cnt(rsum<EPL, LPR>(x, m), n, rn);
@@ -241,6 +248,7 @@ __device__ void crbog_row(const float (&x)[EPL], const bool (&m)[EPL], int order
     a1 = (float)((0.0 > n1) ? 0.0 : n1);                            // python max(x, 0.0)
     a2 = (float)((0.0 > n2) ? 0.0 : n2);
   }
+  if (scales) { scales[0] = mean; scales[2] = a1; scales[3] = a2; }
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     float v = __builtin_fmaf(a1, B1[e], mean);
@@ -257,19 +265,22 @@ __host__ __device__ inline int method_family(int method) {
 }
 
 // Binarization.quantize dispatch, binary.py:2874-2890, within a family.
+// scales (optional): the per-row scales as hor_row / crb_row / crbog_row
+// write them.
 template <int MF, int EPL, int LPR = 64>
 __device__ __forceinline__ void binarize_row(int method, const float (&x)[EPL],
                                              const bool (&m)[EPL], int order,
-                                             const CrbConsts& base, float (&out)[EPL]) {
+                                             const CrbConsts& base, float (&out)[EPL],
+                                             float* scales = nullptr) {
   if (MF == MF_BRAQ) {
-    hor_row<EPL, LPR>(x, m, order, out);
+    hor_row<EPL, LPR>(x, m, order, out, scales);
   } else if (MF == MF_CRBOG) {
-    crbog_row<EPL, LPR>(x, m, order, out);
+    crbog_row<EPL, LPR>(x, m, order, out, scales);
   } else {
     CrbConsts k = base;
     k.skip = (method == CRBQ_CRB_NOREFINE || method == CRBQ_CRB_SYMDAMP_NOREFINE);
     k.sym = (method == CRBQ_CRB_SYMDAMP || method == CRBQ_CRB_SYMDAMP_NOREFINE);
-    crb_row<EPL, LPR>(x, m, order, k, out);
+    crb_row<EPL, LPR>(x, m, order, k, out, scales);
   }
 }
 

@@ -238,6 +238,31 @@ def binarize(x: torch.Tensor, mask: torch.Tensor, order: int, method: str, lam: 
     return out
 
 
+def binarize_scales(x: torch.Tensor, mask: torch.Tensor, order: int, method: str,
+                    lam: float = 1e-5, corr_damp: float = 0.1, refine_iters: int = 1):
+    """Binarization.quantize with each row's scales (crbq_binarize_scales).
+    Returns (out fp32 [R, cols], scales fp32 [R, n]): n = 4, (mean, mu
+    correction, a1, a2), for the CRB variants and CRBOG at order >= 2;
+    n = 2 * order, (mu_k, alpha_k) per pass, for BRAQ and CRBOG at order 1."""
+    _dev_check(x, mask)
+    if method not in _lib.METHODS:
+        raise NotImplementedError(method)
+    xf = x.float().contiguous()
+    m = mask.expand_as(xf).to(torch.uint8).contiguous()
+    R, nc = xf.shape
+    passes = method == "braq" or (method == "crbog" and order == 1)
+    nsc = 2 * order if passes else 4
+    out = torch.empty((R, nc), dtype=torch.float32, device=x.device)
+    sc = torch.zeros((R, nsc), dtype=torch.float32, device=x.device)
+    lib = _lib.ready(x.device)
+    check(lib.crbq_binarize_scales(xf.data_ptr(), R, nc, xf.stride(0), m.data_ptr(),
+                                   m.stride(0), int(order), _lib.METHODS[method], float(lam),
+                                   float(corr_damp), int(refine_iters), out.data_ptr(),
+                                   out.stride(0), sc.data_ptr(), sc.stride(0), stream_of(xf)),
+          "crbq_binarize_scales")
+    return out, sc
+
+
 def sgemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, alpha: float = 1.0,
           beta: float = 0.0, transa: bool = False, transb: bool = False) -> torch.Tensor:
     """C = beta*C + alpha*op(A) op(B) on fp32 MFMA (row-major operands)."""

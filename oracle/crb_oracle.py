@@ -54,16 +54,21 @@ def _zero_nan(t: torch.Tensor) -> torch.Tensor:
 # binarizers
 # --------------------------------------------------------------------------
 @torch.no_grad()
-def hor(x: torch.Tensor, mask: torch.Tensor, order: int = 2) -> torch.Tensor:
+def hor(x: torch.Tensor, mask: torch.Tensor, order: int = 2,
+        return_scales: bool = False):
     """BRAQ / BiLLM high-order residual binarization, binary.py:18-39.
 
     Each pass: residual on the mask (NaN elsewhere), nanmean -> mu (NaN -> 0),
     center, nanmean |.| -> alpha (NaN -> 0), add (sign*alpha + mu) * mask.
     torch.sign(NaN) is 0, so off-mask entries contribute exactly 0.
+    ``return_scales`` also returns the per-row (mu_k, alpha_k) of every pass
+    as an [R, 2 * order] tensor (the reference's mean_tensor_all /
+    scale_tensor_all, binary.py:26-33).
     """
     acc = torch.zeros_like(x)
     base = x.clone() * mask
     nan = torch.tensor(_NAN, dtype=x.dtype)
+    scales = []
     for _ in range(order):
         res = base - acc
         m = torch.where(mask, res, nan)
@@ -74,6 +79,9 @@ def hor(x: torch.Tensor, mask: torch.Tensor, order: int = 2) -> torch.Tensor:
         b *= alpha[:, None]
         b += mu[:, None]
         acc = acc + b * mask
+        scales += [mu, alpha]
+    if return_scales:
+        return acc, torch.stack(scales, dim=1)
     return acc
 
 
@@ -163,15 +171,19 @@ def crb_v7(x, mask, order=2, lam=1e-5, corr_damp=0.1, skip_refinement=False,
 
 
 @torch.no_grad()
-def crbog(x, mask, order=2):
+def crbog(x, mask, order=2, return_scales=False):
     """CRBOG, binary.py:577-687 (``coupled_residual_binarization``).
 
     order 1 is the single BRAQ pass; order >= 2 is a per-row loop over rows
     with a float64 (Python float) 2x2 solve without damping or Tikhonov term.
+    ``return_scales`` also returns per-row scales: order 1 as ``hor``; order
+    >= 2 an [R, 4] tensor (row_mean, 0, alpha1, alpha2) with the alphas as
+    the fp32 values the final approximation uses (:653-682).
     """
     if order == 1:                                           # :595-630
-        return hor(x, mask, order=1)
+        return hor(x, mask, order=1, return_scales=return_scales)
     out = torch.zeros_like(x)
+    sc = torch.zeros(x.shape[0], 4, dtype=x.dtype)
     base = x.clone() * mask
     for i in range(base.shape[0]):                           # :644-685
         rm = mask[i, :]
@@ -194,6 +206,9 @@ def crbog(x, mask, order=2):
             a1 = max((c1w * n - c2w * c12) / det, 0.0)
             a2 = max((c2w * n - c1w * c12) / det, 0.0)
         out[i, rm] = mean + a1 * b1 + a2 * b2
+        sc[i, 0], sc[i, 2], sc[i, 3] = mean, float(a1), float(a2)
+    if return_scales:
+        return out, sc
     return out
 
 

@@ -11,7 +11,7 @@ is quoted on (hidden 4096, ffn 16384, 128 x 2048 calibration tokens).
      U, the upper Cholesky factor of H_d^-1, is near-diagonal inside each
      128-column block, as these near-diagonal Hessians give;
    * the exact forms: U^-1 U^-T = H_d to 1e-5 and W0 - Q = E U' to 1e-5
-     (_u_checks).
+     (gpu_helpers.u_checks).
    * every quantized sublayer packs (shared salient columns, at most 2 / 4
      values per group apart from rare ties at a group mean) and unpacks
      bit-exactly.
@@ -25,7 +25,7 @@ is quoted on (hidden 4096, ffn 16384, 128 x 2048 calibration tokens).
    propagated through the layers (run.py:122-387), for every sublayer of
    both layers: U^-1 U^-T = H_d to 1e-5 (the factor's backward error) and
    W0 - Q = E U' with sum(E^2) / 2 = the accumulated loss to 1e-5 (the
-   block loop's error feedback; U' defined in _u_checks), both evaluated in
+   block loop's error feedback; U' defined in gpu_helpers.u_checks), both evaluated in
    float64.  The H_d-metric form above is printed but not asserted here:
    it assumes feedback inside each block too, which the reference's
    pre-quantize-then-read path (bigptq.py:235-262) does not do, so it only
@@ -38,22 +38,14 @@ import pytest
 import torch
 
 from crb_amd import synth
+from gpu_helpers import acts as _acts
+from gpu_helpers import u_checks as _u_checks
 from oracle import crb_oracle as O
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 NTOK = 128 * 2048
 NBLK = 4
-
-
-def _acts(C, seed):
-    s = synth.channel_scales(C, seed, kind="student_t4", device=DEV)
-    g = torch.Generator(device=DEV)
-    g.manual_seed(seed)
-    x = torch.empty(NTOK, C, dtype=torch.float16, device=DEV)
-    for t0 in range(0, NTOK, 8192):
-        x[t0:t0 + 8192] = (torch.randn(8192, C, generator=g, device=DEV) * s).half()
-    return x
 
 
 def _identity(W0, Q, Hd, err):
@@ -68,41 +60,6 @@ def _identity(W0, Q, Hd, err):
         d = D[r0:r0 + 2048]
         quad += float(((d @ Hd64) * d).sum()) / 2
     return abs(quad - err) / err
-
-
-def _u_checks(W0, Q, Hd, U, err):
-    """Checks that hold to fp32 backward error whatever the conditioning of
-    H_d (real activations of a random-init model give nearly rank-deficient
-    Hessians, e.g. out_proj's input is a near-uniform average over tokens,
-    and then the identity above is only as good as cond(H_d) * eps):
-    * the factor: U^-1 U^-T against H_d, relative Frobenius error (U is the
-      upper Cholesky factor of H_d^-1, so U^-1 U^-T = H_d);
-    * the block loop: the reference quantizes a 128-column block from its
-      values at the block's start (no feedback inside the block,
-      bigptq.py:235-262) and then updates the later blocks,
-      W[:, ed:] -= Err1 U[st:ed, ed:] (:264), so W0 - Q = E U' with U' = U
-      without the strictly upper entries inside each 128 x 128 diagonal
-      block; E = (W0 - Q) U'^-1 and sum(E^2) / 2 is the accumulated loss.
-    Both in float64 from the fp32 U."""
-    U64 = U.double()
-    C = U.shape[0]
-    I = torch.eye(C, dtype=torch.float64, device=U.device)
-    Ui = torch.linalg.solve_triangular(U64, I, upper=True)
-    Ht = Ui @ Ui.t()
-    back = float((Ht - Hd.double()).norm() / Hd.double().norm())
-    del Ht, Ui
-    blk = torch.arange(C, device=U.device) // 128
-    inner = (blk[:, None] == blk[None, :]) & (torch.arange(C, device=U.device)[:, None]
-                                              != torch.arange(C, device=U.device)[None, :])
-    U64.masked_fill_(inner, 0.0)
-    Upi = torch.linalg.solve_triangular(U64, I, upper=True)
-    del I, U64, inner
-    D = (W0 - Q).double()
-    tot = 0.0
-    for r0 in range(0, D.shape[0], 2048):
-        E = D[r0:r0 + 2048] @ Upi
-        tot += float((E * E).sum()) / 2
-    return back, abs(tot - err) / err
 
 
 def _pack_check(name, Q, masks):
@@ -229,3 +186,83 @@ def test_opt67b_two_layer_stack():
     assert len(stats) == 2 and len(results) == 12
     for name, err, back, loop in results:
         assert err > 0 and back < 1e-5 and loop < 1e-5, (name, err, back, loop)
+
+
+def test_opt67b_stack_default_vs_per_call():
+    """One OPT-6.7B-shaped decoder layer (hidden 4096, ffn 16384) from
+    128 x 2048 random token ids, quantized by the stack driver's default mode
+    (chunks of 8 samples, one Hessian call per input over all 262144 tokens)
+    and by its per-call mode (one forward and one add_batch per sample:
+    128 Hessian calls per input, run.py:341-374's order), from the same layer
+    input.  The Hessians differ by fp32 summation order only.  Bar: the
+    layer's reconstruction error sum_s ||(W_s - Q_s) X_s^T||_F^2 over the
+    calibration tokens within 1e-3 relative; each sublayer's spread is
+    printed.  ||(W - Q) X^T||_F^2 = (nseq / 2) sum((D H) * D) with H the
+    undamped Hessian (recovered from the damped one: H_d = H + 0.01 *
+    mean(diag H) I), the per-call run's H for both."""
+    transformers = pytest.importorskip("transformers")
+    from crb_amd.driver import LayerQuantizer
+    from crb_amd.stack import StackQuantizer
+    print("OPT-6.7B layer: stack default mode vs per-call mode", flush=True)
+    rec = {}
+
+    def recorder(tag):
+        class Rec(LayerQuantizer):
+            def quantize(self, times=None):
+                w0 = {s.name: s.weight.float() for s in self.sublayers}
+                errs = super().quantize(times)
+                for s in self.sublayers:
+                    Hd, _ = self.factors[s.group]
+                    Q, _ = self.quantized[s.name]
+                    rec[(tag, s.name)] = (w0[s.name], Q.clone(), Hd, errs[s.name])
+                self.factors, self.quantized = {}, {}
+                return errs
+        return Rec
+
+    def model():
+        torch.manual_seed(0)
+        cfg = transformers.OPTConfig(hidden_size=4096, ffn_dim=16384, num_attention_heads=32,
+                                     num_hidden_layers=1, max_position_embeddings=2048,
+                                     vocab_size=50272, word_embed_proj_dim=4096)
+        with torch.device(DEV):
+            return transformers.OPTForCausalLM(cfg).half().eval()
+
+    g = torch.Generator().manual_seed(1)
+    samples = torch.randint(0, 50272, (128, 2048), generator=g).to(DEV)
+    a = StackQuantizer(model(), chunk=8, defer_hessian=True,
+                       layer_quantizer=recorder("default"), keep_factors=True)
+    x = a.capture(samples)
+    a.quantize_layer(0, x, None)
+    del a
+    torch.cuda.empty_cache()
+    b = StackQuantizer(model(), chunk=1, defer_hessian=False,
+                       layer_quantizer=recorder("per_call"), keep_factors=True)
+    assert torch.equal(b.capture(samples), x)
+    b.quantize_layer(0, x, None)
+    del b, x
+    names = [k for t, k in rec if t == "per_call"]
+    tot = {"default": 0.0, "per_call": 0.0}
+    for k in names:
+        w0, qb, hd, eb = rec[("per_call", k)]
+        _, qa, _, ea = rec[("default", k)]
+        hd64 = hd.double()
+        lam = 0.01 * float(torch.diagonal(hd64).mean()) / 1.01
+        h64 = hd64 - lam * torch.eye(hd.shape[0], dtype=torch.float64, device=DEV)
+        r = {}
+        for tag, q in (("default", qa), ("per_call", qb)):
+            v = 0.0
+            d = (w0 - q).double()
+            for r0 in range(0, d.shape[0], 2048):
+                dd = d[r0:r0 + 2048]
+                v += float(((dd @ h64) * dd).sum()) * 128 / 2
+            r[tag] = v
+            tot[tag] += v
+        print(f"  {k}: recon^2 default {r['default']:.6g} per-call {r['per_call']:.6g} "
+              f"rel {abs(r['default'] - r['per_call']) / r['per_call']:.2e}; loss default "
+              f"{ea:.6g} per-call {eb:.6g} rel {abs(ea - eb) / eb:.2e}", flush=True)
+        del h64, hd64
+    rel = abs(tot["default"] - tot["per_call"]) / tot["per_call"]
+    relf = abs(tot["default"] ** 0.5 - tot["per_call"] ** 0.5) / tot["per_call"] ** 0.5
+    print(f"  layer ||(W - Q) X^T||_F default {tot['default'] ** 0.5:.6g} per-call "
+          f"{tot['per_call'] ** 0.5:.6g}: rel {relf:.2e} (squared {rel:.2e})", flush=True)
+    assert relf < 1e-3, relf
