@@ -343,26 +343,25 @@ __device__ __forceinline__ i4_t xt_rsrc(const uint16_t* base, int nrec) {
               __builtin_amdgcn_readfirstlane(nrec), 0x00020000};
 }
 
-// One wavefront's share of a stage: 8-row groups g = 4w .. 4w+3 of both
-// operand panels (1 KB per group and side: one buffer_load_dwordx4 ... lds,
-// whose 64 lanes write 16 bytes each at M0 + 16 * lane).  Lane l fills slot
-// l & 7 of row l >> 3 of the group, so it reads the chunk that belongs
-// there.  Issued through inline assembly; the caller waits for it.
-__device__ __forceinline__ void xt_stage_loads(uint16_t* buf, int stage, int wave, i4_t rs0,
-                                               i4_t rs1, int voff, int gstep) {
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int g = wave * 4 + q;
-    const int soff = __builtin_amdgcn_readfirstlane(g * gstep + stage * KQ * 2);
-    const unsigned d0 = __builtin_amdgcn_readfirstlane(
-        (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)(buf + g * 8 * KQ));
-    const unsigned d1 = __builtin_amdgcn_readfirstlane(
-        (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)(buf + (ST + g * 8) * KQ));
-    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
-                 :: "v"(voff), "s"(rs0), "s"(soff), "{m0}"(d0) : "memory");
-    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
-                 :: "v"(voff), "s"(rs1), "s"(soff), "{m0}"(d1) : "memory");
-  }
+// Load k (0..7) of one wavefront's share of a stage: 8-row group
+// g = 4w + (k & 3) of operand panel k >> 2 (1 KB: one buffer_load_dwordx4
+// ... lds, whose 64 lanes write 16 bytes each at M0 + 16 * lane).  Lane l
+// fills slot l & 7 of row l >> 3 of the group, so it reads the chunk that
+// belongs there.  Inline assembly: the compiler does not see these loads,
+// so it does not make operand reads of the other buffer wait for them; the
+// caller waits for them (vmcnt).  No "memory" clobber: the load writes a
+// buffer no operand read of the current stage touches, and its order
+// against the barriers (volatile asm) is kept.
+__device__ __forceinline__ void xt_load(uint16_t* buf, int stage, int wave, int k, i4_t rs0,
+                                        i4_t rs1, int voff, int gstep) {
+  const int g = wave * 4 + (k & 3);
+  const int soff = __builtin_amdgcn_readfirstlane(g * gstep + stage * KQ * 2);
+  const unsigned d = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)(buf + ((k >> 2) * ST +
+                                                                              g * 8) * KQ));
+  const i4_t rs = (k >> 2) ? rs1 : rs0;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" :: "v"(voff), "s"(rs), "s"(soff),
+               "{m0}"(d));
 }
 
 // SYRK on Xt, 256 x 256 upper tiles, 8 wavefronts.  Each wavefront computes
@@ -370,12 +369,17 @@ __device__ __forceinline__ void xt_stage_loads(uint16_t* buf, int stage, int wav
 // stage) from a 2-stage LDS ring of 64-token stages, and also loads a
 // quarter of every stage with direct-to-LDS buffer loads (L2 straight into
 // LDS, no VGPR round trip, no loader wavefronts, so each wavefront may use
-// 256 registers).  At the top of iteration c the loads of stage c + 1 go
-// into the buffer every wavefront finished reading at the barrier that
-// ended iteration c - 1; each wavefront waits for its own loads
-// (vmcnt(0)) before the barrier that ends iteration c.  The compiler does
-// not see these loads, so it cannot hold the operand reads of the other
-// buffer behind them.
+// 256 registers).  During stage c a wavefront issues its 8 loads of stage
+// c + 1, one after each 16-row A fragment of the stage's first 32-token
+// slice (between the MFMAs: a burst of 64 loads per CU at the top of the
+// stage held the wavefronts in VMEM issue), into the buffer every
+// wavefront finished reading at the barrier that ended stage c - 1; each
+// wavefront waits for its own loads (vmcnt(0)) before the barrier that
+// ends stage c.  In the last stage the loads repeat stage nch - 1 into the
+// other buffer, which is not read again, so every stage issues the same 8
+// loads without a branch.  The next A fragment is read before the current
+// one's MFMAs, and a scheduling barrier after each fragment's group keeps
+// that order.
 // Requires Cp = nt * 256 rows in Xt, ldt, span and tpad multiples of KQ, and
 // 256 * ldt * 2 < 2^31 (a tile's panel is addressed with 32-bit offsets).
 template <typename T8>
@@ -406,12 +410,15 @@ __global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __res
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
   const int r16 = lane & 15;
-  if (nch > 0) xt_stage_loads(&Xs[0][0][0][0], 0, wave, rs0, rs1, voff, gstep);
+  if (nch > 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) xt_load(&Xs[0][0][0][0], 0, wave, k, rs0, rs1, voff, gstep);
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   sync_lds();
   for (int c = 0; c < nch; ++c) {
-    if (c + 1 < nch)
-      xt_stage_loads(&Xs[(c + 1) & 1][0][0][0], c + 1, wave, rs0, rs1, voff, gstep);
+    const int nxt = c + 1 < nch ? c + 1 : nch - 1;     // stage loaded during this one
+    uint16_t* nbuf = &Xs[(c + 1) & 1][0][0][0];
     const uint16_t (*XA)[KQ] = Xs[c & 1][0];
     const uint16_t (*XB)[KQ] = Xs[c & 1][1];
 #pragma unroll
@@ -421,11 +428,17 @@ __global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __res
       T8 bb[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) bb[j] = *(const T8*)&XB[wn + j * 16 + r16][slot];
+      T8 an = *(const T8*)&XA[wm + r16][slot];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const T8 a = *(const T8*)&XA[wm + i * 16 + r16][slot];
+        const T8 a = an;
+        if (i < 7) an = *(const T8*)&XA[wm + (i + 1) * 16 + r16][slot];
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T8>(a, bb[j], acc[i][j]);
+        if (h == 0) {
+          xt_load(nbuf, nxt, wave, i, rs0, rs1, voff, gstep);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
