@@ -64,6 +64,13 @@ _SIGS = {
     "crbq_hessian_workspace_size": (c_size, [c_i64, c_i64]),
     "crbq_hessian_accum": (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp, c_size,
                                    c_vp]),
+    "crbq_hessian_cm_shape": (c_i32, [c_i64, c_i64, ctypes.POINTER(c_i64),
+                                      ctypes.POINTER(c_i64)]),
+    "crbq_hessian_transpose": (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i64, c_i64,
+                                       c_vp]),
+    "crbq_hessian_cm_workspace_size": (c_size, [c_i64, c_i64]),
+    "crbq_hessian_accum_cm": (c_i32, [c_vp, c_i32, c_i64, c_i64, c_i64, c_vp, c_i64, c_vp,
+                                      c_size, c_vp]),
     "crbq_syrk_timing": (c_i32, [c_i32]),
     "crbq_syrk_timing_collect": (c_i32, [c_vp, c_vp, c_i32, ctypes.POINTER(c_i32)]),
     "crbq_hessian_finalize": (c_i32, [c_vp, c_i64, c_i64, ctypes.c_float, c_vp, c_i64, c_vp]),

@@ -734,6 +734,38 @@ static XtPlan xt_plan(int64_t ntok, int64_t C) {
 }
 }  // namespace crbq
 
+namespace crbq {
+// SYRK of a channel-major operand Xt[Cp][ldt] (rows >= C and tokens in
+// [ntok, tpad) zero, tpad a multiple of KQ, ldt >= tpad): token splits
+// chosen by the cost model within the partial-tile capacity pcap, split 0
+// adding into S and the others summed after it in split order.
+static int syrk_xt(const uint16_t* Xt, int64_t ldt, int64_t tpad, int64_t C, float* S,
+                   int64_t lds, float* Pbuf, size_t pcap, int dtype, hipStream_t s) {
+  const int nt = (int)((C + ST - 1) / ST);
+  const int64_t ntiles = (int64_t)nt * (nt + 1) / 2;
+  int ns = choose_splits(tpad, C, num_cus());
+  while (ns > 1 && (size_t)ns * (size_t)C * (size_t)lds * sizeof(float) > pcap) --ns;
+  int64_t span = (tpad + ns - 1) / ns;
+  span = (span + KQ - 1) / KQ * KQ;
+  ns = (int)((tpad + span - 1) / span);
+  float* P = ns > 1 ? Pbuf : nullptr;
+  dim3 grid((unsigned)ntiles, (unsigned)ns);
+  SyrkTimer tm(s, C);
+  if (dtype == CRBQ_F16)
+    k_syrk16k<h8_t><<<grid, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt, span, P);
+  else
+    k_syrk16k<b8_t><<<grid, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt, span, P);
+  CRBQ_LAUNCH_CHECK();
+  tm.stop(s);
+  if (P) {
+    k_sum_splits<<<dim3((unsigned)C, (unsigned)((C + 1023) / 1024)), 256, 0, s>>>(P, ns - 1,
+                                                                                 (int)C, S, lds);
+    CRBQ_LAUNCH_CHECK();
+  }
+  return CRBQ_OK;
+}
+}  // namespace crbq
+
 extern "C" size_t crbq_hessian_workspace_size(int64_t ntok, int64_t C) {
   if (ntok <= 0 || C <= 0) return 0;
   const crbq::XtPlan pl = crbq::xt_plan(ntok, C);
@@ -782,27 +814,8 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
         crbq::k_xpose16<false><<<nblk, 256, 0, s>>>(Xc, n, ldx, (int)C, Xt, pl.ldt, tpad,
                                                     (int)pl.Cp);
       CRBQ_LAUNCH_CHECK();
-      int ns = crbq::choose_splits(tpad, C, crbq::num_cus());
-      while (ns > 1 && (size_t)ns * (size_t)C * (size_t)lds * sizeof(float) > pcap) --ns;
-      int64_t span = (tpad + ns - 1) / ns;
-      span = (span + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
-      ns = (int)((tpad + span - 1) / span);
-      float* P = ns > 1 ? Pbuf : nullptr;
-      dim3 grid((unsigned)ntiles, (unsigned)ns);
-      crbq::SyrkTimer tm(s, C);
-      if (dtype == CRBQ_F16)
-        crbq::k_syrk16k<h8_t><<<grid, crbq::SYRKD_THREADS, 0, s>>>(Xt, pl.ldt, tpad, (int)C, S,
-                                                                   lds, nt, span, P);
-      else
-        crbq::k_syrk16k<b8_t><<<grid, crbq::SYRKD_THREADS, 0, s>>>(Xt, pl.ldt, tpad, (int)C, S,
-                                                                   lds, nt, span, P);
-      CRBQ_LAUNCH_CHECK();
-      tm.stop(s);
-      if (P) {
-        crbq::k_sum_splits<<<dim3((unsigned)C, (unsigned)((C + 1023) / 1024)), 256, 0, s>>>(
-            P, ns - 1, (int)C, S, lds);
-        CRBQ_LAUNCH_CHECK();
-      }
+      const int st = crbq::syrk_xt(Xt, pl.ldt, tpad, C, S, lds, Pbuf, pcap, dtype, s);
+      if (st) return st;
     }
     return CRBQ_OK;
   }
@@ -833,6 +846,62 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
     CRBQ_LAUNCH_CHECK();
   }
   return CRBQ_OK;
+}
+
+extern "C" int crbq_hessian_cm_shape(int64_t ntok, int64_t C, int64_t* rows, int64_t* ldt) {
+  if (!rows || !ldt || ntok <= 0 || C <= 0 || C > (1 << 20)) return CRBQ_ERR_ARG;
+  const int64_t tpad = (ntok + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
+  if (tpad > ((int64_t)1 << 21)) return CRBQ_ERR_ARG;
+  *rows = (C + crbq::ST - 1) / crbq::ST * crbq::ST;
+  *ldt = tpad;
+  return CRBQ_OK;
+}
+
+extern "C" int crbq_hessian_transpose(const void* X, int dtype, int64_t ntok, int64_t ldx,
+                                      int64_t C, void* Xt, int64_t ldt, int64_t t0,
+                                      void* stream) {
+  if (!X || !Xt || ntok <= 0 || C <= 0 || C > (1 << 20) || ldx < C) return CRBQ_ERR_ARG;
+  if (dtype != CRBQ_F16 && dtype != CRBQ_BF16) return CRBQ_ERR_ARG;
+  if (t0 < 0 || t0 % crbq::KQ || ldt % crbq::KQ || ldt > ((int64_t)1 << 21)) return CRBQ_ERR_ARG;
+  const int64_t tpad = (ntok + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
+  if (t0 + tpad > ldt) return CRBQ_ERR_ARG;
+  if ((((uintptr_t)Xt) & 15) != 0) return CRBQ_ERR_ARG;
+  const int64_t Cp = (C + crbq::ST - 1) / crbq::ST * crbq::ST;
+  const bool fast = (C % 8 == 0) && (ldx % 8 == 0) && ((((uintptr_t)X) & 15) == 0);
+  const int64_t nw = (tpad / 64) * (Cp / 64);
+  const unsigned nblk = (unsigned)((nw + 3) / 4 < 4096 ? (nw + 3) / 4 : 4096);
+  uint16_t* dst = (uint16_t*)Xt + t0;
+  hipStream_t s = (hipStream_t)stream;
+  if (fast)
+    crbq::k_xpose16<true><<<nblk, 256, 0, s>>>((const uint16_t*)X, ntok, ldx, (int)C, dst, ldt,
+                                               tpad, (int)Cp);
+  else
+    crbq::k_xpose16<false><<<nblk, 256, 0, s>>>((const uint16_t*)X, ntok, ldx, (int)C, dst,
+                                                ldt, tpad, (int)Cp);
+  CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}
+
+extern "C" size_t crbq_hessian_cm_workspace_size(int64_t ntok, int64_t C) {
+  if (ntok <= 0 || C <= 0) return 0;
+  const int64_t tpad = (ntok + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
+  const int ns = crbq::choose_splits(tpad, C, crbq::num_cus());
+  return ns > 1 ? (size_t)ns * (size_t)C * (size_t)C * sizeof(float) : 0;
+}
+
+extern "C" int crbq_hessian_accum_cm(const void* Xt, int dtype, int64_t ntok, int64_t ldt,
+                                     int64_t C, float* S, int64_t lds, void* ws,
+                                     size_t ws_bytes, void* stream) {
+  if (!Xt || !S || C <= 0 || C > (1 << 20) || ntok < 0 || lds < C) return CRBQ_ERR_ARG;
+  if (dtype != CRBQ_F16 && dtype != CRBQ_BF16) return CRBQ_ERR_ARG;
+  if (ntok == 0) return CRBQ_OK;
+  const int64_t tpad = (ntok + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
+  if (ldt % crbq::KQ || ldt < tpad || ldt > ((int64_t)1 << 21)) return CRBQ_ERR_ARG;
+  if ((((uintptr_t)Xt) & 15) != 0) return CRBQ_ERR_ARG;
+  const int nt = (int)((C + crbq::ST - 1) / crbq::ST);
+  if ((int64_t)nt * (nt + 1) / 2 > 0x7fffffff) return CRBQ_ERR_ARG;
+  return crbq::syrk_xt((const uint16_t*)Xt, ldt, tpad, C, S, lds, (float*)ws, ws ? ws_bytes : 0,
+                       dtype, (hipStream_t)stream);
 }
 
 extern "C" int crbq_syrk_timing(int on) {

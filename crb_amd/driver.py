@@ -89,6 +89,24 @@ class LayerQuantizer:
             ev = self.ready[group] = torch.cuda.Event()
         ev.record(cur)
 
+    def add_batch_cm(self, group: str, xt: torch.Tensor, ntok: int, nseq: int) -> None:
+        """add_batch for nseq sequences whose ntok tokens in total are
+        already in a channel-major store (kernels.hessian_transpose), the
+        same Hessian update as add_batch on those tokens."""
+        self.nsamples[group] += nseq
+        cur = torch.cuda.current_stream(self.dev)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(cur)
+        kernels.hessian_accum_cm(xt, ntok, self.S[group].shape[0], self.S[group])
+        b.record(cur)
+        first = self.syrk_ev.get(group)
+        self.syrk_ev[group] = (first[0] if first else a, b)
+        ev = self.ready.get(group)
+        if ev is None:
+            ev = self.ready[group] = torch.cuda.Event()
+        ev.record(cur)
+
     def _accum(self, group, inp, stream):
         """Hessian update of `group` on `stream`, bracketed by timing events."""
         a = torch.cuda.Event(enable_timing=True)

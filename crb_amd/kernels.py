@@ -43,6 +43,45 @@ def hessian_accum(X: torch.Tensor, S: torch.Tensor) -> None:
           "crbq_hessian_accum")
 
 
+def hessian_cm_store(ntok: int, C: int, dtype: torch.dtype, device) -> torch.Tensor:
+    """An uninitialised channel-major activation store [rows, ldt] for
+    hessian_transpose / hessian_accum_cm (crbq_hessian_cm_shape)."""
+    rows, ldt = ctypes.c_int64(), ctypes.c_int64()
+    check(_lib.load().crbq_hessian_cm_shape(int(ntok), int(C), ctypes.byref(rows),
+                                            ctypes.byref(ldt)), "crbq_hessian_cm_shape")
+    return torch.empty((rows.value, ldt.value), dtype=dtype, device=device)
+
+
+def hessian_transpose(X: torch.Tensor, Xt: torch.Tensor, t0: int) -> None:
+    """Write the token rows of X [T, C] (f16/bf16) into columns t0.. of the
+    channel-major store Xt (t0 a multiple of 64)."""
+    _dev_check(X, Xt)
+    if X.dim() != 2 or X.stride(1) != 1:
+        X = X.reshape(-1, X.shape[-1]).contiguous()
+    if X.dtype not in (torch.float16, torch.bfloat16) or Xt.dtype != X.dtype:
+        raise _lib.CrbqError("hessian_transpose takes 16-bit activations and a store of "
+                             "the same dtype")
+    if Xt.stride(1) != 1:
+        raise _lib.CrbqError("hessian_transpose writes a row-major store")
+    T, C = X.shape
+    lib = _lib.ready(X.device)
+    check(lib.crbq_hessian_transpose(X.data_ptr(), _lib.DTYPES[X.dtype], T, X.stride(0), C,
+                                     Xt.data_ptr(), Xt.stride(0), int(t0), stream_of(Xt)),
+          "crbq_hessian_transpose")
+
+
+def hessian_accum_cm(Xt: torch.Tensor, ntok: int, C: int, S: torch.Tensor) -> None:
+    """S += Xt[:C, :ntok] Xt[:C, :ntok]^T (upper triangle) from a store that
+    hessian_transpose filled."""
+    _dev_check(Xt, S)
+    lib = _lib.ready(Xt.device)
+    nb = lib.crbq_hessian_cm_workspace_size(int(ntok), int(C)) if S.stride(0) == C else 0
+    ws = _ws(nb, Xt.device) if nb else None
+    check(lib.crbq_hessian_accum_cm(Xt.data_ptr(), _lib.DTYPES[Xt.dtype], int(ntok),
+                                    Xt.stride(0), int(C), S.data_ptr(), S.stride(0), ptr(ws),
+                                    nb, stream_of(S)), "crbq_hessian_accum_cm")
+
+
 def syrk_timing(on: bool) -> None:
     """Switch the per-launch SYRK timing of hessian_accum on or off."""
     check(_lib.load().crbq_syrk_timing(1 if on else 0), "crbq_syrk_timing")

@@ -42,6 +42,7 @@ from dataclasses import dataclass, field
 import torch
 import torch.nn as nn
 
+from . import kernels
 from .driver import LayerQuantizer, PhaseTimes, Sublayer
 
 
@@ -254,10 +255,20 @@ class StackQuantizer:
                 return
             st = stores.get(g)
             if st is None:
-                st = stores[g] = [torch.empty((n * t.shape[1], t.shape[2]), dtype=t.dtype,
-                                              device=t.device), t.shape[1], 0]
+                per, C = t.shape[1], t.shape[2]
+                if self._cm_ok(lq, t, n * per):
+                    # channel-major store: the copy of each chunk into it is
+                    # the Hessian's transpose (kernels.hessian_transpose)
+                    buf = kernels.hessian_cm_store(n * per, C, t.dtype, t.device)
+                    st = stores[g] = [buf, per, 0, True]
+                else:
+                    st = stores[g] = [torch.empty((n * per, C), dtype=t.dtype,
+                                                  device=t.device), per, 0, False]
             per = st[1]
-            st[0][j * per:(j + b) * per] = t.reshape(-1, t.shape[-1])
+            if st[3]:
+                kernels.hessian_transpose(t.reshape(-1, t.shape[-1]), st[0], j * per)
+            else:
+                st[0][j * per:(j + b) * per] = t.reshape(-1, t.shape[-1])
             st[2] += b
 
         b0 = min(self.chunk, n)
@@ -286,8 +297,24 @@ class StackQuantizer:
             finally:
                 for h in hooks:
                     h.remove()
-        pending = [(g, buf.view(nseq, per, buf.shape[1])) for g, (buf, per, nseq) in stores.items()]
+        pending = [(g, (buf, per * nseq, nseq) if cm else buf.view(nseq, per, buf.shape[1]))
+                   for g, (buf, per, nseq, cm) in stores.items()]
         return lq, groups, pending
+
+    @staticmethod
+    def _cm_ok(lq, t, ntok):
+        """The deferred store can be the Hessian's channel-major operand:
+        16-bit activations on the GPU, every chunk starting at a multiple of
+        64 tokens (whole samples of a multiple of 64 tokens), and all tokens
+        in one SYRK pass (at most 2^21 tokens and 8 GiB), so the update's
+        sums are those of add_batch on the same tokens."""
+        if not (t.is_cuda and t.dtype in (torch.float16, torch.bfloat16)):
+            return False
+        if not hasattr(lq, "add_batch_cm") or t.shape[1] % 64:
+            return False
+        rows = (t.shape[2] + 255) // 256 * 256
+        ldt = (ntok + 63) // 64 * 64
+        return ldt <= (1 << 21) and rows * ldt * 2 <= (1 << 33)
 
     @torch.no_grad()
     def quantize_layer(self, i: int, inps: torch.Tensor, outs: torch.Tensor | None) -> LayerStats:
@@ -310,7 +337,10 @@ class StackQuantizer:
         lq, groups, pending = self._capture_layer(i, layer, inps)
         clock.mark()
         for g, x in pending:
-            lq.add_batch(g, x)
+            if isinstance(x, tuple):
+                lq.add_batch_cm(g, *x)
+            else:
+                lq.add_batch(g, x)
         del pending
         clock.mark()
         stats = LayerStats(errors={}, groups=groups)

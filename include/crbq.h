@@ -117,6 +117,29 @@ size_t crbq_hessian_workspace_size(int64_t ntok, int64_t C);
 int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_t ldx,
                        int64_t C, float* S, int64_t lds, void* ws, size_t ws_bytes,
                        void* stream);
+/* The same Hessian update from a channel-major copy of the activations that
+ * the caller builds (for callers that gather the activations of several
+ * forwards before one update: the stack driver's deferred Hessians,
+ * run.py:341-374, whose copy of each forward's activations into the store
+ * is then the transpose, saving crbq_hessian_accum's own pass over X).
+ *   crbq_hessian_cm_shape: the store's shape for ntok tokens of C channels:
+ *     *rows = C rounded up to 256, *ldt = ntok rounded up to 64 (at most
+ *     2^21 tokens);
+ *   crbq_hessian_transpose: writes ntok token rows of X (16-bit, row stride
+ *     ldx) into columns [t0, t0 + ntok rounded up to 64) of the store Xt
+ *     (rows x ldt halves, 16-byte aligned; t0 a multiple of 64), zeros in
+ *     the padding rows and columns; fill the store in token order so every
+ *     column up to ldt is written;
+ *   crbq_hessian_accum_cm: S += Xt Xt^T over the first ntok columns
+ *     (upper triangle), the same sums as crbq_hessian_accum on the same
+ *     tokens; ws holds the per-split partial tiles
+ *     (crbq_hessian_cm_workspace_size bytes; with less, fewer splits). */
+int crbq_hessian_cm_shape(int64_t ntok, int64_t C, int64_t* rows, int64_t* ldt);
+int crbq_hessian_transpose(const void* X, int dtype, int64_t ntok, int64_t ldx, int64_t C,
+                           void* Xt, int64_t ldt, int64_t t0, void* stream);
+size_t crbq_hessian_cm_workspace_size(int64_t ntok, int64_t C);
+int crbq_hessian_accum_cm(const void* Xt, int dtype, int64_t ntok, int64_t ldt, int64_t C,
+                          float* S, int64_t lds, void* ws, size_t ws_bytes, void* stream);
 /* SYRK launch timing, a profiling aid with no counterpart in the reference.
  * While on != 0, crbq_hessian_accum records a pair of HIP events on its
  * stream right before and right after each SYRK kernel launch (process-wide

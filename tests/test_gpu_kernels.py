@@ -242,6 +242,36 @@ def test_hessian_channel_major_passes(dtype, T, C, ldx, pass_tok, monkeypatch):
     assert torch.equal(torch.triu(S).cpu(), torch.triu(S2).cpu())
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("C,chunks", [(300, (128, 64, 192, 100)), (512, (2048, 2048)),
+                                      (1000, (64,))])
+def test_hessian_channel_major_store(dtype, C, chunks):
+    """crbq_hessian_transpose chunk by chunk into a channel-major store, then
+    crbq_hessian_accum_cm: bitwise the sums of crbq_hessian_accum on the same
+    tokens (same operand layout, same token splits), and against float64;
+    the last chunk may be ragged (its padding columns are zeroed)."""
+    print(f"hessian channel-major store {dtype} C={C} chunks={chunks}", flush=True)
+    g = torch.Generator().manual_seed(C + len(chunks))
+    T = sum(chunks)
+    X = (torch.randn(T, C, generator=g) * torch.exp(torch.randn(C, generator=g))).to(dtype)
+    Xd = X.to(DEV)
+    Xt = _k().hessian_cm_store(T, C, dtype, DEV)
+    assert Xt.shape[0] % 256 == 0 and Xt.shape[1] % 64 == 0
+    Xt.fill_(1.0)                       # every entry must be written (data or padding)
+    t0 = 0
+    for n in chunks:
+        _k().hessian_transpose(Xd[t0:t0 + n], Xt, t0)
+        t0 += n
+    S1 = torch.zeros(C, C, device=DEV)
+    _k().hessian_accum_cm(Xt, T, C, S1)
+    S2 = torch.zeros(C, C, device=DEV)
+    _k().hessian_accum(Xd, S2)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.triu(S1), torch.triu(S2))
+    want = X.double().t() @ X.double()
+    assert rel(torch.triu(S1), torch.triu(want)) < 1e-5
+
+
 def test_hessian_matches_reference_add_batch():
     """Incremental rescale of bigptq.py:50-53 vs. one 2/n scaling."""
     print("hessian add_batch", flush=True)
