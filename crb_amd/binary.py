@@ -45,7 +45,16 @@ class Binarization(nn.Module):
 
     def quantize(self, w, mask, order=2, groupi=0, col_weights=None):
         """binary.py:2874-2890.  ``col_weights`` and ``groupi`` are ignored by
-        these methods in the reference as well."""
+        these methods in the reference as well.
+
+        The kernels compute in fp32.  ``BRAGPTQ.fasterquant`` always passes
+        fp32 blocks (bigptq.py:60), so on that path the arithmetic is the
+        reference's.  A direct caller passing fp16/bf16 ``w`` gets the fp32
+        result rounded once to ``w``'s dtype, where the reference computes
+        every step in the input dtype (each torch op rounding to fp16/bf16);
+        the two agree to within that dtype's rounding of the scales, and a
+        sign decision sitting within one such ulp of its group's mean may
+        differ."""
         if not self.on_crbq_path:
             raise NotImplementedError(
                 f"Binarization method {self.method!r} is outside the crbq hot path")
