@@ -726,11 +726,12 @@ def main():
         # and the engine clock it ran at (quoted peaks assume 2.4 GHz)
         out["roofline"]["mfma_busy_per_simd"] = pv["syrk_fc2_mfma_busy_per_simd"]
         out["roofline"]["clock_ghz_under_load"] = pv.get("syrk_fc2_clock_ghz")
-    # The bound the kernel actually meets: its operand stream from L2 into
-    # LDS.  Every upper 256 x 256 tile loads both 256-channel panels (2 x 256
-    # x 2 bytes per token), 1/64 byte per multiply-add; at full MFMA rate a
-    # CU would need 32 bytes per clock, while the L2-to-CU path sustains
-    # about 20 (loads alone, no MFMAs, take 54 ms of the 62).
+    # The operand stream from L2 into LDS: every upper 256 x 256 tile loads
+    # both 256-channel panels (2 x 256 x 2 bytes per token), 1/64 byte per
+    # multiply-add; at full MFMA rate a CU would need 32 bytes per clock.
+    # The kernel's wavefronts spend about 40 % of their cycles waiting for
+    # these loads at the end of each stage (hipBLASLt's 256 x 256 kernel on
+    # the same operand streams 28.8 B/clk/CU at 90 % MFMA busy).
     nt = (Cfc2 + 255) // 256
     sbytes = nt * (nt + 1) // 2 * 2 * 256 * 2 * T
     stream = {"bytes": sbytes, "achieved_TB_s": round(sbytes / t_launch / 1e12, 2)}
