@@ -370,16 +370,24 @@ __device__ __forceinline__ void xt_load(uint16_t* buf, int stage, int wave, int 
 // quarter of every stage with direct-to-LDS buffer loads (L2 straight into
 // LDS, no VGPR round trip, no loader wavefronts, so each wavefront may use
 // 256 registers).  During stage c a wavefront issues its 8 loads of stage
-// c + 1, one after each 16-row A fragment of the stage's first 32-token
-// slice (between the MFMAs: a burst of 64 loads per CU at the top of the
-// stage held the wavefronts in VMEM issue), into the buffer every
-// wavefront finished reading at the barrier that ended stage c - 1; each
-// wavefront waits for its own loads (vmcnt(0)) before the barrier that
-// ends stage c.  In the last stage the loads repeat stage nch - 1 into the
-// other buffer, which is not read again, so every stage issues the same 8
-// loads without a branch.  The next A fragment is read before the current
-// one's MFMAs, and a scheduling barrier after each fragment's group keeps
-// that order.
+// c + 1, one after each 16-row A fragment group of the stage's first
+// 32-token slice (between the MFMAs: a burst of 64 loads per CU at the top
+// of the stage held the wavefronts in VMEM issue), into the buffer every
+// wavefront finished reading at the barrier of stage c - 1.  In the last
+// stage the loads repeat stage nch - 1 into the other buffer, which is not
+// read again, so every stage issues the same 8 loads without a branch.
+// Operand reads run one step ahead of the MFMAs that use them:
+//  * the next A fragment is read before the current one's 4 MFMAs;
+//  * the second slice's B fragments and first A fragment are read during
+//    the first slice's last A group;
+//  * the stage's barrier sits before its last A group: every operand read
+//    of stage c has been issued and waited for by then (the barrier waits
+//    for LDS), each wavefront first waits for its own loads of stage c + 1
+//    (vmcnt(0)), and after the barrier the first fragments of stage c + 1
+//    are read while the last 4 MFMAs of stage c run from registers.
+// A scheduling barrier after each group keeps that order.  Every
+// accumulator receives the same MFMAs in the same order as a plain stage
+// loop, so the sums are bitwise those of one.
 // Requires Cp = nt * 256 rows in Xt, ldt, span and tpad multiples of KQ, and
 // 256 * ldt * 2 < 2^31 (a tile's panel is addressed with 32-bit offsets).
 template <typename T8>
@@ -410,39 +418,63 @@ __global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __res
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
   const int r16 = lane & 15;
+  // rows wm + 16i + r16 and wn + 16j + r16 share r16's low 3 bits: the
+  // slot of each slice's chunk is the same for every fragment of the lane
+  const int sl0 = xt_slot(lane >> 4, r16) * 8, sl1 = xt_slot((lane >> 4) + 4, r16) * 8;
   if (nch > 0) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) xt_load(&Xs[0][0][0][0], 0, wave, k, rs0, rs1, voff, gstep);
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  sync_lds();
-  for (int c = 0; c < nch; ++c) {
-    const int nxt = c + 1 < nch ? c + 1 : nch - 1;     // stage loaded during this one
-    uint16_t* nbuf = &Xs[(c + 1) & 1][0][0][0];
-    const uint16_t (*XA)[KQ] = Xs[c & 1][0];
-    const uint16_t (*XB)[KQ] = Xs[c & 1][1];
-#pragma unroll
-    for (int h = 0; h < KQ / 32; ++h) {
-      // rows wm + 16i + r16 and wn + 16j + r16 share r16's low 3 bits
-      const int slot = xt_slot((lane >> 4) + 4 * h, r16) * 8;
-      T8 bb[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bb[j] = *(const T8*)&XB[wn + j * 16 + r16][slot];
-      T8 an = *(const T8*)&XA[wm + r16][slot];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const T8 a = an;
-        if (i < 7) an = *(const T8*)&XA[wm + (i + 1) * 16 + r16][slot];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T8>(a, bb[j], acc[i][j]);
-        if (h == 0) {
-          xt_load(nbuf, nxt, wave, i, rs0, rs1, voff, gstep);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     sync_lds();
+    T8 bb[4], bbn[4], an;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bb[j] = *(const T8*)&Xs[0][1][wn + j * 16 + r16][sl0];
+    an = *(const T8*)&Xs[0][0][wm + r16][sl0];
+    for (int c = 0; c < nch; ++c) {
+      const int nxt = c + 1 < nch ? c + 1 : nch - 1;     // stage loaded during this one
+      uint16_t* nbuf = &Xs[(c + 1) & 1][0][0][0];
+      const uint16_t (*XA)[KQ] = Xs[c & 1][0];
+      const uint16_t (*XB)[KQ] = Xs[c & 1][1];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {                     // slice 0, loads in between
+        const T8 a = an;
+        if (i < 7) {
+          an = *(const T8*)&XA[wm + (i + 1) * 16 + r16][sl0];
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bbn[j] = *(const T8*)&XB[wn + j * 16 + r16][sl1];
+          an = *(const T8*)&XA[wm + r16][sl1];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T8>(a, bb[j], acc[i][j]);
+        xt_load(nbuf, nxt, wave, i, rs0, rs1, voff, gstep);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bb[j] = bbn[j];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {                     // slice 1, the barrier before group 7
+        const T8 a = an;
+        if (i < 7) an = *(const T8*)&XA[wm + (i + 1) * 16 + r16][sl1];
+        if (i == 7 && c + 1 < nch) {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          sync_lds();
+          const uint16_t (*NA)[KQ] = Xs[(c + 1) & 1][0];
+          const uint16_t (*NB)[KQ] = Xs[(c + 1) & 1][1];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bbn[j] = *(const T8*)&NB[wn + j * 16 + r16][sl0];
+          an = *(const T8*)&NA[wm + r16][sl0];
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T8>(a, bb[j], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bb[j] = bbn[j];
+    }
+    // the last stage's repeated loads land in the unread buffer
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   const int c16 = lane & 15, r4 = (lane >> 4) * 4;
   // split 0 adds into S, split s > 0 writes P[s - 1]; k_sum_splits then
