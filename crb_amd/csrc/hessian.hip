@@ -370,37 +370,43 @@ __device__ __forceinline__ void xt_load(uint16_t* buf, int stage, int wave, int 
 // quarter of every stage with direct-to-LDS buffer loads (L2 straight into
 // LDS, no VGPR round trip, no loader wavefronts, so each wavefront may use
 // 256 registers).  During stage c a wavefront issues its 8 loads of stage
-// c + 1, one after each 16-row A fragment group of the stage's first
-// 32-token slice (between the MFMAs: a burst of 64 loads per CU at the top
-// of the stage held the wavefronts in VMEM issue), into the buffer every
-// wavefront finished reading at the barrier of stage c - 1.  In the last
-// stage the loads repeat stage nch - 1 into the other buffer, which is not
-// read again, so every stage issues the same 8 loads without a branch.
-// Operand reads run one step ahead of the MFMAs that use them:
-//  * the next A fragment is read before the current one's 4 MFMAs;
-//  * the second slice's B fragments and first A fragment are read during
-//    the first slice's last A group;
-//  * the stage's barrier sits before its last A group: every operand read
-//    of stage c has been issued and waited for by then (the barrier waits
-//    for LDS), each wavefront first waits for its own loads of stage c + 1
-//    (vmcnt(0)), and after the barrier the first fragments of stage c + 1
-//    are read while the last 4 MFMAs of stage c run from registers.
-// A scheduling barrier after each group keeps that order.  Every
-// accumulator receives the same MFMAs in the same order as a plain stage
-// loop, so the sums are bitwise those of one.
+// c + 1, one after each 16-row A fragment of the stage's first 32-token
+// slice (between the MFMAs: a burst of 64 loads per CU at the top of the
+// stage held the wavefronts in VMEM issue), into the buffer every
+// wavefront finished reading at the barrier that ended stage c - 1; each
+// wavefront waits for its own loads (vmcnt(0)) before the barrier that
+// ends stage c.  In the last stage the loads repeat stage nch - 1 into the
+// other buffer, which is not read again, so every stage issues the same 8
+// loads without a branch.  The next A fragment is read before the current
+// one's MFMAs, and a scheduling barrier after each fragment's group keeps
+// that order.
 // Requires Cp = nt * 256 rows in Xt, ldt, span and tpad multiples of KQ, and
 // 256 * ldt * 2 < 2^31 (a tile's panel is addressed with 32-bit offsets).
-template <typename T8>
-__global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __restrict__ Xt,
-                                                           int64_t ldt, int64_t tpad, int C,
-                                                           float* S, int64_t lds, int nt,
-                                                           int64_t span, float* P) {
-  __shared__ __attribute__((aligned(1024))) uint16_t Xs[2][2][ST][KQ];   // [buffer][side]
-  int ti, tj;
-  tile_band(xcd_chunk(blockIdx.x, gridDim.x), nt, ti, tj);
-  const int64_t k_beg = (int64_t)blockIdx.y * span;
-  const int64_t k_end = k_beg + span < tpad ? k_beg + span : tpad;
-  const int nch = k_end > k_beg ? (int)((k_end - k_beg) / KQ) : 0;
+//
+// Pacing (THR, the persistent kernel): the workgroups of one XCD share
+// their operand panels through that XCD's L2, but drift apart by more
+// stages than the L2 holds (a panel line read by one is gone before the
+// next asks for it).  Each workgroup adds 1 to its XCD's stage counter at
+// the top of every stage (a returning atomic in the XCD's L2, workgroup
+// scope: every workgroup that uses the counter runs on that XCD) and, at
+// the end of the stage, lets stage g start only once the counter reaches
+// nwx * (g - lag): no workgroup runs more than lag stages ahead of the
+// XCD's slowest.  (The add's result is awaited right away; issuing it as
+// assembly awaited only at the stage end measured slower, 61 against
+// 59.6 ms on the fc2 shape, with occasional 68 ms runs.)  The wait is bounded (maxspin polls), so it is a pace and
+// never a dependence: results do not depend on it.
+struct SyrkPace {
+  unsigned* ctr;     // the XCD's stage counter
+  unsigned nwx;      // workgroups counted on the XCD
+  int lag, maxspin;
+  unsigned g;        // paced stages this workgroup has finished
+  bool on;           // pace this tile (uniform over the workgroup)
+};
+
+template <typename T8, bool THR>
+__device__ __forceinline__ void syrk_tile(uint16_t (*Xs)[2][ST][KQ], const uint16_t* Xt,
+                                          int64_t ldt, int ti, int tj, int64_t k_beg, int nch,
+                                          f4_t (&acc)[8][4], SyrkPace& pc) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -412,75 +418,70 @@ __global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __res
   const int voff = (lr * (int)ldt + xt_slot(lane & 7, lr) * 8) * 2;
   const int gstep = 8 * (int)ldt * 2;
   const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
-  f4_t acc[8][4];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
   const int r16 = lane & 15;
-  // rows wm + 16i + r16 and wn + 16j + r16 share r16's low 3 bits: the
-  // slot of each slice's chunk is the same for every fragment of the lane
-  const int sl0 = xt_slot(lane >> 4, r16) * 8, sl1 = xt_slot((lane >> 4) + 4, r16) * 8;
   if (nch > 0) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) xt_load(&Xs[0][0][0][0], 0, wave, k, rs0, rs1, voff, gstep);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    sync_lds();
-    T8 bb[4], bbn[4], an;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  sync_lds();
+  for (int c = 0; c < nch; ++c) {
+    unsigned snap = 0;
+    if (THR && pc.on && tid == 0)
+      snap = __hip_atomic_fetch_add(pc.ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const int nxt = c + 1 < nch ? c + 1 : nch - 1;     // stage loaded during this one
+    uint16_t* nbuf = &Xs[(c + 1) & 1][0][0][0];
+    const uint16_t (*XA)[KQ] = Xs[c & 1][0];
+    const uint16_t (*XB)[KQ] = Xs[c & 1][1];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bb[j] = *(const T8*)&Xs[0][1][wn + j * 16 + r16][sl0];
-    an = *(const T8*)&Xs[0][0][wm + r16][sl0];
-    for (int c = 0; c < nch; ++c) {
-      const int nxt = c + 1 < nch ? c + 1 : nch - 1;     // stage loaded during this one
-      uint16_t* nbuf = &Xs[(c + 1) & 1][0][0][0];
-      const uint16_t (*XA)[KQ] = Xs[c & 1][0];
-      const uint16_t (*XB)[KQ] = Xs[c & 1][1];
+    for (int h = 0; h < KQ / 32; ++h) {
+      // rows wm + 16i + r16 and wn + 16j + r16 share r16's low 3 bits
+      const int slot = xt_slot((lane >> 4) + 4 * h, r16) * 8;
+      T8 bb[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {                     // slice 0, loads in between
+      for (int j = 0; j < 4; ++j) bb[j] = *(const T8*)&XB[wn + j * 16 + r16][slot];
+      T8 an = *(const T8*)&XA[wm + r16][slot];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
         const T8 a = an;
-        if (i < 7) {
-          an = *(const T8*)&XA[wm + (i + 1) * 16 + r16][sl0];
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) bbn[j] = *(const T8*)&XB[wn + j * 16 + r16][sl1];
-          an = *(const T8*)&XA[wm + r16][sl1];
-        }
+        if (i < 7) an = *(const T8*)&XA[wm + (i + 1) * 16 + r16][slot];
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T8>(a, bb[j], acc[i][j]);
-        xt_load(nbuf, nxt, wave, i, rs0, rs1, voff, gstep);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bb[j] = bbn[j];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {                     // slice 1, the barrier before group 7
-        const T8 a = an;
-        if (i < 7) an = *(const T8*)&XA[wm + (i + 1) * 16 + r16][sl1];
-        if (i == 7 && c + 1 < nch) {
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-          sync_lds();
-          const uint16_t (*NA)[KQ] = Xs[(c + 1) & 1][0];
-          const uint16_t (*NB)[KQ] = Xs[(c + 1) & 1][1];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) bbn[j] = *(const T8*)&NB[wn + j * 16 + r16][sl0];
-          an = *(const T8*)&NA[wm + r16][sl0];
+        if (h == 0) {
+          xt_load(nbuf, nxt, wave, i, rs0, rs1, voff, gstep);
           __builtin_amdgcn_sched_barrier(0);
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T8>(a, bb[j], acc[i][j]);
-        __builtin_amdgcn_sched_barrier(0);
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bb[j] = bbn[j];
     }
-    // the last stage's repeated loads land in the unread buffer
+    // the pace check overlaps this wavefront's loads still in flight
+    if (THR && pc.on && tid == 0) {
+      ++pc.g;
+      const unsigned need = pc.g > (unsigned)pc.lag ? pc.nwx * (pc.g - pc.lag) : 0u;
+      unsigned seen = snap + 1u;
+      for (int it = 0; seen < need && it < pc.maxspin; ++it) {
+        __builtin_amdgcn_s_sleep(1);
+        seen = __hip_atomic_fetch_add(pc.ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    sync_lds();
   }
+}
+
+// tile (split 0 adds into S, split s > 0 writes P[s - 1]; k_sum_splits then
+// adds P[0..] in split order, so S + acc_0 + acc_1 + ... either way)
+__device__ __forceinline__ void syrk_store(const f4_t (&acc)[8][4], int ti, int tj, int C,
+                                           float* S, int64_t lds, float* P, int split) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
   const int c16 = lane & 15, r4 = (lane >> 4) * 4;
-  // split 0 adds into S, split s > 0 writes P[s - 1]; k_sum_splits then
-  // adds P[0..] in split order, so S + acc_0 + acc_1 + ... either way
-  const bool part = P && blockIdx.y > 0;
-  float* out = part ? P + (size_t)(blockIdx.y - 1) * (size_t)C * lds : S;
+  const bool part = P && split > 0;
+  float* out = part ? P + (size_t)(split - 1) * (size_t)C * lds : S;
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -494,6 +495,111 @@ __global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __res
           *q = part ? acc[i][j][r] : *q + acc[i][j][r];
         }
       }
+}
+
+// One workgroup per (tile, split): grid (tiles, splits).
+template <typename T8>
+__global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __restrict__ Xt,
+                                                           int64_t ldt, int64_t tpad, int C,
+                                                           float* S, int64_t lds, int nt,
+                                                           int64_t span, float* P) {
+  __shared__ __attribute__((aligned(1024))) uint16_t Xs[2][2][ST][KQ];   // [buffer][side]
+  int ti, tj;
+  tile_band(xcd_chunk(blockIdx.x, gridDim.x), nt, ti, tj);
+  const int64_t k_beg = (int64_t)blockIdx.y * span;
+  const int64_t k_end = k_beg + span < tpad ? k_beg + span : tpad;
+  const int nch = k_end > k_beg ? (int)((k_end - k_beg) / KQ) : 0;
+  f4_t acc[8][4];
+  SyrkPace pc{nullptr, 0u, 0, 0, 0u, false};
+  syrk_tile<T8, false>(Xs, Xt, ldt, ti, tj, k_beg, nch, acc, pc);
+  syrk_store(acc, ti, tj, C, S, lds, P, blockIdx.y);
+}
+
+// Control words of the persistent SYRK, one 256-byte line each, zeroed
+// before every launch: per XCD a stage counter (pacing), an item claim
+// counter and an arrival counter.
+constexpr int PCTL_LINE = 64;                                  // u32 per line
+constexpr size_t PCTL_BYTES = (size_t)3 * 8 * PCTL_LINE * sizeof(unsigned);
+constexpr int PACE_LAG = 4;
+constexpr int PACE_MAXSPIN = 64;
+// above any need (up to 63 workgroups per XCD x 2^20 paced stages), and
+// 63 of them plus the stage counts stay below 2^32
+constexpr unsigned PACE_RETIRE = 1u << 26;
+
+__global__ void k_zero_u32(unsigned* p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
+// Persistent SYRK: about one workgroup per CU.  The work items (tile,
+// split) are listed per XCD as the launched grid assigns them (the
+// xcd_chunk range of tile indices of XCD x, split by split); a workgroup
+// claims the next item of its own XCD's list (hardware register XCC_ID)
+// with an atomic counter and, when that list is empty, items of the other
+// lists, so every item runs exactly once wherever the workgroups land.
+// The workgroups of an XCD are paced (SyrkPace) so that those working on a
+// 4 x 8 block of tiles read the same operand lines while they are in L2.
+template <typename T8>
+__global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k_pers(
+    const uint16_t* __restrict__ Xt, int64_t ldt, int64_t tpad, int C, float* S, int64_t lds,
+    int nt, int64_t span, int ns, float* P, unsigned* ctl) {
+  __shared__ __attribute__((aligned(1024))) uint16_t Xs[2][2][ST][KQ];
+  __shared__ int bcast[2];
+  int xx;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xx));
+  const int x = xx & 7;
+  const int ntiles = nt * (nt + 1) / 2;
+  const int q = ntiles / 8, r = ntiles % 8;
+  unsigned* ctr = ctl + x * PCTL_LINE;
+  unsigned* claim = ctl + 8 * PCTL_LINE;
+  unsigned* arrive = ctl + 16 * PCTL_LINE + x * PCTL_LINE;
+  if (threadIdx.x == 0) {
+    // the XCD's workgroups that started with this one: counted after a
+    // short settle time (workgroups that start later are not waited for)
+    __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __builtin_amdgcn_s_sleep(127);
+    __builtin_amdgcn_s_sleep(127);
+    bcast[1] = (int)__hip_atomic_fetch_add(arrive, 0u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  __syncthreads();
+  SyrkPace pc{ctr, (unsigned)bcast[1], PACE_LAG, PACE_MAXSPIN, 0u, false};
+  // Only the full rounds of the own list are paced: a workgroup leaves the
+  // pace for good (adding PACE_RETIRE, above any stage count a paced
+  // workgroup can need, so it never holds one back) when it first takes a
+  // tile of its list's last round or of another XCD's list.
+  bool pacing = true;
+  int xs = x;                                    // list being drained
+  for (int lists = 0; lists < 8;) {
+    const int lin0 = xs < r ? xs * (q + 1) : r * (q + 1) + (xs - r) * q;
+    const int nl = xs < r ? q + 1 : q;
+    if (threadIdx.x == 0)
+      bcast[0] = (int)__hip_atomic_fetch_add(claim + xs * PCTL_LINE, 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int it = bcast[0];
+    __syncthreads();
+    const bool paced = pacing && xs == x && it + (int)pc.nwx < nl * ns;
+    if (pacing && !paced) {
+      pacing = false;
+      if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(ctr, PACE_RETIRE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    if (it >= nl * ns) {
+      ++lists;
+      xs = (xs + 1) & 7;
+      continue;
+    }
+    const int split = it / nl;
+    int ti, tj;
+    tile_band(lin0 + it % nl, nt, ti, tj);
+    const int64_t k_beg = (int64_t)split * span;
+    const int64_t k_end = k_beg + span < tpad ? k_beg + span : tpad;
+    const int nch = k_end > k_beg ? (int)((k_end - k_beg) / KQ) : 0;
+    f4_t acc[8][4];
+    pc.on = paced;
+    syrk_tile<T8, true>(Xs, Xt, ldt, ti, tj, k_beg, nch, acc, pc);
+    syrk_store(acc, ti, tj, C, S, lds, P, split);
+  }
 }
 
 // S[i][j] += sum_s P[s][i][j] in split order, upper triangle.  Grid: x =
@@ -771,22 +877,50 @@ namespace crbq {
 // [ntok, tpad) zero, tpad a multiple of KQ, ldt >= tpad): token splits
 // chosen by the cost model within the partial-tile capacity pcap, split 0
 // adding into S and the others summed after it in split order.
+// Channel counts from which the persistent paced SYRK is used (its
+// control words at the end of the workspace): the fc2-sized inputs, whose
+// SYRK fills the GPU for tens of milliseconds.  Smaller SYRKs keep the
+// launched grid, whose short workgroups leave CUs to other streams' work.
+constexpr int64_t PERS_MIN_C = 8192;
+static size_t syrk_ctl_bytes(int64_t C) { return C >= PERS_MIN_C ? PCTL_BYTES + 256 : 0; }
+
 static int syrk_xt(const uint16_t* Xt, int64_t ldt, int64_t tpad, int64_t C, float* S,
                    int64_t lds, float* Pbuf, size_t pcap, int dtype, hipStream_t s) {
   const int nt = (int)((C + ST - 1) / ST);
   const int64_t ntiles = (int64_t)nt * (nt + 1) / 2;
+  // control words of the persistent kernel at the end of the workspace
+  unsigned* ctl = nullptr;
+  if (C >= PERS_MIN_C && Pbuf && pcap >= syrk_ctl_bytes(C)) {
+    const uintptr_t end = (uintptr_t)Pbuf + pcap - PCTL_BYTES;
+    ctl = (unsigned*)(end & ~(uintptr_t)255);
+    pcap = (size_t)((uintptr_t)ctl - (uintptr_t)Pbuf);
+  }
   int ns = choose_splits(tpad, C, num_cus());
   while (ns > 1 && (size_t)ns * (size_t)C * (size_t)lds * sizeof(float) > pcap) --ns;
   int64_t span = (tpad + ns - 1) / ns;
   span = (span + KQ - 1) / KQ * KQ;
   ns = (int)((tpad + span - 1) / span);
   float* P = ns > 1 ? Pbuf : nullptr;
-  dim3 grid((unsigned)ntiles, (unsigned)ns);
+  if (ctl) {
+    k_zero_u32<<<1, 256, 0, s>>>(ctl, (int)(PCTL_BYTES / sizeof(unsigned)));
+    CRBQ_LAUNCH_CHECK();
+  }
   SyrkTimer tm(s, C);
-  if (dtype == CRBQ_F16)
-    k_syrk16k<h8_t><<<grid, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt, span, P);
-  else
-    k_syrk16k<b8_t><<<grid, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt, span, P);
+  if (ctl) {
+    const unsigned nwg = (unsigned)num_cus();
+    if (dtype == CRBQ_F16)
+      k_syrk16k_pers<h8_t><<<nwg, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt,
+                                                         span, ns, P, ctl);
+    else
+      k_syrk16k_pers<b8_t><<<nwg, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt,
+                                                         span, ns, P, ctl);
+  } else {
+    dim3 grid((unsigned)ntiles, (unsigned)ns);
+    if (dtype == CRBQ_F16)
+      k_syrk16k<h8_t><<<grid, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt, span, P);
+    else
+      k_syrk16k<b8_t><<<grid, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt, span, P);
+  }
   CRBQ_LAUNCH_CHECK();
   tm.stop(s);
   if (P) {
@@ -803,7 +937,8 @@ extern "C" size_t crbq_hessian_workspace_size(int64_t ntok, int64_t C) {
   const crbq::XtPlan pl = crbq::xt_plan(ntok, C);
   const int64_t tpad = (pl.tch + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
   const int ns = crbq::choose_splits(tpad, C, crbq::num_cus());
-  return pl.xt_bytes + (ns > 1 ? (size_t)ns * (size_t)C * (size_t)C * sizeof(float) : 0);
+  return pl.xt_bytes + (ns > 1 ? (size_t)ns * (size_t)C * (size_t)C * sizeof(float) : 0) +
+         crbq::syrk_ctl_bytes(C);
 }
 
 extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_t ldx,
@@ -918,7 +1053,8 @@ extern "C" size_t crbq_hessian_cm_workspace_size(int64_t ntok, int64_t C) {
   if (ntok <= 0 || C <= 0) return 0;
   const int64_t tpad = (ntok + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
   const int ns = crbq::choose_splits(tpad, C, crbq::num_cus());
-  return ns > 1 ? (size_t)ns * (size_t)C * (size_t)C * sizeof(float) : 0;
+  return (ns > 1 ? (size_t)ns * (size_t)C * (size_t)C * sizeof(float) : 0) +
+         crbq::syrk_ctl_bytes(C);
 }
 
 extern "C" int crbq_hessian_accum_cm(const void* Xt, int dtype, int64_t ntok, int64_t ldt,

@@ -272,6 +272,45 @@ def test_hessian_channel_major_store(dtype, C, chunks):
     assert rel(torch.triu(S1), torch.triu(want)) < 1e-5
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("T,C", [(2048, 8192), (1000, 8300), (16384, 8192)])
+def test_hessian_persistent_paced(dtype, T, C):
+    """From 8192 channels the SYRK runs as the persistent, XCD-paced kernel
+    (items claimed per XCD, control words at the end of the workspace).
+    Against float64 on the GPU; with one token split (T < 4096) bitwise
+    equal to the launched grid (a workspace without room for the control
+    words) and to the token-major path (NULL workspace), which issue the
+    same MFMAs per tile; with several splits, the same bits on a rerun."""
+    print(f"hessian persistent {dtype} T={T} C={C}", flush=True)
+    from crb_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator(device=DEV).manual_seed(T + C)
+    X = (torch.randn(T, C, device=DEV, generator=g) *
+         torch.exp(torch.randn(C, device=DEV, generator=g))).to(dtype)
+    full = lib.crbq_hessian_workspace_size(T, C)
+    S = torch.full((C, C), 0.5, device=DEV)
+    _accum_raw(X, S, full)
+    Xd = X.double()
+    want = torch.triu(Xd.t() @ Xd + 0.5)
+    got = torch.triu(S.double())
+    assert float((got - want).norm() / want.norm()) < 1e-5
+    del want, got
+    xt_bytes = -(-C // 256) * 256 * (-(-T // 64) * 64) * 2
+    if T < 4096:
+        assert full > xt_bytes                  # room for the control words
+        for nb in (xt_bytes, 0):                # launched grid, token-major path
+            S2 = torch.full((C, C), 0.5, device=DEV)
+            _accum_raw(X, S2, nb)
+            torch.cuda.synchronize()
+            assert torch.equal(torch.triu(S2), torch.triu(S)), nb
+            del S2
+    else:
+        S2 = torch.full((C, C), 0.5, device=DEV)
+        _accum_raw(X, S2, full)
+        torch.cuda.synchronize()
+        assert torch.equal(torch.triu(S2), torch.triu(S))
+
+
 def test_hessian_matches_reference_add_batch():
     """Incremental rescale of bigptq.py:50-53 vs. one 2/n scaling."""
     print("hessian add_batch", flush=True)
