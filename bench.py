@@ -569,7 +569,7 @@ def cpu_baseline(nseq=32, nblocks=48, cfg1_gpu=None, cfg2=None):
 def syrk_compare(dev, ntok, reps=2):
     """The fc2 input's Hessian product two ways on the same data, for counter
     runs that compare them kernel by kernel: crbq_hessian_accum (transpose
-    into the channel-major copy + k_syrk16k over the upper triangle) and
+    into the channel-major copy + k_syrk16k_pers over the upper triangle) and
     hipBLASLt (torch.mm, fp16 in / fp32 accumulate / fp16 out) on the same
     channel-major operand, the full C x C product.  Each timed with events
     on the current stream; prints TFLOP/s of the symmetric half T C (C + 1)
@@ -713,7 +713,7 @@ def main():
                      "quantize_overlapped": round(pt.quantize_ms, 3),
                      "hinv": {g: round(v, 3) for g, v in pt.hinv_ms.items()},
                      "factor_plus_blocks": {g: round(v, 3) for g, v in pt.chain_ms.items()}},
-        "roofline": {"bound": "mfma", "kernel": "k_syrk16k (Hessian SYRK, fc2 input C=16384)",
+        "roofline": {"bound": "mfma", "kernel": "k_syrk16k_pers (Hessian SYRK, fc2 input C=16384)",
                      "achieved": round(achieved / 1e12, 2), "peak": PEAK_F16 / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_F16, 4),
                      "launch_ms": round(t_launch * 1e3, 3),
@@ -729,9 +729,9 @@ def main():
     # The operand stream from L2 into LDS: every upper 256 x 256 tile loads
     # both 256-channel panels (2 x 256 x 2 bytes per token), 1/64 byte per
     # multiply-add; at full MFMA rate a CU would need 32 bytes per clock.
-    # The kernel's wavefronts spend about 40 % of their cycles waiting for
-    # these loads at the end of each stage (hipBLASLt's 256 x 256 kernel on
-    # the same operand streams 28.8 B/clk/CU at 90 % MFMA busy).
+    # The chip holds 1.6-1.75 GHz under this stream (the kernel without its
+    # loads runs at 2.0 GHz); hipBLASLt's 256 x 256 kernel on the same
+    # operand streams 28.8 B/clk/CU at 90 % MFMA busy and 1.46 GHz.
     nt = (Cfc2 + 255) // 256
     sbytes = nt * (nt + 1) // 2 * 2 * 256 * 2 * T
     stream = {"bytes": sbytes, "achieved_TB_s": round(sbytes / t_launch / 1e12, 2)}
