@@ -17,7 +17,9 @@
 //   X22 = chol_inv(A22)                     (recursively)
 //   X21 = -X22 A21
 // so X = [X11 0; X21 X22] = L'^-1 overwrites A.  Blocks of NB or fewer
-// rows are factored and inverted by one workgroup (k_chol_inv_diag).  About
+// rows are factored and inverted by one workgroup (k_chol_inv_diag), nodes
+// of up to 2 NB rows, all five steps, by one workgroup too
+// (k_chol_inv_node).  About
 // 3/4 of the 2C^3/3 flops are in the four products of the top level,
 // which run as large fp32 MFMA GEMMs; the triangular factors' zero halves
 // are skipped.  The upper triangle of A is kept at zero so the triangular
@@ -467,47 +469,54 @@ __device__ __forceinline__ bool block64(DiagSmem& sm, int o, int wv, int lane, i
   return true;
 }
 
-__global__ __launch_bounds__(256) void k_chol_inv_diag(float* A, int64_t lda, int off, int bj,
-                                                       int* info) {
-  if (*info) return;
-  __shared__ DiagSmem sm;
-  // the wavefront index as a scalar, so branches on it are uniform
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool vec = ((lda & 3) == 0) && ((((uintptr_t)A) & 15) == 0) && ((off & 3) == 0);
-  // ---- load the block (lower triangle), identity padding, zero above;
-  // 16 coalesced 4-float groups per thread, all in flight together
-  {
-    float v[16][4];
+// Load the bj x bj diagonal block at (off, off) into sm.Ls: lower triangle,
+// identity padding, zero above; 16 coalesced 4-float groups per thread,
+// all in flight together.  Ends with a barrier.
+__device__ __forceinline__ void diag_load(DiagSmem& sm, const float* A, int64_t lda, int off,
+                                          int bj, bool vec) {
+  const int tid = threadIdx.x;
+  float v[16][4];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int f = tid + 256 * u, i = f >> 5, j0 = (f & 31) * 4;
-      const float* src = A + (int64_t)(off + i) * lda + off + j0;
-      if (vec && i < bj && j0 + 3 < bj) {
-        const float4 q = *(const float4*)src;
-        v[u][0] = q.x; v[u][1] = q.y; v[u][2] = q.z; v[u][3] = q.w;
-      } else {
+  for (int u = 0; u < 16; ++u) {
+    const int f = tid + 256 * u, i = f >> 5, j0 = (f & 31) * 4;
+    const float* src = A + (int64_t)(off + i) * lda + off + j0;
+    if (vec && i < bj && j0 + 3 < bj) {
+      const float4 q = *(const float4*)src;
+      v[u][0] = q.x; v[u][1] = q.y; v[u][2] = q.z; v[u][3] = q.w;
+    } else {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v[u][c] = (i < bj && j0 + c < bj) ? src[c] : 0.f;
-      }
+      for (int c = 0; c < 4; ++c) v[u][c] = (i < bj && j0 + c < bj) ? src[c] : 0.f;
     }
+  }
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int f = tid + 256 * u, i = f >> 5, j0 = (f & 31) * 4;
+  for (int u = 0; u < 16; ++u) {
+    const int f = tid + 256 * u, i = f >> 5, j0 = (f & 31) * 4;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int j = j0 + c;
-        sm.Ls[i][j] = (i < bj && j <= i) ? v[u][c] : (i == j ? 1.f : 0.f);
-      }
+    for (int c = 0; c < 4; ++c) {
+      const int j = j0 + c;
+      sm.Ls[i][j] = (i < bj && j <= i) ? v[u][c] : (i == j ? 1.f : 0.f);
     }
   }
   if (tid == 0) sm.fail = 0;
   __syncthreads();
-  // ---- X = L^-1 over the block (L is not kept)
-  if (!block64(sm, 0, w, lane, off, bj, info)) return;
+}
+
+// X = L^-1 of the block in sm.Ls (L is not kept).  Returns false after a
+// bad pivot (uniformly; *info is set).
+__device__ __forceinline__ bool diag_core(DiagSmem& sm, int w, int lane, int off, int bj,
+                                          int* info) {
+  if (!block64(sm, 0, w, lane, off, bj, info)) return false;
   level_panel<64>(sm, 0, w, lane);
-  if (!block64(sm, 64, w, lane, off, bj, info)) return;
+  if (!block64(sm, 64, w, lane, off, bj, info)) return false;
   level_x21<64>(sm, 0, w, lane);
-  // ---- write X (zero above the diagonal), 16-byte stores where aligned
+  return true;
+}
+
+// Write X (zero above the diagonal) back to the block, 16-byte stores where
+// aligned.
+__device__ __forceinline__ void diag_store(const DiagSmem& sm, float* A, int64_t lda, int off,
+                                           int bj, bool vec) {
+  const int tid = threadIdx.x;
 #pragma unroll
   for (int u = 0; u < 16; ++u) {
     const int f = tid + 256 * u, i = f >> 5, j0 = (f & 31) * 4;
@@ -522,6 +531,196 @@ __global__ __launch_bounds__(256) void k_chol_inv_diag(float* A, int64_t lda, in
       for (int c = 0; c < 4; ++c)
         if (i < bj && j0 + c < bj) dst[c] = q[c];
     }
+  }
+}
+
+__device__ __forceinline__ bool diag_vec(const float* A, int64_t lda, int off) {
+  return ((lda & 3) == 0) && ((((uintptr_t)A) & 15) == 0) && ((off & 3) == 0);
+}
+
+__global__ __launch_bounds__(256) void k_chol_inv_diag(float* A, int64_t lda, int off, int bj,
+                                                       int* info) {
+  if (*info) return;
+  __shared__ DiagSmem sm;
+  // the wavefront index as a scalar, so branches on it are uniform
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool vec = diag_vec(A, lda, off);
+  diag_load(sm, A, lda, off, bj, vec);
+  if (!diag_core(sm, w, lane, off, bj, info)) return;
+  diag_store(sm, A, lda, off, bj, vec);
+}
+
+// A node of 129 to 256 rows in one workgroup: the recursion's five steps
+// for a split at m = 128 (n2 = n - 128 rows in the second half)
+//   X11 = chol_inv(A11)                     (diagonal block in LDS)
+//   T   = A21 X11^T                         (A21 staged in LDS, T over it)
+//   A22 -= T T^T, Q = T X11                 (Q over T; A22 loaded into the
+//                                            block buffer, S subtracted there)
+//   X22 = chol_inv(A22)
+//   X21 = -X22 Q                            (written over A21)
+// instead of five launches, each of which waits for a free CU when other
+// work holds them.  The products are 16 x 16 MFMA tiles over k in
+// ascending steps of 4 with the same operands as the GEMM launches they
+// replace (v_mfma_f32_16x16x4_f32, lane l supplying row l % 16 at k + l / 16)
+// and the same epilogues (T = acc, Q = acc, A22 = A22 - acc, X21 = -acc), so
+// X is bitwise what those launches give; the zero parts of the triangular
+// operands are skipped (exact zeros leave the sums unchanged).  Tiles go
+// to the 4 wavefronts in pairs of a short and a long K range (tile
+// columns or rows w and 7 - w), so every wavefront issues the same number
+// of MFMAs.
+struct NodeSmem {
+  DiagSmem d;                // the diagonal block (X11, then A22 / X22)
+  float P[NB][LDP];          // A21, then T, then Q
+};
+
+__global__ __launch_bounds__(256) void k_chol_inv_node(float* A, int64_t lda, int off, int n,
+                                                       int* info) {
+  if (*info) return;
+  __shared__ NodeSmem nm;
+  DiagSmem& sm = nm.d;
+  float (*P)[LDP] = nm.P;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lk = lane >> 4;
+  const int n2 = n - NB;                          // 1 .. 128
+  const bool vec = diag_vec(A, lda, off);
+  // ---- X11
+  diag_load(sm, A, lda, off, NB, vec);
+  if (!diag_core(sm, w, lane, off, NB, info)) return;
+  diag_store(sm, A, lda, off, NB, vec);
+  // ---- A21 (n2 x 128) into P, zero rows past n2
+  float* A21 = A + (int64_t)(off + NB) * lda + off;
+  {
+    float v[16][4];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int f = tid + 256 * u, i = f >> 5, j0 = (f & 31) * 4;
+      const float* src = A21 + (int64_t)i * lda + j0;
+      if (vec && i < n2) {
+        const float4 q = *(const float4*)src;
+        v[u][0] = q.x; v[u][1] = q.y; v[u][2] = q.z; v[u][3] = q.w;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[u][c] = i < n2 ? src[c] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int f = tid + 256 * u, i = f >> 5, j0 = (f & 31) * 4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) P[i][j0 + c] = v[u][c];
+    }
+  }
+  __syncthreads();
+  // wavefront w's tile columns (T, Q) or rows (X21): w and 7 - w, 8 tiles each
+  const int ca = w, cb = 7 - w;
+  // ---- T = A21 X11^T: column tile j sums k < 16 (j + 1)
+  {
+    f4_t ta[8], tb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { ta[i] = f4_t{0.f, 0.f, 0.f, 0.f}; tb[i] = ta[i]; }
+    const int ka = 16 * (ca + 1), kb = 16 * (cb + 1);   // ka < kb
+    for (int k = 0; k < kb; k += 4) {
+      const float ba = sm.Ls[16 * ca + lr][k + lk], bb = sm.Ls[16 * cb + lr][k + lk];
+      float a[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = P[16 * i + lr][k + lk];
+      if (k < ka) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ta[i] = mfma4(a[i], ba, ta[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tb[i] = mfma4(a[i], bb, tb[i]);
+    }
+    __syncthreads();                              // every read of A21 done
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        P[16 * i + 4 * lk + r][16 * ca + lr] = ta[i][r];
+        P[16 * i + 4 * lk + r][16 * cb + lr] = tb[i][r];
+      }
+  }
+  __syncthreads();
+  // ---- S = T T^T (the 36 lower tiles, full K) and Q = T X11 (column tile j
+  // sums k >= 16 j)
+  f4_t sacc[9];
+  int si[9], sj[9];
+#pragma unroll
+  for (int q = 0; q < 9; ++q) {
+    lower_tile(w + 4 * q, si[q], sj[q]);
+    sacc[q] = f4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int k = 0; k < NB; k += 4) {
+#pragma unroll
+    for (int q = 0; q < 9; ++q)
+      sacc[q] = mfma4(P[16 * si[q] + lr][k + lk], P[16 * sj[q] + lr][k + lk], sacc[q]);
+  }
+  f4_t ua[8], ub[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { ua[i] = f4_t{0.f, 0.f, 0.f, 0.f}; ub[i] = ua[i]; }
+  {
+    const int ka = 16 * ca, kb = 16 * cb;         // start of the K range; ka < kb
+    for (int k = ka; k < NB; k += 4) {
+      const float ba = sm.Ls[k + lk][16 * ca + lr], bb = sm.Ls[k + lk][16 * cb + lr];
+      float a[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a[i] = P[16 * i + lr][k + lk];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ua[i] = mfma4(a[i], ba, ua[i]);
+      if (k >= kb) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ub[i] = mfma4(a[i], bb, ub[i]);
+      }
+    }
+  }
+  __syncthreads();                                // every read of T and X11 done
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      P[16 * i + 4 * lk + r][16 * ca + lr] = ua[i][r];
+      P[16 * i + 4 * lk + r][16 * cb + lr] = ub[i][r];
+    }
+  // ---- A22 - S into the block buffer (rows and columns past n2: identity
+  // padding, where S is 0), then X22
+  diag_load(sm, A, lda, off + NB, n2, vec);       // ends with a barrier
+#pragma unroll
+  for (int q = 0; q < 9; ++q)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int rr = 16 * si[q] + 4 * lk + r, cc = 16 * sj[q] + lr;
+      if (cc <= rr) sm.Ls[rr][cc] = sm.Ls[rr][cc] - sacc[q][r];
+    }
+  __syncthreads();
+  if (!diag_core(sm, w, lane, off + NB, n2, info)) return;
+  diag_store(sm, A, lda, off + NB, n2, vec);
+  // ---- X21 = -X22 Q: row tile i sums k < 16 (i + 1)
+  {
+    f4_t xa[8], xb[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { xa[j] = f4_t{0.f, 0.f, 0.f, 0.f}; xb[j] = xa[j]; }
+    const int ra = ca, rb = cb;
+    const int ka = 16 * (ra + 1), kb = 16 * (rb + 1);
+    for (int k = 0; k < kb; k += 4) {
+      const float aa = sm.Ls[16 * ra + lr][k + lk], ab = sm.Ls[16 * rb + lr][k + lk];
+      float b[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) b[j] = P[k + lk][16 * j + lr];
+      if (k < ka) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xa[j] = mfma4(aa, b[j], xa[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xb[j] = mfma4(ab, b[j], xb[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ia = 16 * ra + 4 * lk + r, ib = 16 * rb + 4 * lk + r, c = 16 * j + lr;
+        if (ia < n2) A21[(int64_t)ia * lda + c] = -xa[j][r];
+        if (ib < n2) A21[(int64_t)ib * lda + c] = -xb[j][r];
+      }
   }
 }
 
@@ -568,6 +767,11 @@ static int chol_inv_rec(float* A, int64_t lda, int o, int n, HinvWs& w, float* Q
                         hipStream_t s) {
   if (n <= NB) {
     k_chol_inv_diag<<<1, 256, 0, s>>>(A, lda, o, n, w.info);
+    CRBQ_LAUNCH_CHECK();
+    return CRBQ_OK;
+  }
+  if (n <= 2 * NB) {                  // split at NB: the whole node in one workgroup
+    k_chol_inv_node<<<1, 256, 0, s>>>(A, lda, o, n, w.info);
     CRBQ_LAUNCH_CHECK();
     return CRBQ_OK;
   }
