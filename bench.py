@@ -360,7 +360,7 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
         _, retries, fallback = kernels.hinv_upper_finish(jobs[-1])
         fl = 2.0 * Cf ** 3 / 3
         out["inverse_factor"][f"C{Cf}"] = {
-            "kernels": "k_chol_inv_diag + k_sgemm (recursive Cholesky-inverse)",
+            "kernels": "k_chol_inv_node + k_sgemm/k_sgemm2 (recursive Cholesky-inverse)",
             "ms": round(ms, 3), "achieved": round(fl / ms / 1e9, 1), "peak": PEAK_F32 / 1e12,
             "unit": "TFLOP/s", "frac": round(fl / ms / 1e9 / (PEAK_F32 / 1e12), 3),
             "retries": retries, "fallback": fallback}
