@@ -7,15 +7,22 @@
 // fp32 accumulate) computes the same sums up to summation order.  fp32
 // inputs use v_mfma_f32_16x16x4_f32.
 //
-// Each MFMA lane reads its 8 consecutive tokens with one ds_read_b128 from a
-// channel-major LDS stage (Xs[c][t]).  Two ways to get there from the
-// token-major activations X[t][c]:
-//  * channel-major path (k_xpose16 + k_syrk16k, used when the workspace can
-//    hold a transposed copy): X is transposed once into the workspace and
-//    the SYRK streams token-contiguous rows straight into LDS;
-//  * token-major path (k_syrk16p): a loading thread reads a 4-token x
+// Each MFMA lane needs 8 consecutive tokens of one channel.  Three ways to
+// get them from the token-major activations X[t][c]:
+//  * token-major stages (k_syrk16k / k_syrk16k_pers with TM, used when C is
+//    a multiple of 256 and X's rows are 16-byte aligned): 64-token stages of
+//    X go straight into LDS as they are (direct-to-LDS buffer loads), and
+//    the lanes read their operands with LDS transpose reads
+//    (ds_read_b64_tr_b16): no copy of X;
+//  * channel-major path (k_xpose16, then the same kernels on the copy, used
+//    for other channel counts when the workspace can hold a transposed
+//    copy): X is transposed once into the workspace and each lane reads its
+//    operand with one ds_read_b128;
+//  * in-place path (k_syrk16p): a loading thread reads a 4-token x
 //    8-channel unit with four 16-byte loads and transposes it in registers
 //    with v_perm_b32 before one 8-byte LDS store per channel.
+// The first two issue the same MFMAs on the same operands for the same
+// token splits, so their sums are bitwise equal.
 #include <stdlib.h>
 
 #include <atomic>
@@ -411,6 +418,30 @@ struct SyrkPace {
   bool on;           // pace this tile (uniform over the workgroup)
 };
 
+// Top of a paced stage: this workgroup's add to its XCD's stage counter
+// (the counter's value before it is returned to thread 0).
+template <bool THR>
+__device__ __forceinline__ unsigned pace_top(SyrkPace& pc, int tid) {
+  unsigned snap = 0;
+  if (THR && pc.on && tid == 0)
+    snap = __hip_atomic_fetch_add(pc.ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  return snap;
+}
+// End of a paced stage: thread 0 polls the counter until the XCD's slowest
+// workgroup is at most lag stages behind, or maxspin polls have passed.
+template <bool THR>
+__device__ __forceinline__ void pace_end(SyrkPace& pc, int tid, unsigned snap) {
+  if (THR && pc.on && tid == 0) {
+    ++pc.g;
+    const unsigned need = pc.g > (unsigned)pc.lag ? pc.nwx * (pc.g - pc.lag) : 0u;
+    unsigned seen = snap + 1u;
+    for (int it = 0; seen < need && it < pc.maxspin; ++it) {
+      __builtin_amdgcn_s_sleep(1);
+      seen = __hip_atomic_fetch_add(pc.ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
+}
+
 template <typename T8, bool THR>
 __device__ __forceinline__ void syrk_tile(uint16_t (*Xs)[2][ST][KQ], const uint16_t* Xt,
                                           int64_t ldt, int ti, int tj, int64_t k_beg, int nch,
@@ -438,9 +469,7 @@ __device__ __forceinline__ void syrk_tile(uint16_t (*Xs)[2][ST][KQ], const uint1
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   sync_lds();
   for (int c = 0; c < nch; ++c) {
-    unsigned snap = 0;
-    if (THR && pc.on && tid == 0)
-      snap = __hip_atomic_fetch_add(pc.ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const unsigned snap = pace_top<THR>(pc, tid);
     const int nxt = c + 1 < nch ? c + 1 : nch - 1;     // stage loaded during this one
     uint16_t* nbuf = &Xs[(c + 1) & 1][0][0][0];
     const uint16_t (*XA)[KQ] = Xs[c & 1][0];
@@ -466,15 +495,145 @@ __device__ __forceinline__ void syrk_tile(uint16_t (*Xs)[2][ST][KQ], const uint1
       }
     }
     // the pace check overlaps this wavefront's loads still in flight
-    if (THR && pc.on && tid == 0) {
-      ++pc.g;
-      const unsigned need = pc.g > (unsigned)pc.lag ? pc.nwx * (pc.g - pc.lag) : 0u;
-      unsigned seen = snap + 1u;
-      for (int it = 0; seen < need && it < pc.maxspin; ++it) {
-        __builtin_amdgcn_s_sleep(1);
-        seen = __hip_atomic_fetch_add(pc.ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    pace_end<THR>(pc, tid, snap);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    sync_lds();
+  }
+}
+
+// Token-major stages: the activations X[t][c] are staged as they are, with
+// no transposed copy.  An operand's stage is 64 token rows of its panel's
+// 256 channels (512 bytes per row, 32 16-byte chunks, chunk c in slot
+// c ^ tm_swz(t)); a wavefront's direct-to-LDS load fills two rows.  The MFMA
+// operands come from ds_read_b64_tr_b16, which gives lane j of a 16-lane
+// group, as its result q (q = 0..3), the 16-bit element j % 4 of the 8 bytes
+// addressed by lane 4q + j / 4 of the group.  With lane s of the group
+// addressing row t0 + s / 4 at channel RB + 4 (s % 4), lane j receives
+// channel RB + j at tokens t0 .. t0 + 3; reads at t0 and t0 + 4 give the 8
+// consecutive tokens of the MFMA operand layout, the values the
+// channel-major path reads with one ds_read_b128, so both paths issue the
+// same MFMAs on the same operands and their sums are bitwise equal.
+// tm_swz depends on bits 0, 1 and 3 of the row: the 8 rows one half of a
+// wavefront reads (bits 0-1 from the lane, bit 3 from its 16-lane group)
+// land on 8 distinct groups of 8 banks.
+__device__ __forceinline__ int tm_swz(int t) { return ((t & 3) | ((t >> 1) & 4)) << 1; }
+
+typedef __fp16 tr4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) tr4_t lds_tr4_t;
+
+// 8 tokens x 1 channel per lane (the MFMA operand) from a token-major stage:
+// p is this lane's byte address of its first 4-token read in LDS.
+template <typename T8>
+__device__ __forceinline__ T8 tm_frag(const char* p) {
+  typedef __attribute__((address_space(3))) const char lchar;
+  lchar* q = (lchar*)(const void*)p;
+  const tr4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr4_t*)(q));
+  const tr4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr4_t*)(q + 4 * ST * 2));
+  struct P { tr4_t a, b; } v{lo, hi};
+  return __builtin_bit_cast(T8, v);
+}
+
+// Descriptor of the stage of rows [t0, t0 + KQ) of panel pn of token-major
+// X: rows at or beyond ntok read as zeros (their offsets lie beyond nrec).
+__device__ __forceinline__ i4_t tm_rsrc(const uint16_t* X, int64_t ldx, int64_t t0,
+                                        int64_t ntok, int pn) {
+  int64_t rows = ntok - t0;
+  rows = rows < 0 ? 0 : (rows > KQ ? KQ : rows);
+  return xt_rsrc(X + t0 * ldx + (int64_t)pn * ST, (int)(rows * ldx * 2));
+}
+
+// Load k (0..7) of one wavefront's share of a token-major stage: rows
+// 2g, 2g + 1 (g = 4 wave + (k & 3)) of operand k >> 2.  Lane l fills slot
+// l & 31 of row 2g + (l >> 5), so it reads the chunk slot ^ tm_swz(row).
+// The row offset is part of the lane offset voff[k & 3] (the buffer range
+// check, which turns rows at or beyond ntok into zeros, covers the lane
+// offset).
+__device__ __forceinline__ void tm_load(uint16_t* buf, int wave, int k, i4_t rs0, i4_t rs1,
+                                        const int (&voff)[4]) {
+  const int g = wave * 4 + (k & 3);
+  const unsigned d = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)(buf + ((k >> 2) * KQ +
+                                                                              2 * g) * ST));
+  const i4_t rs = (k >> 2) ? rs1 : rs0;
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" :: "v"(voff[k & 3]), "s"(rs),
+               "{m0}"(d));
+}
+
+// syrk_tile on token-major X (row stride ldx, ntok valid rows; stages at
+// k_beg + 64 c): the same stage loop, loads and pacing, with token-major
+// stages.  Requires C a multiple of 256, X 16-byte aligned and ldx a
+// multiple of 8 below 2^24.
+template <typename T8, bool THR>
+__device__ __forceinline__ void syrk_tile_tm(uint16_t (*Xs)[2][ST][KQ], const uint16_t* X,
+                                             int64_t ldx, int64_t ntok, int ti, int tj,
+                                             int64_t k_beg, int nch, f4_t (&acc)[8][4],
+                                             SyrkPace& pc) {
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  // direct-to-LDS loads: lane -> (row lr of the pair, slot) -> source chunk
+  const int lr = lane >> 5, slot = lane & 31;
+  int voff[4];
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const int row = 2 * (wave * 4 + kk) + lr;
+    voff[kk] = (row * (int)ldx + (slot ^ tm_swz(row)) * 8) * 2;
+  }
+  // fragment reads: lane (group gq, s) addresses row 8 gq + s / 4 at
+  // channel RB + 4 (s % 4)
+  const int gq = lane >> 4, s = lane & 15;
+  const int trow = 8 * gq + (s >> 2);
+  const int fsw = tm_swz(trow);
+  const int wm = (wave >> 2) * 128, wn = (wave & 3) * 64;
+  int aoff[8], boff[4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int ch = wm + 16 * i + 4 * (s & 3);
+    aoff[i] = trow * ST * 2 + (((ch >> 3) ^ fsw) << 4) + (ch & 7) * 2;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int ch = wn + 16 * j + 4 * (s & 3);
+    boff[j] = (KQ + trow) * ST * 2 + (((ch >> 3) ^ fsw) << 4) + (ch & 7) * 2;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+  if (nch > 0) {
+    const i4_t r0 = tm_rsrc(X, ldx, k_beg, ntok, ti), r1 = tm_rsrc(X, ldx, k_beg, ntok, tj);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) tm_load(&Xs[0][0][0][0], wave, k, r0, r1, voff);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  sync_lds();
+  for (int c = 0; c < nch; ++c) {
+    const unsigned snap = pace_top<THR>(pc, tid);
+    const int nxt = c + 1 < nch ? c + 1 : nch - 1;     // stage loaded during this one
+    const int64_t tn = k_beg + (int64_t)nxt * KQ;
+    const i4_t r0 = tm_rsrc(X, ldx, tn, ntok, ti), r1 = tm_rsrc(X, ldx, tn, ntok, tj);
+    uint16_t* nbuf = &Xs[(c + 1) & 1][0][0][0];
+    const char* cur = (const char*)&Xs[c & 1][0][0][0];
+#pragma unroll
+    for (int h = 0; h < KQ / 32; ++h) {
+      const char* ch = cur + h * 32 * ST * 2;
+      T8 bb[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bb[j] = tm_frag<T8>(ch + boff[j]);
+      T8 an = tm_frag<T8>(ch + aoff[0]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const T8 a = an;
+        if (i < 7) an = tm_frag<T8>(ch + aoff[i + 1]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T8>(a, bb[j], acc[i][j]);
+        if (h == 0) {
+          tm_load(nbuf, wave, i, r0, r1, voff);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
+    pace_end<THR>(pc, tid, snap);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     sync_lds();
   }
@@ -505,12 +664,15 @@ __device__ __forceinline__ void syrk_store(const f4_t (&acc)[8][4], int ti, int 
       }
 }
 
-// One workgroup per (tile, split): grid (tiles, splits).
-template <typename T8>
-__global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __restrict__ Xt,
-                                                           int64_t ldt, int64_t tpad, int C,
-                                                           float* S, int64_t lds, int nt,
-                                                           int64_t span, float* P) {
+// One workgroup per (tile, split): grid (tiles, splits).  TM: X is the
+// token-major activation (ld its row stride, ntok valid rows); otherwise
+// the channel-major copy (ld its row stride, zero-padded to tpad tokens).
+template <typename T8, bool TM>
+__global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __restrict__ X,
+                                                           int64_t ld, int64_t ntok,
+                                                           int64_t tpad, int C, float* S,
+                                                           int64_t lds, int nt, int64_t span,
+                                                           float* P) {
   __shared__ __attribute__((aligned(1024))) uint16_t Xs[2][2][ST][KQ];   // [buffer][side]
   int ti, tj;
   tile_band(xcd_chunk(blockIdx.x, gridDim.x), nt, ti, tj);
@@ -519,7 +681,8 @@ __global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k(const uint16_t* __res
   const int nch = k_end > k_beg ? (int)((k_end - k_beg) / KQ) : 0;
   f4_t acc[8][4];
   SyrkPace pc{nullptr, 0u, 0, 0, 0u, false};
-  syrk_tile<T8, false>(Xs, Xt, ldt, ti, tj, k_beg, nch, acc, pc);
+  if constexpr (TM) syrk_tile_tm<T8, false>(Xs, X, ld, ntok, ti, tj, k_beg, nch, acc, pc);
+  else syrk_tile<T8, false>(Xs, X, ld, ti, tj, k_beg, nch, acc, pc);
   syrk_store(acc, ti, tj, C, S, lds, P, blockIdx.y);
 }
 
@@ -546,10 +709,10 @@ __global__ void k_zero_u32(unsigned* p, int n) {
 // lists, so every item runs exactly once wherever the workgroups land.
 // The workgroups of an XCD are paced (SyrkPace) so that those working on a
 // 4 x 8 block of tiles read the same operand lines while they are in L2.
-template <typename T8>
+template <typename T8, bool TM>
 __global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k_pers(
-    const uint16_t* __restrict__ Xt, int64_t ldt, int64_t tpad, int C, float* S, int64_t lds,
-    int nt, int64_t span, int ns, float* P, unsigned* ctl) {
+    const uint16_t* __restrict__ X, int64_t ld, int64_t ntok, int64_t tpad, int C, float* S,
+    int64_t lds, int nt, int64_t span, int ns, float* P, unsigned* ctl) {
   __shared__ __attribute__((aligned(1024))) uint16_t Xs[2][2][ST][KQ];
   __shared__ int bcast[2];
   int xx;
@@ -605,7 +768,8 @@ __global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k_pers(
     const int nch = k_end > k_beg ? (int)((k_end - k_beg) / KQ) : 0;
     f4_t acc[8][4];
     pc.on = paced;
-    syrk_tile<T8, true>(Xs, Xt, ldt, ti, tj, k_beg, nch, acc, pc);
+    if constexpr (TM) syrk_tile_tm<T8, true>(Xs, X, ld, ntok, ti, tj, k_beg, nch, acc, pc);
+    else syrk_tile<T8, true>(Xs, X, ld, ti, tj, k_beg, nch, acc, pc);
     syrk_store(acc, ti, tj, C, S, lds, P, split);
   }
 }
@@ -892,8 +1056,12 @@ namespace crbq {
 constexpr int64_t PERS_MIN_C = 8192;
 static size_t syrk_ctl_bytes(int64_t C) { return C >= PERS_MIN_C ? PCTL_BYTES + 256 : 0; }
 
-static int syrk_xt(const uint16_t* Xt, int64_t ldt, int64_t tpad, int64_t C, float* S,
-                   int64_t lds, float* Pbuf, size_t pcap, int dtype, hipStream_t s) {
+// tmaj: X is the token-major activation itself (ld its row stride, ntok
+// valid rows, tpad = ntok rounded up to KQ; C a multiple of 256); else the
+// channel-major copy (ld its row stride, ntok unused).
+static int syrk_xt(const uint16_t* X, int64_t ld, int64_t ntok, bool tmaj, int64_t tpad,
+                   int64_t C, float* S, int64_t lds, float* Pbuf, size_t pcap, int dtype,
+                   hipStream_t s) {
   const int nt = (int)((C + ST - 1) / ST);
   const int64_t ntiles = (int64_t)nt * (nt + 1) / 2;
   // control words of the persistent kernel at the end of the workspace
@@ -916,18 +1084,26 @@ static int syrk_xt(const uint16_t* Xt, int64_t ldt, int64_t tpad, int64_t C, flo
   SyrkTimer tm(s, C);
   if (ctl) {
     const unsigned nwg = (unsigned)num_cus();
-    if (dtype == CRBQ_F16)
-      k_syrk16k_pers<h8_t><<<nwg, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt,
-                                                         span, ns, P, ctl);
-    else
-      k_syrk16k_pers<b8_t><<<nwg, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt,
-                                                         span, ns, P, ctl);
+#define CRBQ_PERS_GO(T8_, TM_)                                                              \
+  k_syrk16k_pers<T8_, TM_><<<nwg, SYRKD_THREADS, 0, s>>>(X, ld, ntok, tpad, (int)C, S, lds, \
+                                                         nt, span, ns, P, ctl)
+    if (dtype == CRBQ_F16) {
+      if (tmaj) CRBQ_PERS_GO(h8_t, true); else CRBQ_PERS_GO(h8_t, false);
+    } else {
+      if (tmaj) CRBQ_PERS_GO(b8_t, true); else CRBQ_PERS_GO(b8_t, false);
+    }
+#undef CRBQ_PERS_GO
   } else {
     dim3 grid((unsigned)ntiles, (unsigned)ns);
-    if (dtype == CRBQ_F16)
-      k_syrk16k<h8_t><<<grid, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt, span, P);
-    else
-      k_syrk16k<b8_t><<<grid, SYRKD_THREADS, 0, s>>>(Xt, ldt, tpad, (int)C, S, lds, nt, span, P);
+#define CRBQ_GRID_GO(T8_, TM_)                                                                 \
+  k_syrk16k<T8_, TM_><<<grid, SYRKD_THREADS, 0, s>>>(X, ld, ntok, tpad, (int)C, S, lds, nt, \
+                                                     span, P)
+    if (dtype == CRBQ_F16) {
+      if (tmaj) CRBQ_GRID_GO(h8_t, true); else CRBQ_GRID_GO(h8_t, false);
+    } else {
+      if (tmaj) CRBQ_GRID_GO(b8_t, true); else CRBQ_GRID_GO(b8_t, false);
+    }
+#undef CRBQ_GRID_GO
   }
   CRBQ_LAUNCH_CHECK();
   tm.stop(s);
@@ -942,6 +1118,13 @@ static int syrk_xt(const uint16_t* Xt, int64_t ldt, int64_t tpad, int64_t C, flo
 
 extern "C" size_t crbq_hessian_workspace_size(int64_t ntok, int64_t C) {
   if (ntok <= 0 || C <= 0) return 0;
+  if (C % crbq::ST == 0) {
+    // token-major stages: split partials and control words only
+    const int64_t tpad = (ntok + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
+    const int ns = crbq::choose_splits(tpad, C, crbq::num_cus());
+    return (ns > 1 ? (size_t)ns * (size_t)C * (size_t)C * sizeof(float) : 0) +
+           crbq::syrk_ctl_bytes(C);
+  }
   const crbq::XtPlan pl = crbq::xt_plan(ntok, C);
   const int64_t tpad = (pl.tch + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
   const int ns = crbq::choose_splits(tpad, C, crbq::num_cus());
@@ -970,6 +1153,13 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
   const int64_t ntiles = (int64_t)nt * (nt + 1) / 2;
   if (ntiles > 0x7fffffff) return CRBQ_ERR_ARG;
   const bool fast = (C % 8 == 0) && (ldx % 8 == 0) && ((((uintptr_t)X) & 15) == 0);
+  if (fast && C % crbq::ST == 0 && ldx < ((int64_t)1 << 24)) {
+    // token-major stages straight from X (no transposed copy); the
+    // workspace holds the split partials and the control words
+    const int64_t tpad = (ntok + crbq::KQ - 1) / crbq::KQ * crbq::KQ;
+    return crbq::syrk_xt((const uint16_t*)X, ldx, ntok, true, tpad, C, S, lds, (float*)ws,
+                         ws ? ws_bytes : 0, dtype, s);
+  }
   const crbq::XtPlan pl = crbq::xt_plan(ntok, C);
   if (ws && ws_bytes >= pl.xt_bytes) {
     // channel-major path: transpose each pass into the workspace, then SYRK
@@ -989,7 +1179,7 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
         crbq::k_xpose16<false><<<nblk, 256, 0, s>>>(Xc, n, ldx, (int)C, Xt, pl.ldt, tpad,
                                                     (int)pl.Cp);
       CRBQ_LAUNCH_CHECK();
-      const int st = crbq::syrk_xt(Xt, pl.ldt, tpad, C, S, lds, Pbuf, pcap, dtype, s);
+      const int st = crbq::syrk_xt(Xt, pl.ldt, 0, false, tpad, C, S, lds, Pbuf, pcap, dtype, s);
       if (st) return st;
     }
     return CRBQ_OK;
@@ -1076,7 +1266,8 @@ extern "C" int crbq_hessian_accum_cm(const void* Xt, int dtype, int64_t ntok, in
   if ((((uintptr_t)Xt) & 15) != 0) return CRBQ_ERR_ARG;
   const int nt = (int)((C + crbq::ST - 1) / crbq::ST);
   if ((int64_t)nt * (nt + 1) / 2 > 0x7fffffff) return CRBQ_ERR_ARG;
-  return crbq::syrk_xt((const uint16_t*)Xt, ldt, tpad, C, S, lds, (float*)ws, ws ? ws_bytes : 0,
+  return crbq::syrk_xt((const uint16_t*)Xt, ldt, 0, false, tpad, C, S, lds, (float*)ws,
+                       ws ? ws_bytes : 0,
                        dtype, (hipStream_t)stream);
 }
 

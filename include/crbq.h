@@ -104,15 +104,18 @@ int         crbq_set_percentiles(const float* q81);
  * accumulate in fp32 on MFMA; fp32 inputs use the fp32 MFMA.
  * The reference's running rescale H *= n/(n+b); H += (2/n) X^T X is applied
  * once, in crbq_hessian_finalize, which gives the same H up to rounding.
- * ws (optional, crbq_hessian_workspace_size bytes; may be NULL) holds a
- * channel-major copy of X (16-bit inputs: C rounded up to 256 rows of up to
- * 2^21 tokens, at most 8 GiB per pass; longer inputs run in passes), from
- * which the SYRK streams whole cache lines, followed by the per-split
- * partial sums when the token range is split across workgroups to fill the
- * GPU; the partials are added to S in a fixed order.  With a smaller ws
- * (or NULL) the SYRK reads X in place, a slower path with the same result
- * up to summation order.  fp32 inputs use no workspace.  The environment
- * variable CRBQ_XT_PASS_TOKENS (read per call) lowers the pass length. */
+ * 16-bit inputs with C a multiple of 256, ldx a multiple of 8 and X 16-byte
+ * aligned are staged into LDS as they are; ws (optional,
+ * crbq_hessian_workspace_size bytes; may be NULL) then holds the per-split
+ * partial sums, used when the token range is split across workgroups to
+ * fill the GPU (added to S in a fixed order), and a few control words.
+ * Other 16-bit inputs: ws also holds a channel-major copy of X (C rounded
+ * up to 256 rows of up to 2^21 tokens, at most 8 GiB per pass; longer
+ * inputs run in passes), bitwise the same sums; with a workspace too small
+ * for it (or NULL) the SYRK transposes X in registers, a slower path with
+ * the same result up to summation order.  fp32 inputs use no workspace.
+ * The environment variable CRBQ_XT_PASS_TOKENS (read per call) lowers the
+ * pass length of the copy. */
 size_t crbq_hessian_workspace_size(int64_t ntok, int64_t C);
 int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_t ldx,
                        int64_t C, float* S, int64_t lds, void* ws, size_t ws_bytes,
@@ -121,7 +124,8 @@ int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_t ldx,
  * the caller builds (for callers that gather the activations of several
  * forwards before one update: the stack driver's deferred Hessians,
  * run.py:341-374, whose copy of each forward's activations into the store
- * is then the transpose, saving crbq_hessian_accum's own pass over X).
+ * is then the transpose; crbq_hessian_accum on a token-major store gives
+ * the same sums).
  *   crbq_hessian_cm_shape: the store's shape for ntok tokens of C channels:
  *     *rows = C rounded up to 256, *ldt = ntok rounded up to 64 (at most
  *     2^21 tokens);

@@ -273,14 +273,58 @@ def test_hessian_channel_major_store(dtype, C, chunks):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("T,C,ldx", [(77, 256, 256), (1000, 512, 520), (4109, 4096, 4096),
+                                     (3000, 8192, 8200), (20000, 8192, 8192)])
+def test_hessian_token_major_stages(dtype, T, C, ldx):
+    """C a multiple of 256 with 16-byte aligned rows: the SYRK stages the
+    token-major X as it is and reads its MFMA operands with LDS transpose
+    reads.  Bitwise the sums of the channel-major path (crbq_hessian_transpose
+    + crbq_hessian_accum_cm, same token splits) on the same tokens, and
+    against float64: ragged token counts (rows past ntok read as zeros),
+    strided rows, the launched grid, the persistent kernel (C = 8192) and
+    several token splits; also with no workspace (one split, launched
+    grid)."""
+    print(f"hessian token-major stages {dtype} T={T} C={C} ldx={ldx}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(T + C)
+    Xf = (torch.randn(T, ldx, device=DEV, generator=g) *
+          torch.exp(torch.randn(ldx, device=DEV, generator=g))).to(dtype)
+    X = Xf[:, :C]
+    S1 = torch.full((C, C), 0.5, device=DEV)
+    _k().hessian_accum(X, S1)
+    Xt = _k().hessian_cm_store(T, C, dtype, DEV)
+    _k().hessian_transpose(X, Xt, 0)
+    S2 = torch.full((C, C), 0.5, device=DEV)
+    _k().hessian_accum_cm(Xt, T, C, S2)
+    del Xt
+    torch.cuda.synchronize()
+    assert torch.equal(torch.triu(S1), torch.triu(S2))
+    del S2
+    Xd = X.double()
+    want = torch.triu(Xd.t() @ Xd + 0.5)
+    assert float((torch.triu(S1.double()) - want).norm() / want.norm()) < 1e-5
+    del want, Xd
+    if T <= 4109:
+        S3 = torch.full((C, C), 0.5, device=DEV)
+        _accum_raw(X, S3, 0)
+        torch.cuda.synchronize()
+        if T < 4096:
+            # one token split either way: the same sums bit for bit
+            assert torch.equal(torch.triu(S3), torch.triu(S1))
+        Xd = X.double()
+        want = torch.triu(Xd.t() @ Xd + 0.5)
+        assert float((torch.triu(S3.double()) - want).norm() / want.norm()) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("T,C", [(2048, 8192), (1000, 8300), (16384, 8192)])
 def test_hessian_persistent_paced(dtype, T, C):
     """From 8192 channels the SYRK runs as the persistent, XCD-paced kernel
     (items claimed per XCD, control words at the end of the workspace).
     Against float64 on the GPU; with one token split (T < 4096) bitwise
-    equal to the launched grid (a workspace without room for the control
-    words) and to the token-major path (NULL workspace), which issue the
-    same MFMAs per tile; with several splits, the same bits on a rerun."""
+    equal to the launched grid (C = 8192: no workspace; C = 8300: a
+    workspace without room for the control words) and, for C = 8300, to
+    the in-place path (NULL workspace), which issue the same MFMAs per tile;
+    with several splits, the same bits on a rerun."""
     print(f"hessian persistent {dtype} T={T} C={C}", flush=True)
     from crb_amd import _lib
     lib = _lib.load()
@@ -297,8 +341,9 @@ def test_hessian_persistent_paced(dtype, T, C):
     del want, got
     xt_bytes = -(-C // 256) * 256 * (-(-T // 64) * 64) * 2
     if T < 4096:
-        assert full > xt_bytes                  # room for the control words
-        for nb in (xt_bytes, 0):                # launched grid, token-major path
+        if C % 256:
+            assert full > xt_bytes              # room for the control words
+        for nb in ((xt_bytes, 0) if C % 256 else (0,)):
             S2 = torch.full((C, C), 0.5, device=DEV)
             _accum_raw(X, S2, nb)
             torch.cuda.synchronize()
