@@ -713,7 +713,9 @@ def main():
                      "quantize_overlapped": round(pt.quantize_ms, 3),
                      "hinv": {g: round(v, 3) for g, v in pt.hinv_ms.items()},
                      "factor_plus_blocks": {g: round(v, 3) for g, v in pt.chain_ms.items()}},
-        "roofline": {"bound": "mfma", "kernel": "k_syrk16k_pers (Hessian SYRK, fc2 input C=16384)",
+        "roofline": {"bound": "mfma",
+                     "kernel": "k_syrk16k_pers<TM> (Hessian SYRK, token-major stages, "
+                               "fc2 input C=16384)",
                      "achieved": round(achieved / 1e12, 2), "peak": PEAK_F16 / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_F16, 4),
                      "launch_ms": round(t_launch * 1e3, 3),
