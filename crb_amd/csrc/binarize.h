@@ -113,6 +113,11 @@ __device__ void hor_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
   }
 }
 
+// The lanes of a row hold the same d, c12, c1w, c2w (row sums end equal on
+// every lane of the group), so the two quotients are split over each pair
+// of adjacent lanes: the even lane divides n1, the odd lane n2, and a DPP
+// swap hands each lane the other's (the same IEEE quotients, one division
+// per lane instead of two).
 __device__ __forceinline__ void crb_solve(float d, float c12, float c1w, float c2w,
                                           const CrbConsts& k, float& a1, float& a2) {
   // binary.py:1582-1596 (solve_alphas_vec)
@@ -124,8 +129,11 @@ __device__ __forceinline__ void crb_solve(float d, float c12, float c1w, float c
   const float sden = ok ? den : 1.f;
   const float n1 = A * c1w - c12 * c2w;
   const float n2 = A * c2w - c12 * c1w;
-  a1 = ok ? clamp0(n1 / sden) : 0.f;
-  a2 = ok ? clamp0(n2 / sden) : 0.f;
+  const bool odd = (threadIdx.x & 1) != 0;
+  const float q = (odd ? n2 : n1) / sden;
+  const float o = __builtin_bit_cast(float, dpp_u32<DPP_XOR1>(__builtin_bit_cast(unsigned, q)));
+  a1 = ok ? clamp0(odd ? o : q) : 0.f;
+  a2 = ok ? clamp0(odd ? q : o) : 0.f;
 }
 
 // coupled_residual_binarization_stable_v7, binary.py:1544-1638.
@@ -175,8 +183,8 @@ __device__ void crb_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
     c2w = rdot_sign<EPL, LPR>(cen, B2);
   }
   crb_solve(d, c12, c1w, c2w, k, a1, a2);
-  if (!k.skip) {
-    for (int it = 0; it < k.iters; ++it) {
+  if (!k.skip && k.iters > 0) {
+    auto round = [&]() {
 #pragma unroll
       for (int e = 0; e < EPL; ++e) t[e] = __builtin_fmaf(-a1, B1[e], cen[e]);  // step 5
       const float t5m = div_cnt(rsum_z<EPL, LPR>(t), ds, rds);
@@ -193,7 +201,11 @@ __device__ void crb_row(const float (&x)[EPL], const bool (&m)[EPL], int order,
       c1w = rdot_sign<EPL, LPR>(cen, B1);
       c12 = rdot_sign<EPL, LPR>(B1, B2);
       crb_solve(d, c12, c1w, c2w, k, a1, a2);
-    }
+    };
+    // the reference's single round (binary.py:1607-1631) straight-line, so
+    // its registers need no loop-carried copies; more rounds loop
+    round();
+    for (int it = 1; it < k.iters; ++it) round();
   }
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {                                   // step 7
