@@ -79,12 +79,14 @@ __device__ __forceinline__ float rdot_sign(const float (&a)[EPL], const float (&
   return group_sum_f<LPR>(tree_sum(t));
 }
 
+// Row count of the mask: an integer add-with-carry per element (the mask
+// bit is the carry-in), then the lane sums as exact integer-valued floats.
 template <int EPL, int LPR = 64>
 __device__ __forceinline__ float rcount(const bool (&m)[EPL]) {
-  float c = m[0] ? 1.f : 0.f;
+  unsigned c = 0;
 #pragma unroll
-  for (int e = 1; e < EPL; ++e) c += m[e] ? 1.f : 0.f;
-  return group_sum_f<LPR>(c);  // integer-valued, exact
+  for (int e = 0; e < EPL; ++e) c += m[e] ? 1u : 0u;
+  return group_sum_f<LPR>((float)c);  // integer-valued, exact
 }
 
 // high_order_residual, binary.py:18-39.

@@ -1697,23 +1697,21 @@ __global__ __launch_bounds__(256) void k_binarize_scales(const float* x, int R, 
 // accesses (x, out and their row strides 16-byte aligned, mask rows 4-byte
 // aligned; the host checks).  Row reductions stay inside the row's lane
 // group.
-template <int MF, int LPR, int EPL>
-__global__ __launch_bounds__(256) void k_binarize_g(const float* x, int R, int nc, int64_t ldx,
-                                                    const uint8_t* __restrict__ mask, int64_t ldm,
-                                                    int order, int method, CrbConsts k,
-                                                    float* out, int64_t ldo) {
+// One row of k_binarize_g.  FULL: the row is exactly 4 LPR NH columns, so
+// every chunk is in range and the loads, mask tests and stores carry no
+// per-chunk guards (a guarded chunk makes the compiler keep the mask as
+// packed bytes across the branches and unpack it again).
+template <int MF, int LPR, int EPL, bool FULL>
+__device__ __forceinline__ void binarize_g_row(const float* xr, const uint8_t* mr, float* orow,
+                                               int r, int nc, int order, int method,
+                                               const CrbConsts& k) {
   constexpr int NH = EPL / 4;
-  const int r = threadIdx.x % LPR;
-  const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
-  if (row >= R) return;                      // whole lane groups leave together
   float v[EPL], o[EPL];
   bool m[EPL];
-  const float* xr = x + (int64_t)row * ldx;
-  const uint8_t* mr = mask + (int64_t)row * ldm;
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
     const int c0 = h * 4 * LPR + r * 4;
-    if (c0 + 3 < nc) {
+    if (FULL || c0 + 3 < nc) {
       const float4 q = *(const float4*)(xr + c0);
       const unsigned mb = *(const unsigned*)(mr + c0);
       v[4 * h] = q.x; v[4 * h + 1] = q.y; v[4 * h + 2] = q.z; v[4 * h + 3] = q.w;
@@ -1729,11 +1727,10 @@ __global__ __launch_bounds__(256) void k_binarize_g(const float* x, int R, int n
     }
   }
   binarize_row<MF, EPL, LPR>(method, v, m, order, k, o);
-  float* orow = out + (int64_t)row * ldo;
 #pragma unroll
   for (int h = 0; h < NH; ++h) {
     const int c0 = h * 4 * LPR + r * 4;
-    if (c0 + 3 < nc) {
+    if (FULL || c0 + 3 < nc) {
       *(float4*)(orow + c0) = make_float4(o[4 * h], o[4 * h + 1], o[4 * h + 2], o[4 * h + 3]);
     } else {
 #pragma unroll
@@ -1741,6 +1738,23 @@ __global__ __launch_bounds__(256) void k_binarize_g(const float* x, int R, int n
         if (c0 + j < nc) orow[c0 + j] = o[4 * h + j];
     }
   }
+}
+
+template <int MF, int LPR, int EPL>
+__global__ __launch_bounds__(256) void k_binarize_g(const float* x, int R, int nc, int64_t ldx,
+                                                    const uint8_t* __restrict__ mask, int64_t ldm,
+                                                    int order, int method, CrbConsts k,
+                                                    float* out, int64_t ldo) {
+  const int r = threadIdx.x % LPR;
+  const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
+  if (row >= R) return;                      // whole lane groups leave together
+  const float* xr = x + (int64_t)row * ldx;
+  const uint8_t* mr = mask + (int64_t)row * ldm;
+  float* orow = out + (int64_t)row * ldo;
+  if (nc == EPL * LPR)
+    binarize_g_row<MF, LPR, EPL, true>(xr, mr, orow, r, nc, order, method, k);
+  else
+    binarize_g_row<MF, LPR, EPL, false>(xr, mr, orow, r, nc, order, method, k);
 }
 }  // namespace crbq
 
