@@ -316,6 +316,30 @@ def test_hessian_token_major_stages(dtype, T, C, ldx):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("T,C,ldx", [(300, 512, 513), (5000, 256, 260)])
+def test_hessian_token_major_unaligned(dtype, T, C, ldx):
+    """C a multiple of 256 but rows that cannot be staged with 16-byte loads
+    (odd or non-multiple-of-8 row stride): crbq_hessian_workspace_size then
+    holds only the split partials, so the SYRK transposes in registers
+    (k_syrk16p); against float64."""
+    print(f"hessian token-major unaligned {dtype} T={T} C={C} ldx={ldx}", flush=True)
+    from crb_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator(device=DEV).manual_seed(T + 3 * C)
+    Xf = (torch.randn(T, ldx, device=DEV, generator=g) *
+          torch.exp(torch.randn(ldx, device=DEV, generator=g))).to(dtype)
+    X = Xf[:, :C]
+    nb = lib.crbq_hessian_workspace_size(T, C)
+    assert nb < -(-T // 64) * 64 * C * 2          # no room for a channel-major copy
+    S = torch.full((C, C), 0.25, device=DEV)
+    _accum_raw(X, S, nb)
+    torch.cuda.synchronize()
+    Xd = X.double()
+    want = torch.triu(Xd.t() @ Xd + 0.25)
+    assert float((torch.triu(S.double()) - want).norm() / want.norm()) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("T,C", [(2048, 8192), (1000, 8300), (16384, 8192)])
 def test_hessian_persistent_paced(dtype, T, C):
     """From 8192 channels the SYRK runs as the persistent, XCD-paced kernel
