@@ -100,6 +100,18 @@ struct SearchWs {
   float* pvals;      // [NQ]
 };
 
+// Sublayers that share one inverse factor (q/k/v, Llama's gate/up) run one
+// block loop together: every search and quantize launch covers up to NSEG
+// of them, blockIdx.y selecting the sublayer (its weights, search scratch
+// and trace), and each sublayer's work is exactly that of a launch of its
+// own (same workgroups, same reductions, same bits).
+constexpr int NSEG = 4;
+struct SegSearch {
+  const float* W[NSEG];
+  SearchWs s[NSEG];
+  crbq_block_trace* tr[NSEG];
+};
+
 static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 static void carve_search(WsCarver& c, int64_t R, SearchWs& s) {
@@ -236,8 +248,10 @@ __device__ int wave_argmin(const double* v, int n) {
 constexpr int CS_PH = CRBQ_CS_PH;            // row phases per workgroup
 constexpr int CS_THREADS = NCMAX * CS_PH;
 __global__ __launch_bounds__(CS_THREADS) void k_colscore(
-    const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
+    SegSearch seg, int64_t ldw, int R, int nc, const float* __restrict__ U, int64_t ldu,
+    int metric) {
+  const float* __restrict__ W = seg.W[blockIdx.y];
+  const SearchWs s = seg.s[blockIdx.y];
   __shared__ double part[CS_PH][NCMAX];
   __shared__ double red[CS_PH][NCMAX];
   __shared__ double sc[NCMAX];
@@ -338,8 +352,10 @@ __device__ __forceinline__ void q_cols(const float* __restrict__ U, int64_t ldu,
 
 // Level-1: histogram of bits [31:20] of the (non-negative) float pattern.
 __global__ __launch_bounds__(256) void k_qpass1(
-    const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
+    SegSearch seg, int64_t ldw, int R, int nc, const float* __restrict__ U, int64_t ldu,
+    int metric) {
+  const float* __restrict__ W = seg.W[blockIdx.y];
+  const SearchWs s = seg.s[blockIdx.y];
   __shared__ uint32_t lh[H1];
   __shared__ float d2s[NCMAX];
   __shared__ int rk[NCMAX];
@@ -438,8 +454,10 @@ __device__ __forceinline__ int find_bin(const uint32_t* cum, uint32_t r) {
 // order inside a list does not matter to the selection).  The list counters
 // are cleared by k_colscore.
 __global__ __launch_bounds__(256) void k_qlist(
-    const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s) {
+    SegSearch seg, int64_t ldw, int R, int nc, const float* __restrict__ U, int64_t ldu,
+    int metric) {
+  const float* __restrict__ W = seg.W[blockIdx.y];
+  const SearchWs s = seg.s[blockIdx.y];
   __shared__ uint32_t cum[H1];
   __shared__ int lead[H1];
   __shared__ uint32_t tmp[256];
@@ -554,7 +572,8 @@ __device__ void qselect_hist(const uint32_t* list, int n, int b2, uint32_t* h) {
   }
 }
 
-__global__ __launch_bounds__(QS_T) void k_qselect(int R, int nc, SearchWs s) {
+__global__ __launch_bounds__(QS_T) void k_qselect(SegSearch seg, int R, int nc) {
+  const SearchWs s = seg.s[blockIdx.y];
   static_assert(H2 == H3, "one histogram buffer for both rounds");
   __shared__ uint32_t h[H2];
   __shared__ uint32_t cum[H2];
@@ -838,8 +857,11 @@ __device__ __forceinline__ void wave_prefix(SortedRow& r, float x0, float x1, in
 // pairs over all its lanes, each two binary searches per group and range
 // sums (group_err1); the last workgroup takes k* = first strict minimum.
 __global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
-    const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, SearchWs s, crbq_block_trace* tr) {
+    SegSearch seg, int64_t ldw, int R, int nc, const float* __restrict__ U, int64_t ldu,
+    int metric) {
+  const float* __restrict__ W = seg.W[blockIdx.y];
+  const SearchWs s = seg.s[blockIdx.y];
+  crbq_block_trace* const tr = seg.tr[blockIdx.y];
   __shared__ SortedRow rows[PC_WAVES];
   __shared__ double red[10][96];
   __shared__ double e[128];
@@ -916,9 +938,15 @@ struct QuantArgs {
   float* losses;
   uint8_t* masks; int64_t ldm;       // optional
 };
+struct QuantSegs {                   // one per sublayer of the launch (blockIdx.y)
+  QuantArgs a[NSEG];
+  SearchWs s[NSEG];
+};
 
 template <int MF, int EPL>
-__global__ __launch_bounds__(256) void k_quantize(QuantArgs a, SearchWs s) {
+__global__ __launch_bounds__(256) void k_quantize(QuantSegs qs) {
+  const QuantArgs a = qs.a[blockIdx.y];
+  const SearchWs s = qs.s[blockIdx.y];
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= a.R) return;
@@ -1007,7 +1035,9 @@ __device__ __forceinline__ void vstore(float* p, const float* v) {
 #endif
 constexpr int QG_LPR = CRBQ_QG_LPR;          // lanes per row of the block quantize
 template <int MF>
-__global__ __launch_bounds__(256) void k_quantize_g(QuantArgs a, SearchWs s) {
+__global__ __launch_bounds__(256) void k_quantize_g(QuantSegs qs) {
+  const QuantArgs a = qs.a[blockIdx.y];
+  const SearchWs s = qs.s[blockIdx.y];
   constexpr int LPR = QG_LPR, EPL = 128 / LPR, VW = EPL < 4 ? EPL : 4, NH = EPL / VW;
   const int r = threadIdx.x % LPR;
   const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
@@ -1248,9 +1278,11 @@ __device__ __forceinline__ double row_cand_err(const float* x, int i, int nc, do
 }
 
 __global__ __launch_bounds__(64 * PR_CW) void k_phase_a_rows(
-    const float* __restrict__ W, int64_t ldw, int R, int nc,
-    const float* __restrict__ U, int64_t ldu, int metric, int ncand, int up_lim, int ncg,
-    int cw, SearchWs s, crbq_block_trace* tr) {
+    SegSearch seg, int64_t ldw, int R, int nc, const float* __restrict__ U, int64_t ldu,
+    int metric, int ncand, int up_lim, int ncg, int cw) {
+  const float* __restrict__ W = seg.W[blockIdx.y];
+  const SearchWs s = seg.s[blockIdx.y];
+  crbq_block_trace* const tr = seg.tr[blockIdx.y];
   constexpr int LMAX = (64 + PR_MINW - 1) / PR_MINW;   // rows loaded per wavefront
   __shared__ __attribute__((aligned(16))) float xs[64][PR_XS];
   __shared__ double cs[NCMAX / 8][64];           // fp64 sums of 8-rank chunks, per row
@@ -1322,9 +1354,8 @@ __global__ __launch_bounds__(64 * PR_CW) void k_phase_a_rows(
 // ---------------------------------------------------------------------------
 // host drivers
 // ---------------------------------------------------------------------------
-static int search_block(const float* W, int64_t ldw, int R, int nc, const float* U,
-                        int64_t ldu, int metric, int up_lim, SearchWs& s,
-                        crbq_block_trace* tr, hipStream_t st) {
+static int search_block(const SegSearch& seg, int nseg, int64_t ldw, int R, int nc,
+                        const float* U, int64_t ldu, int metric, int up_lim, hipStream_t st) {
   const int ncand = up_lim - 1;
   const int nwg_cs = (int)std::min<int64_t>(cdiv(R, CS_PH), CS_MAXWG);
   const int nwg_q = (int)cdiv(R, Q_RPW);
@@ -1333,13 +1364,14 @@ static int search_block(const float* W, int64_t ldw, int R, int nc, const float*
   // 64-row group (at least PR_MINW wavefronts: the reduction's 576 threads)
   const int ncg = (int)cdiv(ncand, PR_CW), cw = (int)cdiv(ncand, ncg);
   const int nrg = (int)std::min<int64_t>(cdiv(R, 64), PX_MAXWG);
-  k_colscore<<<nwg_cs, CS_THREADS, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  k_phase_a_rows<<<nrg * ncg, 64 * std::max(cw, PR_MINW), 0, st>>>(
-      W, ldw, R, nc, U, ldu, metric, ncand, up_lim, ncg, cw, s, tr);
-  k_qpass1<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  k_qlist<<<nwg_q, 256, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s);
-  k_qselect<<<NT, QS_T, 0, st>>>(R, nc, s);
-  k_phase_c<<<nwg_c, 64 * PC_WAVES, 0, st>>>(W, ldw, R, nc, U, ldu, metric, s, tr);
+  const unsigned y = (unsigned)nseg;
+  k_colscore<<<dim3(nwg_cs, y), CS_THREADS, 0, st>>>(seg, ldw, R, nc, U, ldu, metric);
+  k_phase_a_rows<<<dim3(nrg * ncg, y), 64 * std::max(cw, PR_MINW), 0, st>>>(
+      seg, ldw, R, nc, U, ldu, metric, ncand, up_lim, ncg, cw);
+  k_qpass1<<<dim3(nwg_q, y), 256, 0, st>>>(seg, ldw, R, nc, U, ldu, metric);
+  k_qlist<<<dim3(nwg_q, y), 256, 0, st>>>(seg, ldw, R, nc, U, ldu, metric);
+  k_qselect<<<dim3(NT, y), QS_T, 0, st>>>(seg, R, nc);
+  k_phase_c<<<dim3(nwg_c, y), 64 * PC_WAVES, 0, st>>>(seg, ldw, R, nc, U, ldu, metric);
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }
@@ -1446,7 +1478,11 @@ extern "C" int crbq_block_search(const float* W, int64_t R, int32_t ncols, int64
   if (st) return st;
   hipStream_t hs = (hipStream_t)stream;
   k_init_ctrl<<<1, 64, 0, hs>>>(s);
-  st = search_block(W, ldw, (int)R, ncols, Ublk, ldu, metric, up_lim, s, trace, hs);
+  SegSearch seg{};
+  seg.W[0] = W;
+  seg.s[0] = s;
+  seg.tr[0] = trace;
+  st = search_block(seg, 1, ldw, (int)R, ncols, Ublk, ldu, metric, up_lim, hs);
   if (st) return st;
   if (masks) {
     const int64_t n = R * (int64_t)ncols;
@@ -1476,31 +1512,45 @@ extern "C" size_t crbq_fasterquant_workspace_size(int64_t R, int64_t C, const cr
 }
 
 namespace crbq {
-static int fasterquant_impl(float* W, int64_t R, int64_t C, int64_t ldw, const float* U,
-                            int64_t ldu, const crbq_params* p, float* losses, uint8_t* masks,
-                            int64_t ldm, crbq_block_trace* traces, void* ws, size_t ws_bytes,
+// The block loop over nseg sublayers of one shape that share the factor U
+// (nseg = 1: one sublayer).  Segment i has its own weights W[i], losses,
+// masks, traces and its own part of the workspace (search scratch and the
+// super-block's error rows), so its results are those of a call of its own.
+static int fasterquant_impl(int nseg, float* const* Ws, int64_t R, int64_t C, int64_t ldw,
+                            const float* U, int64_t ldu, const crbq_params* p,
+                            float* const* losses, uint8_t* const* masks, int64_t ldm,
+                            crbq_block_trace* const* traces, void* ws, size_t ws_bytes,
                             void* stream) {
   int st = check_params(p);
   if (st) return st;
-  if (!W || !U || !losses || R <= 0 || C <= 0 || ldw < C || ldu < C) return CRBQ_ERR_ARG;
+  if (nseg < 1 || nseg > NSEG || !Ws || !losses) return CRBQ_ERR_ARG;
+  if (!U || R <= 0 || C <= 0 || ldw < C || ldu < C) return CRBQ_ERR_ARG;
+  for (int i = 0; i < nseg; ++i)
+    if (!Ws[i] || !losses[i]) return CRBQ_ERR_ARG;
+  const bool any_masks = masks && masks[0];
+  for (int i = 0; i < nseg; ++i)
+    if (masks && ((masks[i] != nullptr) != any_masks)) return CRBQ_ERR_ARG;
   if (R * (int64_t)NCMAX >= (1 << 24)) return CRBQ_ERR_ARG;
-  if (masks && ldm < C) return CRBQ_ERR_ARG;
+  if (any_masks && ldm < C) return CRBQ_ERR_ARG;
   const int bs = p->blocksize;
   const int64_t SB = std::min<int64_t>((int64_t)SB_BLOCKS * bs, C);
   WsCarver c(ws, ws_bytes);
-  SearchWs s;
-  carve_search(c, R, s);
-  float* err = c.take<float>((size_t)R * SB);
+  SearchWs s[NSEG];
+  float* err[NSEG] = {};
+  for (int i = 0; i < nseg; ++i) {
+    carve_search(c, R, s[i]);
+    err[i] = c.take<float>((size_t)R * SB);
+  }
   if (!c.ok()) return CRBQ_ERR_WORKSPACE;
-  st = ensure_q_table();
-  if (st) return st;
-  hipStream_t hs = (hipStream_t)stream;
-  k_init_ctrl<<<1, 64, 0, hs>>>(s);
   if (p->partition == 3) {
     // every block must be at least up_lim wide (torch.topk k <= n)
     const int64_t last = C - (C - 1) / bs * bs;
     if (last < p->up_lim || bs < p->up_lim) return CRBQ_ERR_TOPK;
   }
+  st = ensure_q_table();
+  if (st) return st;
+  hipStream_t hs = (hipStream_t)stream;
+  for (int i = 0; i < nseg; ++i) k_init_ctrl<<<1, 64, 0, hs>>>(s[i]);
   CrbConsts k;
   k.lam = p->lam;
   k.omg = (float)(1.0 - (double)p->corr_damp);
@@ -1508,38 +1558,47 @@ static int fasterquant_impl(float* W, int64_t R, int64_t C, int64_t ldw, const f
   k.skip = false;
   k.iters = p->refine_iters;
   const bool gptq = !p->disable_gptq;
+  const int mf = method_family(p->method);
+  const unsigned y = (unsigned)nseg;
   int bi = 0;
   for (int64_t sb0 = 0; sb0 < C; sb0 += SB) {
     const int64_t sb1 = std::min<int64_t>(sb0 + SB, C);
     for (int64_t st0 = sb0; st0 < sb1; st0 += bs, ++bi) {
       const int nc = (int)std::min<int64_t>(bs, sb1 - st0);
-      float* Wb = W + st0;
       const float* Ub = U + st0 * ldu + st0;
-      crbq_block_trace* tr = traces ? traces + bi : nullptr;
       if (p->partition == 3) {
-        st = search_block(Wb, ldw, (int)R, nc, Ub, ldu, p->metric, p->up_lim, s, tr, hs);
+        SegSearch seg{};
+        for (int i = 0; i < nseg; ++i) {
+          seg.W[i] = Ws[i] + st0;
+          seg.s[i] = s[i];
+          seg.tr[i] = traces && traces[i] ? traces[i] + bi : nullptr;
+        }
+        st = search_block(seg, nseg, ldw, (int)R, nc, Ub, ldu, p->metric, p->up_lim, hs);
         if (st) return st;
       }
-      QuantArgs a;
-      a.W = Wb; a.ldw = ldw; a.R = (int)R; a.nc = nc;
-      a.U = Ub; a.ldu = ldu;
-      a.metric = p->metric; a.method = p->method; a.partition = p->partition;
-      for (int g = 0; g < 3; ++g) a.orders[g] = p->orders[g];
-      a.k = k;
-      a.gptq = gptq;
-      a.err = err + (st0 - sb0); a.lde = SB;
-      a.losses = losses;
-      a.masks = masks ? masks + st0 : nullptr; a.ldm = ldm;
-      const bool vec = ((uintptr_t)Wb % 16 == 0) && ldw % 4 == 0 &&
-                       ((uintptr_t)a.err % 16 == 0) && a.lde % 4 == 0 &&
-                       (!a.masks || (((uintptr_t)a.masks % 4 == 0) && ldm % 4 == 0));
-      const int mf = method_family(p->method);
-#define CRBQ_QUANT_GO(MF_)                                                  \
-  do {                                                                      \
-    if (vec && nc <= 128)                                                   \
-      k_quantize_g<MF_><<<(unsigned)cdiv(R, 256 / QG_LPR), 256, 0, hs>>>(a, s); \
-    else                                                                    \
-      k_quantize<MF_, 2><<<(unsigned)cdiv(R, 4), 256, 0, hs>>>(a, s);       \
+      QuantSegs qs{};
+      bool vec = ldw % 4 == 0 && SB % 4 == 0 && (!any_masks || ldm % 4 == 0);
+      for (int i = 0; i < nseg; ++i) {
+        QuantArgs& a = qs.a[i];
+        a.W = Ws[i] + st0; a.ldw = ldw; a.R = (int)R; a.nc = nc;
+        a.U = Ub; a.ldu = ldu;
+        a.metric = p->metric; a.method = p->method; a.partition = p->partition;
+        for (int g = 0; g < 3; ++g) a.orders[g] = p->orders[g];
+        a.k = k;
+        a.gptq = gptq;
+        a.err = err[i] + (st0 - sb0); a.lde = SB;
+        a.losses = losses[i];
+        a.masks = any_masks ? masks[i] + st0 : nullptr; a.ldm = ldm;
+        qs.s[i] = s[i];
+        vec = vec && ((uintptr_t)a.W % 16 == 0) && ((uintptr_t)a.err % 16 == 0) &&
+              (!a.masks || (uintptr_t)a.masks % 4 == 0);
+      }
+#define CRBQ_QUANT_GO(MF_)                                                          \
+  do {                                                                              \
+    if (vec && nc <= 128)                                                           \
+      k_quantize_g<MF_><<<dim3((unsigned)cdiv(R, 256 / QG_LPR), y), 256, 0, hs>>>(qs); \
+    else                                                                            \
+      k_quantize<MF_, 2><<<dim3((unsigned)cdiv(R, 4), y), 256, 0, hs>>>(qs);       \
   } while (0)
       if (mf == MF_BRAQ) CRBQ_QUANT_GO(MF_BRAQ);
       else if (mf == MF_CRBOG) CRBQ_QUANT_GO(MF_CRBOG);
@@ -1548,15 +1607,19 @@ static int fasterquant_impl(float* W, int64_t R, int64_t C, int64_t ldw, const f
       CRBQ_LAUNCH_CHECK();
       const int64_t ed = st0 + nc;
       if (gptq && ed < sb1) {            // rest of this super-block
-        st = sgemm_launch(false, false, false, R, sb1 - ed, nc, -1.f, a.err, SB,
-                          U + st0 * ldu + ed, ldu, 1.f, W + ed, ldw, nullptr, hs);
-        if (st) return st;
+        for (int i = 0; i < nseg; ++i) {
+          st = sgemm_launch(false, false, false, R, sb1 - ed, nc, -1.f, qs.a[i].err, SB,
+                            U + st0 * ldu + ed, ldu, 1.f, Ws[i] + ed, ldw, nullptr, hs);
+          if (st) return st;
+        }
       }
     }
     if (gptq && sb1 < C) {               // every later column, K = sb1 - sb0
-      st = sgemm_launch(false, false, false, R, C - sb1, sb1 - sb0, -1.f, err, SB,
-                        U + sb0 * ldu + sb1, ldu, 1.f, W + sb1, ldw, nullptr, hs);
-      if (st) return st;
+      for (int i = 0; i < nseg; ++i) {
+        st = sgemm_launch(false, false, false, R, C - sb1, sb1 - sb0, -1.f, err[i], SB,
+                          U + sb0 * ldu + sb1, ldu, 1.f, Ws[i] + sb1, ldw, nullptr, hs);
+        if (st) return st;
+      }
     }
   }
   return CRBQ_OK;
@@ -1599,7 +1662,23 @@ extern "C" int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw, con
                                 int64_t ldu, const crbq_params* p, float* losses,
                                 uint8_t* masks, int64_t ldm, crbq_block_trace* traces,
                                 void* ws, size_t ws_bytes, void* stream) {
-  return crbq::fasterquant_impl(W, R, C, ldw, U, ldu, p, losses, masks, ldm, traces, ws,
+  return crbq::fasterquant_impl(1, &W, R, C, ldw, U, ldu, p, &losses, &masks, ldm, &traces,
+                                ws, ws_bytes, stream);
+}
+
+extern "C" size_t crbq_fasterquant_batched_workspace_size(int32_t nseg, int64_t R, int64_t C,
+                                                          const crbq_params* p) {
+  if (nseg < 1 || nseg > crbq::NSEG) return 0;
+  return (size_t)nseg * crbq_fasterquant_workspace_size(R, C, p);
+}
+
+extern "C" int crbq_fasterquant_batched(int32_t nseg, float* const* W, int64_t R, int64_t C,
+                                        int64_t ldw, const float* U, int64_t ldu,
+                                        const crbq_params* p, float* const* losses,
+                                        uint8_t* const* masks, int64_t ldm,
+                                        crbq_block_trace* const* traces, void* ws,
+                                        size_t ws_bytes, void* stream) {
+  return crbq::fasterquant_impl(nseg, W, R, C, ldw, U, ldu, p, losses, masks, ldm, traces, ws,
                                 ws_bytes, stream);
 }
 
@@ -1624,8 +1703,8 @@ extern "C" int crbq_fasterquant_noalloc(float* W, int64_t R, int64_t C, int64_t 
   void* ws = nullptr;
   const int sst = crbq::scratch_of_current_device(&ws);
   if (sst) return sst;
-  return crbq::fasterquant_impl(W, R, C, ldw, U, ldu, p, losses, masks, ldm, traces, ws,
-                                CRBQ_NOALLOC_SCRATCH_BYTES, stream);
+  return crbq::fasterquant_impl(1, &W, R, C, ldw, U, ldu, p, &losses, &masks, ldm, &traces,
+                                ws, CRBQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -12,6 +12,10 @@ Hessians and therefore identical inverse factors U.  This driver
   * enqueues every sublayer's block loop right behind its factor (an event
     wait, no host synchronisation), the widest input's chain first and on
     a stream of its own since it is the longest,
+  * runs the block loops of up to four same-shape sublayers of one input
+    (q/k/v, gate/up) as one loop whose launches cover all of them
+    (kernels.fasterquant_blocks_batched: same results, a third of the
+    launches for q/k/v),
   * checks the factorizations once at the end and, for an input whose
     Cholesky needed the reference's retries or fallback (bigptq.py:114-126),
     recomputes its sublayers with the final factor,
@@ -49,7 +53,7 @@ class LayerQuantizer:
     def __init__(self, sublayers, method="crb", metric="hessian", blocksize=128,
                  percdamp=0.01, partition=3, orders=(1, 1, 2), refine_iters=1,
                  lam=1e-5, corr_damp=0.1, disable_gptq=False, nstreams=NSTREAMS,
-                 keep_masks=False, keep_factors=False):
+                 keep_masks=False, keep_factors=False, batch_sublayers=True):
         self.sublayers = list(sublayers)
         self.p = _lib.params(method, metric=metric, blocksize=blocksize, partition=partition,
                              orders=orders, up_lim=50, refine_iters=refine_iters,
@@ -57,6 +61,7 @@ class LayerQuantizer:
         self.percdamp = percdamp
         self.dev = self.sublayers[0].weight.device
         self.nstreams = max(1, int(nstreams))
+        self.batch_sublayers = bool(batch_sublayers)
         self.keep_masks = bool(keep_masks)
         self.masks = {}            # keep_masks: name -> uint8 [R, C] mask codes 1/2/3
         # keep_factors (for checks): group -> (damped H, U), name -> (fp32
@@ -123,39 +128,68 @@ class LayerQuantizer:
         a, b = self.syrk_ev[group]
         return a.elapsed_time(b)
 
-    def _assign_streams(self, groups):
+    def _batches(self, groups):
+        """The sublayers in the order their loops are enqueued (the widest
+        input's first, larger weights first), cut into batches: runs of up
+        to kernels.MAX_BATCH sublayers of one input, weight shape and dtype
+        (single sublayers when batching is off)."""
+        order = sorted(self.sublayers, key=lambda s: (groups.index(s.group), -s.weight.numel()))
+        out = []
+        for s in order:
+            b = out[-1] if out else None
+            if (self.batch_sublayers and b is not None and len(b) < kernels.MAX_BATCH
+                    and b[0].group == s.group and b[0].weight.shape == s.weight.shape
+                    and b[0].weight.dtype == s.weight.dtype):
+                b.append(s)
+            else:
+                out.append([s])
+        return order, out
+
+    def _assign_streams(self, groups, batches):
         """The widest input gets stream 0 for its factor and its sublayers;
-        the other factors and sublayers share the remaining streams,
-        balanced by weight count."""
+        the other factors and the batches of sublayers share the remaining
+        streams, balanced by weight count."""
         ns = self.nstreams
         gstream = {}
         for i, g in enumerate(groups):
             gstream[g] = 0 if i == 0 or ns == 1 else 1 + (i - 1) % (ns - 1)
         load = [0] * ns
-        sstream = {}
-        for s in sorted(self.sublayers, key=lambda s: -s.weight.numel()):
-            if s.group == groups[0] or ns == 1:
+        bstream = []
+        for i in sorted(range(len(batches)), key=lambda i: -sum(s.weight.numel()
+                                                               for s in batches[i])):
+            b = batches[i]
+            if b[0].group == groups[0] or ns == 1:
                 k = 0
             else:
                 k = min(range(1, ns), key=lambda j: load[j])
-            load[k] += s.weight.numel()
-            sstream[s.name] = k
-        return gstream, sstream
+            load[k] += sum(s.weight.numel() for s in b)
+            bstream.append((i, k))
+        return gstream, [k for _, k in sorted(bstream)]
 
-    def _blocks(self, s, U, dead):
-        W = s.weight.float() if s.weight.dtype != torch.float32 else s.weight.clone()
-        W = W.contiguous()
-        W.masked_fill_(dead[None, :], 0.0)                               # bigptq.py:105
-        losses = torch.zeros(W.shape[0], device=self.dev)
-        masks, _ = kernels.fasterquant_blocks(W, U, self.p, losses, want_masks=self.keep_masks)
-        return W, losses, masks
+    def _blocks(self, batch, U, dead):
+        """Block loops of one batch: {name: (W fp32, losses, masks)}."""
+        Ws, ls = [], []
+        for s in batch:
+            W = s.weight.float() if s.weight.dtype != torch.float32 else s.weight.clone()
+            W = W.contiguous()
+            W.masked_fill_(dead[None, :], 0.0)                           # bigptq.py:105
+            Ws.append(W)
+            ls.append(torch.zeros(W.shape[0], device=self.dev))
+        if len(batch) == 1:
+            m, _ = kernels.fasterquant_blocks(Ws[0], U, self.p, ls[0], want_masks=self.keep_masks)
+            masks = [m]
+        else:
+            masks, _ = kernels.fasterquant_blocks_batched(Ws, U, self.p, ls,
+                                                          want_masks=self.keep_masks)
+        return {s.name: (Ws[i], ls[i], masks[i]) for i, s in enumerate(batch)}
 
     def quantize(self, times: PhaseTimes | None = None) -> dict:
         """fasterquant for every sublayer; returns {name: error}."""
         main = torch.cuda.current_stream(self.dev)
         streams = [torch.cuda.Stream(device=self.dev) for _ in range(self.nstreams)]
         groups = sorted(self.S.keys(), key=lambda g: -self.S[g].shape[0])
-        gstream, sstream = self._assign_streams(groups)
+        order, batches = self._batches(groups)
+        gstream, bstream = self._assign_streams(groups, batches)
         t0 = torch.cuda.Event(enable_timing=True)
         t0.record(main)
 
@@ -178,15 +212,17 @@ class LayerQuantizer:
                 hdone[g] = timed(st)
         work, sdone = {}, {}
         # the widest input's sublayers first (their chain is the longest)
-        order = sorted(self.sublayers, key=lambda s: (groups.index(s.group), -s.weight.numel()))
-        for s in order:
-            st = streams[sstream[s.name]]
-            st.wait_event(hdone[s.group])
-            U[s.group].record_stream(st)
-            dead[s.group].record_stream(st)
+        for b, k in zip(batches, bstream):
+            st = streams[k]
+            g = b[0].group
+            st.wait_event(hdone[g])
+            U[g].record_stream(st)
+            dead[g].record_stream(st)
             with torch.cuda.stream(st):
-                work[s.name] = self._blocks(s, U[s.group], dead[s.group])
-                sdone[s.name] = timed(st)
+                work.update(self._blocks(b, U[g], dead[g]))
+                e = timed(st)
+            for s in b:
+                sdone[s.name] = e
         torch.cuda.synchronize(self.dev)
         # the first attempt of every factorization has finished: read its
         # outcome; retries / fallback (rare) recompute U and its sublayers
@@ -199,9 +235,9 @@ class LayerQuantizer:
                 # the retries / fallback write U on the factor's stream and
                 # return without waiting: the redo below runs on `main`
                 main.wait_stream(jobs[g].stream)
-        for s in order:
-            if s.group in redo:
-                work[s.name] = self._blocks(s, U[s.group], dead[s.group])
+        for b in batches:
+            if b[0].group in redo:
+                work.update(self._blocks(b, U[b[0].group], dead[b[0].group]))
         if self.keep_factors:
             self.factors = {g: (jobs[g].H, U[g]) for g in groups}
             self.quantized = {s.name: (work[s.name][0], work[s.name][1]) for s in order}

@@ -1,0 +1,96 @@
+"""crbq_fasterquant_batched (the block loop of up to four same-shape
+sublayers that share one inverse factor, q/k/v or gate/up, with every
+launch covering all of them) against one crbq_fasterquant call per
+sublayer: bitwise-equal weights, losses, masks and block traces for every
+sublayer, across methods, both partitions, ragged shapes, row strides that
+rule out the 16-byte path, and GPTQ off."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _factor(C, seed):
+    from crb_amd import kernels
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    X = torch.randn(4 * C, C, generator=g, device=DEV) * torch.exp(
+        torch.randn(C, generator=g, device=DEV))
+    H = (X.t() @ X) * (2.0 / 16)
+    U, retries, fb = kernels.hinv_upper(H, None, 0.01)
+    assert retries == 0 and not fb
+    return U
+
+
+def _weights(n, R, C, ldw, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    base = torch.randn(n, R, ldw, generator=g, device=DEV) * 0.02
+    for i in range(n):
+        base[i, :, torch.randperm(C, generator=g, device=DEV)[:max(1, C // 50)]] *= 8
+    return base
+
+
+def _one_by_one(base, C, U, p):
+    from crb_amd import kernels
+    out = []
+    for i in range(base.shape[0]):
+        W = base[i].clone()[:, :C]
+        L = torch.zeros(W.shape[0], device=DEV)
+        m, t = kernels.fasterquant_blocks(W, U, p, L, want_masks=True, want_traces=True)
+        out.append((W, L, m, t))
+    return out
+
+
+@pytest.mark.parametrize("method,partition,gptq", [
+    ("crb", 3, True), ("braq", 3, True), ("crbog", 3, True), ("crb", 1, True),
+    ("crb", 3, False)])
+@pytest.mark.parametrize("n,R,C,ldw,seed", [
+    (3, 4096, 1280, 1280, 1),      # q/k/v of a 1280-wide block
+    (2, 1000, 384, 384, 2),        # gate/up
+    (4, 333, 200, 203, 3),         # ragged last block, rows not 16-byte aligned
+])
+def test_batched_matches_one_call_per_sublayer(method, partition, gptq, n, R, C, ldw, seed):
+    from crb_amd import _lib, kernels
+    print(f"batched n={n} {R}x{C} ldw={ldw} {method} p{partition} gptq={gptq}", flush=True)
+    p = _lib.params(method, partition=partition, disable_gptq=not gptq)
+    U = _factor(C, seed)
+    base = _weights(n, R, C, ldw, seed)
+    ref = _one_by_one(base, C, U, p)
+    Wb = base.clone()
+    Ws = [Wb[i][:, :C] for i in range(n)]
+    Ls = [torch.zeros(R, device=DEV) for _ in range(n)]
+    masks, traces = kernels.fasterquant_blocks_batched(Ws, U, p, Ls, want_masks=True,
+                                                       want_traces=True)
+    torch.cuda.synchronize()
+    for i in range(n):
+        W, L, m, t = ref[i]
+        assert torch.equal(Ws[i], W), i
+        assert torch.equal(Ls[i], L), i
+        assert torch.equal(masks[i], m), i
+        assert traces[i] == t, i
+        # columns beyond C of the padded rows are untouched
+        assert torch.equal(Wb[i][:, C:], base[i][:, C:]), i
+
+
+def test_batched_single_segment_and_argument_checks():
+    from crb_amd import _lib, kernels
+    print("batched nseg=1 and argument checks", flush=True)
+    p = _lib.params("crb")
+    R, C = 512, 256
+    U = _factor(C, 5)
+    base = _weights(1, R, C, C, 5)
+    ref = _one_by_one(base, C, U, p)
+    W = base[0].clone()
+    L = torch.zeros(R, device=DEV)
+    masks, _ = kernels.fasterquant_blocks_batched([W], U, p, [L], want_masks=True)
+    assert torch.equal(W, ref[0][0]) and torch.equal(L, ref[0][1])
+    assert torch.equal(masks[0], ref[0][2])
+    five = [base[0].clone() for _ in range(5)]
+    with pytest.raises(_lib.CrbqError):
+        kernels.fasterquant_blocks_batched(five, U, p, [torch.zeros(R, device=DEV)] * 5)
+    with pytest.raises(_lib.CrbqError):
+        kernels.fasterquant_blocks_batched([base[0].clone(), base[0][:, :C - 8].clone()], U, p,
+                                           [torch.zeros(R, device=DEV)] * 2)
+    lib = _lib.load()
+    assert lib.crbq_fasterquant_batched_workspace_size(0, R, C, p) == 0
+    assert lib.crbq_fasterquant_batched_workspace_size(5, R, C, p) == 0
