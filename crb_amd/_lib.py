@@ -89,7 +89,7 @@ _SIGS = {
     "crbq_fasterquant_batched_workspace_size": (c_size, [c_i32, c_i64, c_i64,
                                                          ctypes.POINTER(CrbqParams)]),
     "crbq_fasterquant_batched": (c_i32, [c_i32, ctypes.POINTER(c_vp), c_i64, c_i64, c_i64,
-                                         c_vp, c_i64, ctypes.POINTER(CrbqParams),
+                                         ctypes.POINTER(c_vp), c_i64, ctypes.POINTER(CrbqParams),
                                          ctypes.POINTER(c_vp), ctypes.POINTER(c_vp), c_i64,
                                          ctypes.POINTER(c_vp), c_vp, c_size, c_vp]),
     "crbq_fasterquant_noalloc": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, c_i64,

@@ -100,14 +100,16 @@ struct SearchWs {
   float* pvals;      // [NQ]
 };
 
-// Sublayers that share one inverse factor (q/k/v, Llama's gate/up) run one
-// block loop together: every search and quantize launch covers up to NSEG
-// of them, blockIdx.y selecting the sublayer (its weights, search scratch
-// and trace), and each sublayer's work is exactly that of a launch of its
-// own (same workgroups, same reductions, same bits).
+// Sublayers of one shape (q/k/v/out of an attention block, Llama's
+// gate/up) run one block loop together: every search and quantize launch
+// covers up to NSEG of them, blockIdx.y selecting the sublayer (its
+// weights, inverse factor, search scratch and trace), and each sublayer's
+// work is exactly that of a launch of its own (same workgroups, same
+// reductions, same bits).
 constexpr int NSEG = 4;
 struct SegSearch {
   const float* W[NSEG];
+  const float* U[NSEG];   // the block's diagonal corner of each factor
   SearchWs s[NSEG];
   crbq_block_trace* tr[NSEG];
 };
@@ -248,9 +250,10 @@ __device__ int wave_argmin(const double* v, int n) {
 constexpr int CS_PH = CRBQ_CS_PH;            // row phases per workgroup
 constexpr int CS_THREADS = NCMAX * CS_PH;
 __global__ __launch_bounds__(CS_THREADS) void k_colscore(
-    SegSearch seg, int64_t ldw, int R, int nc, const float* __restrict__ U, int64_t ldu,
+    SegSearch seg, int64_t ldw, int R, int nc, int64_t ldu,
     int metric) {
   const float* __restrict__ W = seg.W[blockIdx.y];
+  const float* __restrict__ U = seg.U[blockIdx.y];
   const SearchWs s = seg.s[blockIdx.y];
   __shared__ double part[CS_PH][NCMAX];
   __shared__ double red[CS_PH][NCMAX];
@@ -352,9 +355,10 @@ __device__ __forceinline__ void q_cols(const float* __restrict__ U, int64_t ldu,
 
 // Level-1: histogram of bits [31:20] of the (non-negative) float pattern.
 __global__ __launch_bounds__(256) void k_qpass1(
-    SegSearch seg, int64_t ldw, int R, int nc, const float* __restrict__ U, int64_t ldu,
+    SegSearch seg, int64_t ldw, int R, int nc, int64_t ldu,
     int metric) {
   const float* __restrict__ W = seg.W[blockIdx.y];
+  const float* __restrict__ U = seg.U[blockIdx.y];
   const SearchWs s = seg.s[blockIdx.y];
   __shared__ uint32_t lh[H1];
   __shared__ float d2s[NCMAX];
@@ -454,9 +458,10 @@ __device__ __forceinline__ int find_bin(const uint32_t* cum, uint32_t r) {
 // order inside a list does not matter to the selection).  The list counters
 // are cleared by k_colscore.
 __global__ __launch_bounds__(256) void k_qlist(
-    SegSearch seg, int64_t ldw, int R, int nc, const float* __restrict__ U, int64_t ldu,
+    SegSearch seg, int64_t ldw, int R, int nc, int64_t ldu,
     int metric) {
   const float* __restrict__ W = seg.W[blockIdx.y];
+  const float* __restrict__ U = seg.U[blockIdx.y];
   const SearchWs s = seg.s[blockIdx.y];
   __shared__ uint32_t cum[H1];
   __shared__ int lead[H1];
@@ -857,9 +862,10 @@ __device__ __forceinline__ void wave_prefix(SortedRow& r, float x0, float x1, in
 // pairs over all its lanes, each two binary searches per group and range
 // sums (group_err1); the last workgroup takes k* = first strict minimum.
 __global__ __launch_bounds__(64 * PC_WAVES) void k_phase_c(
-    SegSearch seg, int64_t ldw, int R, int nc, const float* __restrict__ U, int64_t ldu,
+    SegSearch seg, int64_t ldw, int R, int nc, int64_t ldu,
     int metric) {
   const float* __restrict__ W = seg.W[blockIdx.y];
+  const float* __restrict__ U = seg.U[blockIdx.y];
   const SearchWs s = seg.s[blockIdx.y];
   crbq_block_trace* const tr = seg.tr[blockIdx.y];
   __shared__ SortedRow rows[PC_WAVES];
@@ -945,8 +951,8 @@ struct QuantSegs {                   // one per sublayer of the launch (blockIdx
 
 template <int MF, int EPL>
 __global__ __launch_bounds__(256) void k_quantize(QuantSegs qs) {
-  const QuantArgs a = qs.a[blockIdx.y];
-  const SearchWs s = qs.s[blockIdx.y];
+  const QuantArgs& a = qs.a[blockIdx.y];
+  const SearchWs& s = qs.s[blockIdx.y];
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= a.R) return;
@@ -1036,8 +1042,8 @@ __device__ __forceinline__ void vstore(float* p, const float* v) {
 constexpr int QG_LPR = CRBQ_QG_LPR;          // lanes per row of the block quantize
 template <int MF>
 __global__ __launch_bounds__(256) void k_quantize_g(QuantSegs qs) {
-  const QuantArgs a = qs.a[blockIdx.y];
-  const SearchWs s = qs.s[blockIdx.y];
+  const QuantArgs& a = qs.a[blockIdx.y];
+  const SearchWs& s = qs.s[blockIdx.y];
   constexpr int LPR = QG_LPR, EPL = 128 / LPR, VW = EPL < 4 ? EPL : 4, NH = EPL / VW;
   const int r = threadIdx.x % LPR;
   const int row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
@@ -1135,8 +1141,14 @@ __global__ __launch_bounds__(256) void k_quantize_g(QuantSegs qs) {
 }
 
 // clears the arrival counters of the last-workgroup reductions
-__global__ void k_init_ctrl(SearchWs s) {
-  if (threadIdx.x < 4) s.ctrl->cnt[threadIdx.x] = 0u;
+// Arrival counters of every segment's search scratch cleared (thread
+// 4 i + j: counter j of segment i).
+struct SegCtrl {
+  Ctrl* c[NSEG];
+};
+__global__ void k_init_ctrl(SegCtrl g, int nseg) {
+  const int t = threadIdx.x;
+  if (t < 4 * nseg) g.c[t >> 2]->cnt[t & 3] = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -1278,9 +1290,10 @@ __device__ __forceinline__ double row_cand_err(const float* x, int i, int nc, do
 }
 
 __global__ __launch_bounds__(64 * PR_CW) void k_phase_a_rows(
-    SegSearch seg, int64_t ldw, int R, int nc, const float* __restrict__ U, int64_t ldu,
+    SegSearch seg, int64_t ldw, int R, int nc, int64_t ldu,
     int metric, int ncand, int up_lim, int ncg, int cw) {
   const float* __restrict__ W = seg.W[blockIdx.y];
+  const float* __restrict__ U = seg.U[blockIdx.y];
   const SearchWs s = seg.s[blockIdx.y];
   crbq_block_trace* const tr = seg.tr[blockIdx.y];
   constexpr int LMAX = (64 + PR_MINW - 1) / PR_MINW;   // rows loaded per wavefront
@@ -1355,7 +1368,7 @@ __global__ __launch_bounds__(64 * PR_CW) void k_phase_a_rows(
 // host drivers
 // ---------------------------------------------------------------------------
 static int search_block(const SegSearch& seg, int nseg, int64_t ldw, int R, int nc,
-                        const float* U, int64_t ldu, int metric, int up_lim, hipStream_t st) {
+                        int64_t ldu, int metric, int up_lim, hipStream_t st) {
   const int ncand = up_lim - 1;
   const int nwg_cs = (int)std::min<int64_t>(cdiv(R, CS_PH), CS_MAXWG);
   const int nwg_q = (int)cdiv(R, Q_RPW);
@@ -1365,13 +1378,13 @@ static int search_block(const SegSearch& seg, int nseg, int64_t ldw, int R, int 
   const int ncg = (int)cdiv(ncand, PR_CW), cw = (int)cdiv(ncand, ncg);
   const int nrg = (int)std::min<int64_t>(cdiv(R, 64), PX_MAXWG);
   const unsigned y = (unsigned)nseg;
-  k_colscore<<<dim3(nwg_cs, y), CS_THREADS, 0, st>>>(seg, ldw, R, nc, U, ldu, metric);
+  k_colscore<<<dim3(nwg_cs, y), CS_THREADS, 0, st>>>(seg, ldw, R, nc, ldu, metric);
   k_phase_a_rows<<<dim3(nrg * ncg, y), 64 * std::max(cw, PR_MINW), 0, st>>>(
-      seg, ldw, R, nc, U, ldu, metric, ncand, up_lim, ncg, cw);
-  k_qpass1<<<dim3(nwg_q, y), 256, 0, st>>>(seg, ldw, R, nc, U, ldu, metric);
-  k_qlist<<<dim3(nwg_q, y), 256, 0, st>>>(seg, ldw, R, nc, U, ldu, metric);
+      seg, ldw, R, nc, ldu, metric, ncand, up_lim, ncg, cw);
+  k_qpass1<<<dim3(nwg_q, y), 256, 0, st>>>(seg, ldw, R, nc, ldu, metric);
+  k_qlist<<<dim3(nwg_q, y), 256, 0, st>>>(seg, ldw, R, nc, ldu, metric);
   k_qselect<<<dim3(NT, y), QS_T, 0, st>>>(seg, R, nc);
-  k_phase_c<<<dim3(nwg_c, y), 64 * PC_WAVES, 0, st>>>(seg, ldw, R, nc, U, ldu, metric);
+  k_phase_c<<<dim3(nwg_c, y), 64 * PC_WAVES, 0, st>>>(seg, ldw, R, nc, ldu, metric);
   CRBQ_LAUNCH_CHECK();
   return CRBQ_OK;
 }
@@ -1477,12 +1490,15 @@ extern "C" int crbq_block_search(const float* W, int64_t R, int32_t ncols, int64
   int st = ensure_q_table();
   if (st) return st;
   hipStream_t hs = (hipStream_t)stream;
-  k_init_ctrl<<<1, 64, 0, hs>>>(s);
+  SegCtrl sc{};
+  sc.c[0] = s.ctrl;
+  k_init_ctrl<<<1, 64, 0, hs>>>(sc, 1);
   SegSearch seg{};
   seg.W[0] = W;
+  seg.U[0] = Ublk;
   seg.s[0] = s;
   seg.tr[0] = trace;
-  st = search_block(seg, 1, ldw, (int)R, ncols, Ublk, ldu, metric, up_lim, hs);
+  st = search_block(seg, 1, ldw, (int)R, ncols, ldu, metric, up_lim, hs);
   if (st) return st;
   if (masks) {
     const int64_t n = R * (int64_t)ncols;
@@ -1512,21 +1528,22 @@ extern "C" size_t crbq_fasterquant_workspace_size(int64_t R, int64_t C, const cr
 }
 
 namespace crbq {
-// The block loop over nseg sublayers of one shape that share the factor U
-// (nseg = 1: one sublayer).  Segment i has its own weights W[i], losses,
-// masks, traces and its own part of the workspace (search scratch and the
-// super-block's error rows), so its results are those of a call of its own.
+// The block loop over nseg sublayers of one shape (nseg = 1: one
+// sublayer).  Segment i has its own weights Ws[i], factor Us[i] (segments
+// may share one), losses, masks, traces and its own part of the workspace
+// (search scratch and the super-block's error rows), so its results are
+// those of a call of its own.
 static int fasterquant_impl(int nseg, float* const* Ws, int64_t R, int64_t C, int64_t ldw,
-                            const float* U, int64_t ldu, const crbq_params* p,
+                            const float* const* Us, int64_t ldu, const crbq_params* p,
                             float* const* losses, uint8_t* const* masks, int64_t ldm,
                             crbq_block_trace* const* traces, void* ws, size_t ws_bytes,
                             void* stream) {
   int st = check_params(p);
   if (st) return st;
-  if (nseg < 1 || nseg > NSEG || !Ws || !losses) return CRBQ_ERR_ARG;
-  if (!U || R <= 0 || C <= 0 || ldw < C || ldu < C) return CRBQ_ERR_ARG;
+  if (nseg < 1 || nseg > NSEG || !Ws || !Us || !losses) return CRBQ_ERR_ARG;
+  if (R <= 0 || C <= 0 || ldw < C || ldu < C) return CRBQ_ERR_ARG;
   for (int i = 0; i < nseg; ++i)
-    if (!Ws[i] || !losses[i]) return CRBQ_ERR_ARG;
+    if (!Ws[i] || !Us[i] || !losses[i]) return CRBQ_ERR_ARG;
   const bool any_masks = masks && masks[0];
   for (int i = 0; i < nseg; ++i)
     if (masks && ((masks[i] != nullptr) != any_masks)) return CRBQ_ERR_ARG;
@@ -1550,7 +1567,9 @@ static int fasterquant_impl(int nseg, float* const* Ws, int64_t R, int64_t C, in
   st = ensure_q_table();
   if (st) return st;
   hipStream_t hs = (hipStream_t)stream;
-  for (int i = 0; i < nseg; ++i) k_init_ctrl<<<1, 64, 0, hs>>>(s[i]);
+  SegCtrl sc{};
+  for (int i = 0; i < nseg; ++i) sc.c[i] = s[i].ctrl;
+  k_init_ctrl<<<1, 64, 0, hs>>>(sc, nseg);
   CrbConsts k;
   k.lam = p->lam;
   k.omg = (float)(1.0 - (double)p->corr_damp);
@@ -1565,15 +1584,15 @@ static int fasterquant_impl(int nseg, float* const* Ws, int64_t R, int64_t C, in
     const int64_t sb1 = std::min<int64_t>(sb0 + SB, C);
     for (int64_t st0 = sb0; st0 < sb1; st0 += bs, ++bi) {
       const int nc = (int)std::min<int64_t>(bs, sb1 - st0);
-      const float* Ub = U + st0 * ldu + st0;
       if (p->partition == 3) {
         SegSearch seg{};
         for (int i = 0; i < nseg; ++i) {
           seg.W[i] = Ws[i] + st0;
+          seg.U[i] = Us[i] + st0 * ldu + st0;
           seg.s[i] = s[i];
           seg.tr[i] = traces && traces[i] ? traces[i] + bi : nullptr;
         }
-        st = search_block(seg, nseg, ldw, (int)R, nc, Ub, ldu, p->metric, p->up_lim, hs);
+        st = search_block(seg, nseg, ldw, (int)R, nc, ldu, p->metric, p->up_lim, hs);
         if (st) return st;
       }
       QuantSegs qs{};
@@ -1581,7 +1600,7 @@ static int fasterquant_impl(int nseg, float* const* Ws, int64_t R, int64_t C, in
       for (int i = 0; i < nseg; ++i) {
         QuantArgs& a = qs.a[i];
         a.W = Ws[i] + st0; a.ldw = ldw; a.R = (int)R; a.nc = nc;
-        a.U = Ub; a.ldu = ldu;
+        a.U = Us[i] + st0 * ldu + st0; a.ldu = ldu;
         a.metric = p->metric; a.method = p->method; a.partition = p->partition;
         for (int g = 0; g < 3; ++g) a.orders[g] = p->orders[g];
         a.k = k;
@@ -1607,19 +1626,21 @@ static int fasterquant_impl(int nseg, float* const* Ws, int64_t R, int64_t C, in
       CRBQ_LAUNCH_CHECK();
       const int64_t ed = st0 + nc;
       if (gptq && ed < sb1) {            // rest of this super-block
-        for (int i = 0; i < nseg; ++i) {
-          st = sgemm_launch(false, false, false, R, sb1 - ed, nc, -1.f, qs.a[i].err, SB,
-                            U + st0 * ldu + ed, ldu, 1.f, Ws[i] + ed, ldw, nullptr, hs);
-          if (st) return st;
-        }
+        GemmArgs g[NSEG];
+        for (int i = 0; i < nseg; ++i)
+          g[i] = GemmArgs{false, false, false, R, sb1 - ed, nc, -1.f, qs.a[i].err, SB,
+                          Us[i] + st0 * ldu + ed, ldu, 1.f, Ws[i] + ed, ldw, GEMM_TRI_NONE};
+        st = sgemm_seg_launch(nseg, g, hs);
+        if (st) return st;
       }
     }
     if (gptq && sb1 < C) {               // every later column, K = sb1 - sb0
-      for (int i = 0; i < nseg; ++i) {
-        st = sgemm_launch(false, false, false, R, C - sb1, sb1 - sb0, -1.f, err[i], SB,
-                          U + sb0 * ldu + sb1, ldu, 1.f, Ws[i] + sb1, ldw, nullptr, hs);
-        if (st) return st;
-      }
+      GemmArgs g[NSEG];
+      for (int i = 0; i < nseg; ++i)
+        g[i] = GemmArgs{false, false, false, R, C - sb1, sb1 - sb0, -1.f, err[i], SB,
+                        Us[i] + sb0 * ldu + sb1, ldu, 1.f, Ws[i] + sb1, ldw, GEMM_TRI_NONE};
+      st = sgemm_seg_launch(nseg, g, hs);
+      if (st) return st;
     }
   }
   return CRBQ_OK;
@@ -1662,7 +1683,7 @@ extern "C" int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw, con
                                 int64_t ldu, const crbq_params* p, float* losses,
                                 uint8_t* masks, int64_t ldm, crbq_block_trace* traces,
                                 void* ws, size_t ws_bytes, void* stream) {
-  return crbq::fasterquant_impl(1, &W, R, C, ldw, U, ldu, p, &losses, &masks, ldm, &traces,
+  return crbq::fasterquant_impl(1, &W, R, C, ldw, &U, ldu, p, &losses, &masks, ldm, &traces,
                                 ws, ws_bytes, stream);
 }
 
@@ -1673,7 +1694,7 @@ extern "C" size_t crbq_fasterquant_batched_workspace_size(int32_t nseg, int64_t 
 }
 
 extern "C" int crbq_fasterquant_batched(int32_t nseg, float* const* W, int64_t R, int64_t C,
-                                        int64_t ldw, const float* U, int64_t ldu,
+                                        int64_t ldw, const float* const* U, int64_t ldu,
                                         const crbq_params* p, float* const* losses,
                                         uint8_t* const* masks, int64_t ldm,
                                         crbq_block_trace* const* traces, void* ws,
@@ -1703,7 +1724,7 @@ extern "C" int crbq_fasterquant_noalloc(float* W, int64_t R, int64_t C, int64_t 
   void* ws = nullptr;
   const int sst = crbq::scratch_of_current_device(&ws);
   if (sst) return sst;
-  return crbq::fasterquant_impl(1, &W, R, C, ldw, U, ldu, p, &losses, &masks, ldm, &traces,
+  return crbq::fasterquant_impl(1, &W, R, C, ldw, &U, ldu, p, &losses, &masks, ldm, &traces,
                                 ws, CRBQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 

@@ -33,15 +33,6 @@ namespace crbq {
 
 constexpr int NB = 128;
 
-__global__ __launch_bounds__(256) void k_dead(float* H, int64_t ldh, int C, uint8_t* dead) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= C) return;
-  float* p = H + (int64_t)i * ldh + i;
-  const bool d = *p == 0.f;                     // bigptq.py:103-104
-  dead[i] = d;
-  if (d) *p = 1.f;
-}
-
 __global__ __launch_bounds__(256) void k_zero_dead(float* W, int64_t ldw, int R, int C,
                                                    const uint8_t* __restrict__ dead) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -51,10 +42,23 @@ __global__ __launch_bounds__(256) void k_zero_dead(float* W, int64_t ldw, int R,
 }
 
 // H_ii += factor * mean(diag H); retry mode: 1e-6 when that is 0.
+// dead (optional): first the dead columns, H_ii == 0, flagged and set to 1
+// (each thread handles the same diagonal entries in both passes, so the
+// mean sees the 1s).
+// info (optional): the factorization's failure flag, cleared.
 __global__ __launch_bounds__(1024) void k_damp(float* H, int64_t ldh, int C, float factor,
-                                               int retry, float* out) {
+                                               int retry, float* out, uint8_t* dead,
+                                               int* info) {
   __shared__ double red[1024];
   const int tid = threadIdx.x;
+  if (dead)
+    for (int i = tid; i < C; i += 1024) {
+      float* p = H + (int64_t)i * ldh + i;
+      const bool d = *p == 0.f;                 // bigptq.py:103-104
+      dead[i] = d;
+      if (d) *p = 1.f;
+    }
+  if (info && tid == 0) *info = 0;
   double s = 0.0;
   for (int i = tid; i < C; i += 1024) s += (double)H[(int64_t)i * ldh + i];
   red[tid] = s;
@@ -841,15 +845,13 @@ extern "C" int crbq_hinv_upper_async(float* H, int64_t ldh, int64_t C, float* W,
   if (!c.ok()) return CRBQ_ERR_WORKSPACE;
   hipStream_t s = (hipStream_t)stream;
   const int Ci = (int)C;
-  k_dead<<<nblocks(C), 256, 0, s>>>(H, ldh, Ci, w.dead);
+  // dead columns, damping (bigptq.py:103-111) and the failure flag cleared
+  k_damp<<<1, 1024, 0, s>>>(H, ldh, Ci, percdamp, 0, w.scal, w.dead, w.info);
   CRBQ_LAUNCH_CHECK();
   if (W) {
     k_zero_dead<<<nblocks(R * C), 256, 0, s>>>(W, ldw, (int)R, Ci, w.dead);
     CRBQ_LAUNCH_CHECK();
   }
-  k_damp<<<1, 1024, 0, s>>>(H, ldh, Ci, percdamp, 0, w.scal);      // bigptq.py:109-111
-  CRBQ_LAUNCH_CHECK();
-  k_set_int<<<1, 1, 0, s>>>(w.info, 0);
   k_reverse_lower<<<rows_grid(C), 256, 0, s>>>(H, ldh, Ci, w.A, C,
                                                 reverse_vec(H, ldh, C, w.A, C));
   CRBQ_LAUNCH_CHECK();
@@ -882,7 +884,7 @@ extern "C" int crbq_hinv_upper_finish(float* H, int64_t ldh, int64_t C, float* U
   bool ok = hinfo == 0;
   for (int attempt = 1; !ok && attempt <= 10; ++attempt) {        // bigptq.py:115-123
     ++nretry;
-    k_damp<<<1, 1024, 0, s>>>(H, ldh, Ci, 1e-3f, 1, w.scal);
+    k_damp<<<1, 1024, 0, s>>>(H, ldh, Ci, 1e-3f, 1, w.scal, nullptr, nullptr);
     CRBQ_LAUNCH_CHECK();
     if (attempt == 10) break;                                       // 10 attempts in all
     k_set_int<<<1, 1, 0, s>>>(w.info, 0);

@@ -35,4 +35,8 @@ struct GemmArgs {
 // allowed).  One launch when both pick the same tile size, with x's tiles
 // first; otherwise the two launches of sgemm_launch in order.
 int sgemm2_launch(const GemmArgs& x, const GemmArgs& y, const int* stop, hipStream_t s);
+// nseg (1..4) plain products op(A) B with no transposes, no triangle and
+// one shape (M, N, K): one launch, each product computed as its own
+// sgemm_launch would; otherwise one sgemm_launch per product in order.
+int sgemm_seg_launch(int nseg, const GemmArgs* gs, hipStream_t s);
 }  // namespace crbq

@@ -436,6 +436,23 @@ __global__ __launch_bounds__(256) void k_sgemm2(SgP p1, int n1, SgP p2,
     sgemm_tile<BT, TA2, TB2, LO2>(p2, As, Bs, (int)blockIdx.x - n1, (int)gridDim.x - n1);
 }
 
+// Up to SG_NSEG products of one shape, one per blockIdx.y: the block loop
+// of sublayers that share the factor updates each one's weights with its
+// own error rows against the same U rows, all in one launch.  Every
+// product's tiles are those of its own k_sgemm launch (same tile size,
+// same grid, same sums).
+constexpr int SG_NSEG = 4;
+struct SgSeg {
+  SgP p[SG_NSEG];
+};
+
+template <int BT>
+__global__ __launch_bounds__(256) void k_sgemm_seg(SgSeg g) {
+  __shared__ __attribute__((aligned(16))) float As[2][TileCfg<BT>::ELEMS];
+  __shared__ __attribute__((aligned(16))) float Bs[2][TileCfg<BT>::ELEMS];
+  sgemm_tile<BT, false, false, false>(g.p[blockIdx.y], As, Bs, blockIdx.x, gridDim.x);
+}
+
 static inline bool vec_ok(const float* p, int64_t ld) {
   return ((((uintptr_t)p) & 15) == 0) && ((ld & 3) == 0);
 }
@@ -501,6 +518,44 @@ int sgemm_launch(bool ta, bool tb, bool lower, int64_t M, int64_t N, int64_t K,
                         tri);
   return sgemm_go<128>(ta, tb, lower, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stop, s,
                        tri);
+}
+
+static SgP sg_params(const GemmArgs& g);
+
+template <int BT>
+static int sgemm_seg_go(int nseg, const GemmArgs* gs, hipStream_t s) {
+  const int64_t nwg = ((gs[0].M + BT - 1) / BT) * ((gs[0].N + BT - 1) / BT);
+  if (nwg > 0x7fffffff) return CRBQ_ERR_ARG;
+  SgSeg g{};
+  for (int i = 0; i < nseg; ++i) g.p[i] = sg_params(gs[i]);
+  k_sgemm_seg<BT><<<dim3((unsigned)nwg, (unsigned)nseg), 256, 0, s>>>(g);
+  CRBQ_LAUNCH_CHECK();
+  return CRBQ_OK;
+}
+
+int sgemm_seg_launch(int nseg, const GemmArgs* gs, hipStream_t s) {
+  if (nseg < 1 || nseg > SG_NSEG) return CRBQ_ERR_ARG;
+  const GemmArgs& g0 = gs[0];
+  bool same = true;
+  for (int i = 0; i < nseg; ++i) {
+    const GemmArgs& g = gs[i];
+    same = same && !g.ta && !g.tb && !g.lower && g.tri == GEMM_TRI_NONE && g.M == g0.M &&
+           g.N == g0.N && g.K == g0.K;
+  }
+  if (!same || nseg == 1 || g0.M <= 0 || g0.N <= 0 || g0.M > (1 << 30) ||
+      g0.N > (1 << 30) || g0.K < 0 || g0.K > (1 << 30)) {
+    for (int i = 0; i < nseg; ++i) {
+      const GemmArgs& g = gs[i];
+      const int st = sgemm_launch(g.ta, g.tb, g.lower, g.M, g.N, g.K, g.alpha, g.A, g.lda, g.B,
+                                  g.ldb, g.beta, g.C, g.ldc, nullptr, s, g.tri);
+      if (st) return st;
+    }
+    return CRBQ_OK;
+  }
+  const int bt = tile_of(g0.M, g0.N);
+  if (bt == 32) return sgemm_seg_go<32>(nseg, gs, s);
+  if (bt == 64) return sgemm_seg_go<64>(nseg, gs, s);
+  return sgemm_seg_go<128>(nseg, gs, s);
 }
 
 static SgP sg_params(const GemmArgs& g) {

@@ -12,10 +12,10 @@ Hessians and therefore identical inverse factors U.  This driver
   * enqueues every sublayer's block loop right behind its factor (an event
     wait, no host synchronisation), the widest input's chain first and on
     a stream of its own since it is the longest,
-  * runs the block loops of up to four same-shape sublayers of one input
-    (q/k/v, gate/up) as one loop whose launches cover all of them
-    (kernels.fasterquant_blocks_batched: same results, a third of the
-    launches for q/k/v),
+  * runs the block loops of up to four sublayers of one weight shape
+    (q/k/v/out, gate/up), each with its own input's factor, as one loop
+    whose launches cover all of them (kernels.fasterquant_blocks_batched:
+    the same results, a quarter of the launches for q/k/v/out),
   * checks the factorizations once at the end and, for an input whose
     Cholesky needed the reference's retries or fallback (bigptq.py:114-126),
     recomputes its sublayers with the final factor,
@@ -130,57 +130,60 @@ class LayerQuantizer:
 
     def _batches(self, groups):
         """The sublayers in the order their loops are enqueued (the widest
-        input's first, larger weights first), cut into batches: runs of up
-        to kernels.MAX_BATCH sublayers of one input, weight shape and dtype
-        (single sublayers when batching is off)."""
+        input's first, larger weights first), and that order cut into
+        batches: sublayers of one weight shape and dtype, whatever input
+        they read, up to kernels.MAX_BATCH per batch, in order of first
+        appearance (single sublayers when batching is off)."""
         order = sorted(self.sublayers, key=lambda s: (groups.index(s.group), -s.weight.numel()))
-        out = []
+        if not self.batch_sublayers:
+            return order, [[s] for s in order]
+        buckets = {}
         for s in order:
-            b = out[-1] if out else None
-            if (self.batch_sublayers and b is not None and len(b) < kernels.MAX_BATCH
-                    and b[0].group == s.group and b[0].weight.shape == s.weight.shape
-                    and b[0].weight.dtype == s.weight.dtype):
-                b.append(s)
-            else:
-                out.append([s])
+            buckets.setdefault((tuple(s.weight.shape), s.weight.dtype), []).append(s)
+        out = []
+        for lst in buckets.values():
+            for i in range(0, len(lst), kernels.MAX_BATCH):
+                out.append(lst[i:i + kernels.MAX_BATCH])
         return order, out
 
     def _assign_streams(self, groups, batches):
-        """The widest input gets stream 0 for its factor and its sublayers;
-        the other factors and the batches of sublayers share the remaining
-        streams, balanced by weight count."""
+        """The widest input gets stream 0 for its factor and the batches
+        holding its sublayers; the other factors and batches share the
+        remaining streams, balanced by weight count."""
         ns = self.nstreams
         gstream = {}
         for i, g in enumerate(groups):
             gstream[g] = 0 if i == 0 or ns == 1 else 1 + (i - 1) % (ns - 1)
         load = [0] * ns
-        bstream = []
+        bstream = [0] * len(batches)
         for i in sorted(range(len(batches)), key=lambda i: -sum(s.weight.numel()
                                                                for s in batches[i])):
             b = batches[i]
-            if b[0].group == groups[0] or ns == 1:
+            if ns == 1 or any(s.group == groups[0] for s in b):
                 k = 0
             else:
                 k = min(range(1, ns), key=lambda j: load[j])
             load[k] += sum(s.weight.numel() for s in b)
-            bstream.append((i, k))
-        return gstream, [k for _, k in sorted(bstream)]
+            bstream[i] = k
+        return gstream, bstream
 
     def _blocks(self, batch, U, dead):
-        """Block loops of one batch: {name: (W fp32, losses, masks)}."""
+        """Block loops of one batch (U, dead: per input): {name: (W fp32,
+        losses, masks)}."""
         Ws, ls = [], []
         for s in batch:
             W = s.weight.float() if s.weight.dtype != torch.float32 else s.weight.clone()
             W = W.contiguous()
-            W.masked_fill_(dead[None, :], 0.0)                           # bigptq.py:105
+            W.masked_fill_(dead[s.group][None, :], 0.0)                  # bigptq.py:105
             Ws.append(W)
             ls.append(torch.zeros(W.shape[0], device=self.dev))
         if len(batch) == 1:
-            m, _ = kernels.fasterquant_blocks(Ws[0], U, self.p, ls[0], want_masks=self.keep_masks)
+            m, _ = kernels.fasterquant_blocks(Ws[0], U[batch[0].group], self.p, ls[0],
+                                              want_masks=self.keep_masks)
             masks = [m]
         else:
-            masks, _ = kernels.fasterquant_blocks_batched(Ws, U, self.p, ls,
-                                                          want_masks=self.keep_masks)
+            masks, _ = kernels.fasterquant_blocks_batched(Ws, [U[s.group] for s in batch],
+                                                          self.p, ls, want_masks=self.keep_masks)
         return {s.name: (Ws[i], ls[i], masks[i]) for i, s in enumerate(batch)}
 
     def quantize(self, times: PhaseTimes | None = None) -> dict:
@@ -214,12 +217,12 @@ class LayerQuantizer:
         # the widest input's sublayers first (their chain is the longest)
         for b, k in zip(batches, bstream):
             st = streams[k]
-            g = b[0].group
-            st.wait_event(hdone[g])
-            U[g].record_stream(st)
-            dead[g].record_stream(st)
+            for g in dict.fromkeys(s.group for s in b):
+                st.wait_event(hdone[g])
+                U[g].record_stream(st)
+                dead[g].record_stream(st)
             with torch.cuda.stream(st):
-                work.update(self._blocks(b, U[g], dead[g]))
+                work.update(self._blocks(b, U, dead))
                 e = timed(st)
             for s in b:
                 sdone[s.name] = e
@@ -236,8 +239,8 @@ class LayerQuantizer:
                 # return without waiting: the redo below runs on `main`
                 main.wait_stream(jobs[g].stream)
         for b in batches:
-            if b[0].group in redo:
-                work.update(self._blocks(b, U[b[0].group], dead[b[0].group]))
+            if any(s.group in redo for s in b):
+                work.update(self._blocks(b, U, dead))
         if self.keep_factors:
             self.factors = {g: (jobs[g].H, U[g]) for g in groups}
             self.quantized = {s.name: (work[s.name][0], work[s.name][1]) for s in order}

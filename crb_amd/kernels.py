@@ -200,39 +200,47 @@ def fasterquant_blocks(W: torch.Tensor, U: torch.Tensor, p: _lib.CrbqParams,
 MAX_BATCH = 4   # sublayers per crbq_fasterquant_batched call
 
 
-def fasterquant_blocks_batched(Ws, U: torch.Tensor, p: _lib.CrbqParams, losses,
+def fasterquant_blocks_batched(Ws, Us, p: _lib.CrbqParams, losses,
                                want_masks: bool = False, want_traces: bool = False):
-    """fasterquant_blocks on up to MAX_BATCH same-shape weights that share
-    the factor U (q/k/v, gate/up), as one block loop.  Every W is updated in
-    place and every losses[i] accumulated exactly as fasterquant_blocks
-    would for it alone.  Returns ([masks or None], [traces or None])."""
+    """fasterquant_blocks on up to MAX_BATCH weights of one shape and row
+    stride, as one block loop.  Us is one factor for all of them or a list
+    with one factor per weight (all of one size and row stride).  Every W
+    is updated in place and every losses[i] accumulated exactly as
+    fasterquant_blocks would for it alone.  Returns ([masks or None],
+    [traces or None])."""
     n = len(Ws)
-    if not 1 <= n <= MAX_BATCH or len(losses) != n:
+    if isinstance(Us, torch.Tensor):
+        Us = [Us] * n
+    if not 1 <= n <= MAX_BATCH or len(losses) != n or len(Us) != n:
         raise _lib.CrbqError(f"fasterquant_blocks_batched takes 1..{MAX_BATCH} weights and "
-                             "as many loss vectors")
-    _dev_check(U, *Ws, *losses)
+                             "as many factors and loss vectors")
+    Us = [U if U.stride(1) == 1 else U.contiguous() for U in Us]
+    _dev_check(*Us, *Ws, *losses)
     R, C = Ws[0].shape
-    ldw = Ws[0].stride(0)
+    ldw, ldu = Ws[0].stride(0), Us[0].stride(0)
     for W in Ws:
         if W.dtype != torch.float32 or W.stride(1) != 1:
             raise _lib.CrbqError("fasterquant_blocks_batched works in place on row-major fp32 W")
         if tuple(W.shape) != (R, C) or W.stride(0) != ldw:
             raise _lib.CrbqError("fasterquant_blocks_batched needs weights of one shape and stride")
-    if U.stride(1) != 1:
-        U = U.contiguous()
-    lib = _lib.ready(U.device)
-    ws = _ws(lib.crbq_fasterquant_batched_workspace_size(n, R, C, ctypes.byref(p)), U.device)
-    masks = [torch.zeros((R, C), dtype=torch.uint8, device=U.device) if want_masks else None
+    for U in Us:
+        if U.dtype != torch.float32 or tuple(U.shape) != (C, C) or U.stride(0) != ldu:
+            raise _lib.CrbqError("fasterquant_blocks_batched needs fp32 C x C factors of one "
+                                 "row stride")
+    dev = Ws[0].device
+    lib = _lib.ready(dev)
+    ws = _ws(lib.crbq_fasterquant_batched_workspace_size(n, R, C, ctypes.byref(p)), dev)
+    masks = [torch.zeros((R, C), dtype=torch.uint8, device=dev) if want_masks else None
              for _ in range(n)]
     nblk = (C + p.blocksize - 1) // p.blocksize
-    trs = [torch.zeros(nblk * _lib.TRACE_BYTES, dtype=torch.uint8, device=U.device)
+    trs = [torch.zeros(nblk * _lib.TRACE_BYTES, dtype=torch.uint8, device=dev)
            if want_traces else None for _ in range(n)]
     arr = ctypes.c_void_p * n
     check(lib.crbq_fasterquant_batched(
-        n, arr(*[W.data_ptr() for W in Ws]), R, C, ldw, U.data_ptr(), U.stride(0),
+        n, arr(*[W.data_ptr() for W in Ws]), R, C, ldw, arr(*[U.data_ptr() for U in Us]), ldu,
         ctypes.byref(p), arr(*[x.data_ptr() for x in losses]), arr(*[ptr(m) for m in masks]),
         masks[0].stride(0) if want_masks else 0, arr(*[ptr(t) for t in trs]),
-        ws.data_ptr(), ws.numel(), stream_of(U)), "crbq_fasterquant_batched")
+        ws.data_ptr(), ws.numel(), stream_of(Ws[0])), "crbq_fasterquant_batched")
     traces = [decode_traces(t, nblk) if t is not None else None for t in trs]
     return masks, traces
 

@@ -199,20 +199,20 @@ int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw,
                      void* stream);
 
 /* crbq_fasterquant over nseg (1..4) sublayers of one shape (R x C, row
- * stride ldw) that share the inverse factor U: q/k/v of an attention
- * block, or gate/up of a gated MLP.  Replaces nseg consecutive calls of
- * gptq[name].fasterquant(...) in the per-sublayer loop of run.py:286-305
- * (BRAGPTQ.fasterquant, bigptq.py:56-291) when their Hessians are the same
- * matrix, as they are for sublayers fed by one input.  W, losses, masks and
- * traces are HOST arrays of nseg device pointers (masks and traces may be
- * NULL, or arrays whose entries are all NULL); every sublayer's results are
- * bit-for-bit those of its own crbq_fasterquant call with the same params.
- * The block loop runs once, each search and quantize launch covering all
- * nseg sublayers.  Workspace: crbq_fasterquant_batched_workspace_size. */
+ * stride ldw), each with its own inverse factor U[i] (row stride ldu;
+ * entries may repeat): q/k/v/out of an attention block, gate/up of a gated
+ * MLP.  Replaces nseg consecutive calls of gptq[name].fasterquant(...) in
+ * the per-sublayer loop of run.py:286-305 (BRAGPTQ.fasterquant,
+ * bigptq.py:56-291).  W, U, losses, masks and traces are HOST arrays of
+ * nseg device pointers (masks and traces may be NULL, or arrays whose
+ * entries are all NULL); every sublayer's results are bit for bit those of
+ * its own crbq_fasterquant call with the same params.  The block loop runs
+ * once, each search, quantize and update launch covering all nseg
+ * sublayers.  Workspace: crbq_fasterquant_batched_workspace_size. */
 size_t crbq_fasterquant_batched_workspace_size(int32_t nseg, int64_t R, int64_t C,
                                                const crbq_params* p);
 int crbq_fasterquant_batched(int32_t nseg, float* const* W, int64_t R, int64_t C,
-                             int64_t ldw, const float* U, int64_t ldu,
+                             int64_t ldw, const float* const* U, int64_t ldu,
                              const crbq_params* p, float* const* losses,
                              uint8_t* const* masks, int64_t ldm,
                              crbq_block_trace* const* traces, void* ws,

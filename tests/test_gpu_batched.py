@@ -1,6 +1,6 @@
-"""crbq_fasterquant_batched (the block loop of up to four same-shape
-sublayers that share one inverse factor, q/k/v or gate/up, with every
-launch covering all of them) against one crbq_fasterquant call per
+"""crbq_fasterquant_batched (the block loop of up to four sublayers of one
+shape, q/k/v/out or gate/up, each with its own or a shared inverse factor,
+every launch covering all of them) against one crbq_fasterquant call per
 sublayer: bitwise-equal weights, losses, masks and block traces for every
 sublayer, across methods, both partitions, ragged shapes, row strides that
 rule out the 16-byte path, and GPTQ off."""
@@ -30,13 +30,13 @@ def _weights(n, R, C, ldw, seed):
     return base
 
 
-def _one_by_one(base, C, U, p):
+def _one_by_one(base, C, Us, p):
     from crb_amd import kernels
     out = []
     for i in range(base.shape[0]):
         W = base[i].clone()[:, :C]
         L = torch.zeros(W.shape[0], device=DEV)
-        m, t = kernels.fasterquant_blocks(W, U, p, L, want_masks=True, want_traces=True)
+        m, t = kernels.fasterquant_blocks(W, Us[i], p, L, want_masks=True, want_traces=True)
         out.append((W, L, m, t))
     return out
 
@@ -49,18 +49,24 @@ def _one_by_one(base, C, U, p):
     (2, 1000, 384, 384, 2),        # gate/up
     (4, 333, 200, 203, 3),         # ragged last block, rows not 16-byte aligned
 ])
-def test_batched_matches_one_call_per_sublayer(method, partition, gptq, n, R, C, ldw, seed):
+@pytest.mark.parametrize("factors", ["shared", "own"])
+def test_batched_matches_one_call_per_sublayer(method, partition, gptq, n, R, C, ldw, seed,
+                                               factors):
     from crb_amd import _lib, kernels
-    print(f"batched n={n} {R}x{C} ldw={ldw} {method} p{partition} gptq={gptq}", flush=True)
+    print(f"batched n={n} {R}x{C} ldw={ldw} {method} p{partition} gptq={gptq} {factors}",
+          flush=True)
     p = _lib.params(method, partition=partition, disable_gptq=not gptq)
-    U = _factor(C, seed)
+    if factors == "shared":
+        Us = [_factor(C, seed)] * n
+    else:                              # q/k/v with one factor, out with another
+        Us = [_factor(C, seed)] * (n - 1) + [_factor(C, seed + 100)]
     base = _weights(n, R, C, ldw, seed)
-    ref = _one_by_one(base, C, U, p)
+    ref = _one_by_one(base, C, Us, p)
     Wb = base.clone()
     Ws = [Wb[i][:, :C] for i in range(n)]
     Ls = [torch.zeros(R, device=DEV) for _ in range(n)]
-    masks, traces = kernels.fasterquant_blocks_batched(Ws, U, p, Ls, want_masks=True,
-                                                       want_traces=True)
+    masks, traces = kernels.fasterquant_blocks_batched(Ws, Us[0] if factors == "shared" else Us,
+                                                       p, Ls, want_masks=True, want_traces=True)
     torch.cuda.synchronize()
     for i in range(n):
         W, L, m, t = ref[i]
@@ -79,7 +85,7 @@ def test_batched_single_segment_and_argument_checks():
     R, C = 512, 256
     U = _factor(C, 5)
     base = _weights(1, R, C, C, 5)
-    ref = _one_by_one(base, C, U, p)
+    ref = _one_by_one(base, C, [U], p)
     W = base[0].clone()
     L = torch.zeros(R, device=DEV)
     masks, _ = kernels.fasterquant_blocks_batched([W], U, p, [L], want_masks=True)
@@ -90,6 +96,10 @@ def test_batched_single_segment_and_argument_checks():
         kernels.fasterquant_blocks_batched(five, U, p, [torch.zeros(R, device=DEV)] * 5)
     with pytest.raises(_lib.CrbqError):
         kernels.fasterquant_blocks_batched([base[0].clone(), base[0][:, :C - 8].clone()], U, p,
+                                           [torch.zeros(R, device=DEV)] * 2)
+    with pytest.raises(_lib.CrbqError):              # factors of two sizes
+        kernels.fasterquant_blocks_batched([base[0].clone(), base[0].clone()],
+                                           [U, _factor(C + 8, 6)], p,
                                            [torch.zeros(R, device=DEV)] * 2)
     lib = _lib.load()
     assert lib.crbq_fasterquant_batched_workspace_size(0, R, C, p) == 0
