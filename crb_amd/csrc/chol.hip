@@ -43,24 +43,44 @@ __global__ __launch_bounds__(256) void k_zero_dead(float* W, int64_t ldw, int R,
 
 // H_ii += factor * mean(diag H); retry mode: 1e-6 when that is 0.
 // dead (optional): first the dead columns, H_ii == 0, flagged and set to 1
-// (each thread handles the same diagonal entries in both passes, so the
-// mean sees the 1s).
-// info (optional): the factorization's failure flag, cleared.
+// (the mean sees the 1s).  info (optional): the factorization's failure
+// flag, cleared.  One workgroup; thread t handles the entries i = t + 1024 u
+// in ascending u, DG of them per round loaded together (each is a row
+// stride from the last, one cache line apart), few registers so the
+// workgroup finds room beside other kernels' waves.  The sum: per thread in
+// ascending i in fp64, then a fixed tree over the threads.
+constexpr int DG = 4;
 __global__ __launch_bounds__(1024) void k_damp(float* H, int64_t ldh, int C, float factor,
                                                int retry, float* out, uint8_t* dead,
                                                int* info) {
   __shared__ double red[1024];
   const int tid = threadIdx.x;
-  if (dead)
-    for (int i = tid; i < C; i += 1024) {
-      float* p = H + (int64_t)i * ldh + i;
-      const bool d = *p == 0.f;                 // bigptq.py:103-104
-      dead[i] = d;
-      if (d) *p = 1.f;
-    }
+  const int64_t step = ldh + 1;
   if (info && tid == 0) *info = 0;
   double s = 0.0;
-  for (int i = tid; i < C; i += 1024) s += (double)H[(int64_t)i * ldh + i];
+  for (int i0 = tid; i0 < C; i0 += 1024 * DG) {
+    float v[DG];
+#pragma unroll
+    for (int u = 0; u < DG; ++u) {
+      const int i = i0 + 1024 * u;
+      v[u] = i < C ? H[(int64_t)i * step] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < DG; ++u) {
+      const int i = i0 + 1024 * u;
+      if (i < C) {
+        if (dead) {
+          const bool d = v[u] == 0.f;           // bigptq.py:103-104
+          dead[i] = d;
+          if (d) {
+            v[u] = 1.f;
+            H[(int64_t)i * step] = 1.f;
+          }
+        }
+        s += (double)v[u];
+      }
+    }
+  }
   red[tid] = s;
   __syncthreads();
   for (int o = 512; o > 0; o >>= 1) {
@@ -70,9 +90,18 @@ __global__ __launch_bounds__(1024) void k_damp(float* H, int64_t ldh, int C, flo
   const float mean = (float)red[0] / (float)C;
   float v = factor * mean;
   if (retry && v == 0.f) v = 1e-6f;             // bigptq.py:120-121
-  for (int i = tid; i < C; i += 1024) {
-    float* p = H + (int64_t)i * ldh + i;
-    *p = *p + v;
+  for (int i0 = tid; i0 < C; i0 += 1024 * DG) {
+    float h[DG];
+#pragma unroll
+    for (int u = 0; u < DG; ++u) {
+      const int i = i0 + 1024 * u;
+      h[u] = i < C ? H[(int64_t)i * step] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < DG; ++u) {
+      const int i = i0 + 1024 * u;
+      if (i < C) H[(int64_t)i * step] = h[u] + v;
+    }
   }
   if (tid == 0 && out) *out = v;
 }

@@ -776,22 +776,78 @@ __global__ __launch_bounds__(SYRKD_THREADS) void k_syrk16k_pers(
 
 // S[i][j] += sum_s P[s][i][j] in split order, upper triangle.  Grid: x =
 // row, y = 1024-column chunk; 256 threads, 4 columns each.
+// Upper tile id of an nt x nt grid of FT x FT tiles, row by row from the
+// last (k_sum_splits, k_finalize).
+constexpr int FT = 64;
+__device__ __forceinline__ void upper_tile(int id, int nt, int& ti, int& tj) {
+  const int k = nt * (nt + 1) / 2 - 1 - id;          // lower-triangle index (r >= b)
+  int r = (int)((sqrtf(8.f * (float)k + 1.f) - 1.f) * 0.5f);
+  while ((r + 1) * (r + 2) / 2 <= k) ++r;
+  while (r * (r + 1) / 2 > k) --r;
+  const int b = k - r * (r + 1) / 2;
+  ti = nt - 1 - r;
+  tj = nt - 1 - b;
+}
+
+// S[i][j] += P[0][i][j] + P[1][i][j] + ... (in that order) for j >= i,
+// over the 64 x 64 tiles of the upper triangle (the same sums as the
+// SYRK's split partials need), 16-byte accesses where S's rows allow.
 __global__ __launch_bounds__(256) void k_sum_splits(const float* __restrict__ P, int nsplit,
-                                                    int C, float* S, int64_t lds) {
-  const int i = blockIdx.x;
-  const int j0 = blockIdx.y * 1024;
-  if (j0 + 1023 < i) return;
-  const float* pi = P + (int64_t)i * lds;
-  float* si = S + (int64_t)i * lds;
+                                                    int C, float* S, int64_t lds, int nt,
+                                                    int vec) {
+  int ti, tj;
+  upper_tile(blockIdx.x, nt, ti, tj);
+  const int r0 = ti * FT, c0 = tj * FT;
   const size_t pstride = (size_t)C * lds;
+  const int tid = threadIdx.x;
+  if (vec && r0 + FT <= C && c0 + FT <= C) {
+    // thread: rows tid / 16 + 16 k, columns 4 (tid % 16) .. + 3
+    const int rr = tid >> 4, cc = (tid & 15) * 4;
+    float4 v[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int j = j0 + k * 256 + threadIdx.x;
-    if (j < i || j >= C) continue;
-    float v = si[j];
-    for (int sp = 0; sp < nsplit; ++sp) v = v + pi[sp * pstride + j];
-    si[j] = v;
+    for (int k = 0; k < 4; ++k) v[k] = *(const float4*)(S + (int64_t)(r0 + rr + 16 * k) * lds + c0 + cc);
+    for (int sp = 0; sp < nsplit; ++sp) {
+      float4 q[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        q[k] = *(const float4*)(P + sp * pstride + (int64_t)(r0 + rr + 16 * k) * lds + c0 + cc);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[k].x = v[k].x + q[k].x; v[k].y = v[k].y + q[k].y;
+        v[k].z = v[k].z + q[k].z; v[k].w = v[k].w + q[k].w;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = r0 + rr + 16 * k, j = c0 + cc;
+      float* d = S + (int64_t)i * lds + j;
+      if (j >= i) {
+        *(float4*)d = v[k];
+      } else if (j + 3 >= i) {                  // the float4 straddles the diagonal
+        const float e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (j + c >= i) d[c] = e[c];
+      }
+    }
+    return;
   }
+  const int tx = tid & 63, ty = tid >> 6;
+  for (int k = 0; k < FT; k += 4) {
+    const int i = r0 + ty + k, j = c0 + tx;
+    if (i >= C || j >= C || j < i) continue;
+    float v = S[(int64_t)i * lds + j];
+    for (int sp = 0; sp < nsplit; ++sp) v = v + P[sp * pstride + (int64_t)i * lds + j];
+    S[(int64_t)i * lds + j] = v;
+  }
+}
+
+static void sum_splits(const float* P, int nsplit, int64_t C, float* S, int64_t lds,
+                       hipStream_t s) {
+  const int nt = (int)((C + FT - 1) / FT);
+  const int vec = (lds & 3) == 0 && ((((uintptr_t)S) | ((uintptr_t)P)) & 15) == 0;
+  k_sum_splits<<<(unsigned)((int64_t)nt * (nt + 1) / 2), 256, 0, s>>>(P, nsplit, (int)C, S, lds,
+                                                                      nt, vec);
 }
 
 // fp32 inputs: LDS in natural token-major layout, A[i][k] = X[k][i].
@@ -860,16 +916,6 @@ __global__ __launch_bounds__(256) void k_syrk32(const float* __restrict__ X, int
 // nt (nt + 1) / 2 upper tiles, row by row from the last.  H may alias S: a
 // workgroup reads only its own upper tile, all of it before any store, and
 // lower tiles are never read.
-constexpr int FT = 64;
-__device__ __forceinline__ void upper_tile(int id, int nt, int& ti, int& tj) {
-  const int k = nt * (nt + 1) / 2 - 1 - id;          // lower-triangle index (r >= b)
-  int r = (int)((sqrtf(8.f * (float)k + 1.f) - 1.f) * 0.5f);
-  while ((r + 1) * (r + 2) / 2 <= k) ++r;
-  while (r * (r + 1) / 2 > k) --r;
-  const int b = k - r * (r + 1) / 2;
-  ti = nt - 1 - r;
-  tj = nt - 1 - b;
-}
 
 __global__ __launch_bounds__(256) void k_finalize(const float* S, int64_t lds, int C,
                                                   float scale, float* H, int64_t ldh, int nt,
@@ -1108,8 +1154,7 @@ static int syrk_xt(const uint16_t* X, int64_t ld, int64_t ntok, bool tmaj, int64
   CRBQ_LAUNCH_CHECK();
   tm.stop(s);
   if (P) {
-    k_sum_splits<<<dim3((unsigned)C, (unsigned)((C + 1023) / 1024)), 256, 0, s>>>(P, ns - 1,
-                                                                                 (int)C, S, lds);
+    sum_splits(P, ns - 1, C, S, lds, s);
     CRBQ_LAUNCH_CHECK();
   }
   return CRBQ_OK;
@@ -1206,8 +1251,7 @@ extern "C" int crbq_hessian_accum(const void* X, int dtype, int64_t ntok, int64_
   CRBQ_LAUNCH_CHECK();
   tm.stop(s);
   if (P) {
-    crbq::k_sum_splits<<<dim3((unsigned)C, (unsigned)((C + 1023) / 1024)), 256, 0, s>>>(
-        P, ns - 1, (int)C, S, lds);
+    crbq::sum_splits(P, ns - 1, C, S, lds, s);
     CRBQ_LAUNCH_CHECK();
   }
   return CRBQ_OK;
