@@ -221,9 +221,11 @@ def _ev_ms(fn, reps):
     return a.elapsed_time(b) / reps
 
 
-def _graph_ms(fn, reps):
-    """Average ms of one fn() launch: reps calls captured in a HIP graph,
-    replayed between two events recorded on the replay stream."""
+def _graph_ms(fn, reps, warm=4, rounds=5):
+    """Average ms of one fn() launch: reps calls captured in a HIP graph;
+    `warm` untimed replays (the kernel's own steady state, not the clock
+    the previous measurement left), then the median of `rounds` replays,
+    each between two events recorded on the replay stream."""
     fn()
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
@@ -233,26 +235,68 @@ def _graph_ms(fn, reps):
             for _ in range(reps):
                 fn()
     torch.cuda.synchronize()
-    gr.replay()
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(s):
-        a.record(s)
+    for _ in range(warm):
         gr.replay()
-        b.record(s)
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / reps
+    ms = []
+    for _ in range(rounds):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            a.record(s)
+            gr.replay()
+            b.record(s)
+        torch.cuda.synchronize()
+        ms.append(a.elapsed_time(b) / reps)
+    return sorted(ms)[len(ms) // 2]
 
 
-def kernel_rooflines(dev, R=4096, C=16384, reps=20):
+def binarize_rates(dev, reps=20, methods=(("crb", 2), ("crb", 1), ("braq", 2), ("crbog", 2)),
+                   sustained=True):
+    """k_binarize_g over 524288 rows x 128 columns per launch (604 MB: the
+    launch gaps amortized), 9 bytes per element (fp32 in, mask byte, fp32
+    out) against HBM: launches of crbq_binarize through the C ABI (uint8
+    mask prepared once) captured in a HIP graph and replayed between two
+    events on the replay stream, so the figure is the kernel's and not the
+    Python wrapper's.  For crb order 2 also `sustained`: 40 times as many
+    launches as one continuous stream (about 0.1 s)."""
+    from crb_amd import _lib
+    g = torch.Generator(device=dev)
+    g.manual_seed(12)
+    nb = 524288
+    x = torch.randn(nb, 128, device=dev, generator=g) * 0.02
+    m = (torch.rand(nb, 128, device=dev, generator=g) < 0.9).to(torch.uint8)
+    ob = torch.empty_like(x)
+    lib = _lib.ready(dev)
+    out = {}
+    for method, order in methods:
+        def launch(method=method, order=order):
+            st = torch.cuda.current_stream().cuda_stream
+            _lib.check(lib.crbq_binarize(x.data_ptr(), nb, 128, 128, m.data_ptr(), 128, order,
+                                         _lib.METHODS[method], 1e-5, 0.1, 1, ob.data_ptr(),
+                                         128, st), "crbq_binarize")
+        ms = _graph_ms(launch, reps)
+        by = nb * 128 * 9
+        rec = {
+            "kernel": "k_binarize_g (8 lanes x 16 columns per row)", "shape": [nb, 128],
+            "ms": round(ms, 5), "achieved": round(by / ms / 1e6, 1), "peak": PEAK_HBM / 1e9,
+            "unit": "GB/s", "frac": round(by / ms / 1e6 / (PEAK_HBM / 1e9), 3)}
+        if sustained and method == "crb" and order == 2:
+            ms_s = _graph_ms(launch, reps * 40, warm=1, rounds=1)
+            rec["sustained"] = {"ms": round(ms_s, 5), "launches": reps * 40,
+                                "frac": round(by / ms_s / 1e6 / (PEAK_HBM / 1e9), 3)}
+        out[f"{method}_order{order}"] = rec
+    del x, m, ob
+    return out
+
+
+def kernel_rooflines(dev, R=4096, C=16384, reps=20, binarize=None):
     """The block loop's kernels launched alone at the fc2 sublayer's shapes
     (R x C = 4096 x 16384, 128-column blocks, 1024-column super-blocks),
     each against its roofline:
     * trailing update W[:, sb1:] -= Err @ U[sb0:sb1, sb1:] (k_sgemm, fp32
       MFMA), K = 1024, N = 8192 remaining columns: 2 M N K flop;
-    * binarization (k_binarize_g; crb order 2 and 1, braq and crbog order 2)
-      over 524288 rows x 128 columns in one launch, 9 bytes per element (fp32
-      in, mask byte, fp32 out) against HBM;
+    * binarization (binarize_rates; given when measured earlier, before the
+      layer steps, and then crb order 2 measured again here);
     * one block step (salient/split search + binarize + in-block error
       feedback, crbq_fasterquant on a 4096 x 128 block): its algorithmic
       bytes (W block in, U block in, Q, Err and masks out) against HBM;
@@ -274,28 +318,14 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
         "kernel": "k_sgemm<128> (fp32 MFMA)", "shape": [R, N, K], "ms": round(ms, 4),
         "achieved": round(fl / ms / 1e9, 1), "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
         "frac": round(fl / ms / 1e9 / (PEAK_F32 / 1e12), 3)}
-    # binarization, streaming shape: launches of crbq_binarize through the C
-    # ABI (uint8 mask prepared once), captured in a HIP graph and replayed
-    # between two events on the replay stream, so the figure is the kernel's
-    # and not the Python wrapper's
-    nb = 524288                 # 604 MB per launch: the launch gaps amortized
-    x = torch.randn(nb, 128, device=dev, generator=g) * 0.02
-    m = (torch.rand(nb, 128, device=dev, generator=g) < 0.9).to(torch.uint8)
-    ob = torch.empty_like(x)
-    lib = _lib.ready(dev)
-    out["binarize"] = {}
-    for method, order in (("crb", 2), ("crb", 1), ("braq", 2), ("crbog", 2)):
-        def launch(method=method, order=order):
-            st = torch.cuda.current_stream().cuda_stream
-            _lib.check(lib.crbq_binarize(x.data_ptr(), nb, 128, 128, m.data_ptr(), 128, order,
-                                         _lib.METHODS[method], 1e-5, 0.1, 1, ob.data_ptr(),
-                                         128, st), "crbq_binarize")
-        ms = _graph_ms(launch, reps)
-        by = nb * 128 * 9
-        out["binarize"][f"{method}_order{order}"] = {
-            "kernel": "k_binarize_g (8 lanes x 16 columns per row)", "shape": [nb, 128],
-            "ms": round(ms, 5), "achieved": round(by / ms / 1e6, 1), "peak": PEAK_HBM / 1e9,
-            "unit": "GB/s", "frac": round(by / ms / 1e6 / (PEAK_HBM / 1e9), 3)}
+    if binarize is None:
+        out["binarize"] = binarize_rates(dev, reps)
+    else:
+        # measured before the layer steps; the headline one again now, on a
+        # chip that has just run at its power limit for seconds
+        out["binarize"] = binarize
+        out["binarize_after_layer_steps"] = binarize_rates(dev, reps, (("crb", 2),),
+                                                           sustained=False)
     # one block step and the whole loop
     p = _lib.params("crb")
     U = torch.triu(torch.randn(C, C, device=dev, generator=g) * 1e-3)
@@ -317,7 +347,7 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20):
         "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(by / ms / 1e6 / (PEAK_HBM / 1e9), 4),
         "note": "2 MB working set per block, resident in L2/MALL; bound by the search's "
                 "dependent passes, not by HBM"}
-    del Ubig, E, x, m, ob
+    del Ubig, E
     W = Wbig.clone()
 
     def loop():
@@ -663,6 +693,12 @@ def main():
     torch.cuda.set_device(dev)
     from crb_amd import _lib
     _lib.ready(dev)
+    bin_rates = None
+    if not args.no_kernels:
+        # the standalone binarizer first, on a chip that has not yet run the
+        # layer at its power limit (kernel_rooflines measures it again after)
+        bin_rates = binarize_rates(dev)
+        print(f"[bench] binarizer: {bin_rates}", file=sys.stderr, flush=True)
     print(f"[bench] building OPT-6.7B layer inputs ({args.tokens} tokens)", file=sys.stderr,
           flush=True)
     subs, W0 = make_layer(dev)
@@ -742,7 +778,7 @@ def main():
         stream["bytes_per_clk_per_cu"] = round(sbytes / t_launch / 256 / (clk * 1e9), 1)
     out["roofline"]["operand_stream_l2_to_lds"] = stream
     if not args.no_kernels:
-        out["kernels"] = kernel_rooflines(dev)
+        out["kernels"] = kernel_rooflines(dev, binarize=bin_rates)
         print(f"[bench] kernels: {out['kernels']}", file=sys.stderr, flush=True)
     if args.stack_layers > 0:
         del X
