@@ -1544,6 +1544,14 @@ static int fasterquant_impl(int nseg, float* const* Ws, int64_t R, int64_t C, in
   if (R <= 0 || C <= 0 || ldw < C || ldu < C) return CRBQ_ERR_ARG;
   for (int i = 0; i < nseg; ++i)
     if (!Ws[i] || !Us[i] || !losses[i]) return CRBQ_ERR_ARG;
+  // one launch updates every segment's outputs: two segments given the
+  // same buffer would race (factors may be shared: they are only read)
+  for (int i = 0; i < nseg; ++i)
+    for (int j = 0; j < i; ++j)
+      if (Ws[i] == Ws[j] || losses[i] == losses[j] ||
+          (masks && masks[i] && masks[i] == masks[j]) ||
+          (traces && traces[i] && traces[i] == traces[j]))
+        return CRBQ_ERR_ARG;
   const bool any_masks = masks && masks[0];
   for (int i = 0; i < nseg; ++i)
     if (masks && ((masks[i] != nullptr) != any_masks)) return CRBQ_ERR_ARG;

@@ -205,8 +205,10 @@ int crbq_fasterquant(float* W, int64_t R, int64_t C, int64_t ldw,
  * the per-sublayer loop of run.py:286-305 (BRAGPTQ.fasterquant,
  * bigptq.py:56-291).  W, U, losses, masks and traces are HOST arrays of
  * nseg device pointers (masks and traces may be NULL, or arrays whose
- * entries are all NULL); every sublayer's results are bit for bit those of
- * its own crbq_fasterquant call with the same params.  The block loop runs
+ * entries are all NULL); the sublayers' weights, losses, masks and traces
+ * must not overlap (the same pointer twice is rejected with CRBQ_ERR_ARG).
+ * Every sublayer's results are bit for bit those of its own
+ * crbq_fasterquant call with the same params.  The block loop runs
  * once, each search, quantize and update launch covering all nseg
  * sublayers.  Workspace: crbq_fasterquant_batched_workspace_size. */
 size_t crbq_fasterquant_batched_workspace_size(int32_t nseg, int64_t R, int64_t C,

@@ -101,6 +101,13 @@ def test_batched_single_segment_and_argument_checks():
         kernels.fasterquant_blocks_batched([base[0].clone(), base[0].clone()],
                                            [U, _factor(C + 8, 6)], p,
                                            [torch.zeros(R, device=DEV)] * 2)
+    Wd = base[0].clone()                      # the same weight twice: rejected
+    with pytest.raises(_lib.CrbqError):
+        kernels.fasterquant_blocks_batched([Wd, Wd], U, p,
+                                           [torch.zeros(R, device=DEV) for _ in range(2)])
+    Ld = torch.zeros(R, device=DEV)           # the same loss vector twice: rejected
+    with pytest.raises(_lib.CrbqError):
+        kernels.fasterquant_blocks_batched([base[0].clone(), base[0].clone()], U, p, [Ld, Ld])
     lib = _lib.load()
     assert lib.crbq_fasterquant_batched_workspace_size(0, R, C, p) == 0
     assert lib.crbq_fasterquant_batched_workspace_size(5, R, C, p) == 0
