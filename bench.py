@@ -301,7 +301,8 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20, binarize=None):
       feedback, crbq_fasterquant on a 4096 x 128 block): its algorithmic
       bytes (W block in, U block in, Q, Err and masks out) against HBM;
     * the whole fc2 block loop alone (128 blocks, with trailing updates),
-      and fc1's (16384 x 4096, 32 blocks)."""
+      and fc1's (16384 x 4096, 32 blocks);
+    * q/k/v/out_proj's four 4096 x 4096 loops one by one and batched."""
     from crb_amd import _lib, kernels
     g = torch.Generator(device=dev)
     g.manual_seed(11)
@@ -371,6 +372,34 @@ def kernel_rooflines(dev, R=4096, C=16384, reps=20, binarize=None):
 
     out["block_loop_fc1_alone_ms"] = round(_ev_ms(loop1, 2), 3)
     del W1, U1, Wq
+    # q/k/v/out_proj's shape (four 4096 x 4096 sublayers, the first three
+    # sharing one factor, out_proj with its own): four block loops one after
+    # another against one batched loop (crbq_fasterquant_batched), as the
+    # layer driver runs them
+    C4 = C // 4
+    W4 = [torch.randn(R, C4, device=dev, generator=g) * 0.02 for _ in range(4)]
+    U4 = []
+    for _ in range(2):
+        u = torch.triu(torch.randn(C4, C4, device=dev, generator=g) * 1e-3)
+        u.diagonal().add_(1.0)
+        U4.append(u)
+    U4 = [U4[0], U4[0], U4[0], U4[1]]
+    L4 = [torch.zeros(R, device=dev) for _ in range(4)]
+    Wc = [w.clone() for w in W4]
+
+    def loops_one_by_one():
+        for w, w0, u, l in zip(Wc, W4, U4, L4):
+            w.copy_(w0)
+            kernels.fasterquant_blocks(w, u, p, l, want_masks=False)
+
+    def loop_batched():
+        for w, w0 in zip(Wc, W4):
+            w.copy_(w0)
+        kernels.fasterquant_blocks_batched(Wc, U4, p, L4)
+
+    out["block_loops_qkvo_alone_ms"] = {"one_by_one": round(_ev_ms(loops_one_by_one, 2), 3),
+                                        "batched": round(_ev_ms(loop_batched, 2), 3)}
+    del W4, U4, L4, Wc
     torch.cuda.empty_cache()
     # inverse factor alone (crbq_hinv_upper: damping, Cholesky-inverse of the
     # index-reversed H, U) on a well-conditioned H of the fc2 input's size and
