@@ -111,3 +111,31 @@ def test_batched_single_segment_and_argument_checks():
     lib = _lib.load()
     assert lib.crbq_fasterquant_batched_workspace_size(0, R, C, p) == 0
     assert lib.crbq_fasterquant_batched_workspace_size(5, R, C, p) == 0
+
+
+@pytest.mark.parametrize("name,n,R,C,nfac,method,iters", [
+    ("opt-6.7b q/k/v/out", 4, 4096, 4096, 2, "crb", 1),
+    ("llama-3-8b q/o", 2, 4096, 4096, 2, "crb", 5),
+    ("llama-3-8b k/v", 2, 1024, 4096, 1, "crbog", 1),
+    ("llama-3-8b gate/up", 2, 14336, 4096, 1, "crb", 5),
+])
+def test_batched_full_size_layers(name, n, R, C, nfac, method, iters):
+    """The sublayer groups the layer driver batches, at full model shapes:
+    bitwise the weights and losses of one call per sublayer."""
+    from crb_amd import _lib, kernels
+    print(f"batched full size: {name} ({n} x {R} x {C}, {nfac} factors, {method})", flush=True)
+    p = _lib.params(method, refine_iters=iters)
+    facs = [_factor(C, 40 + f) for f in range(nfac)]
+    Us = [facs[0]] * (n - nfac + 1) + facs[1:]
+    base = _weights(n, R, C, C, 41)
+    Wb = base.clone()
+    Ws = [Wb[i] for i in range(n)]
+    Ls = [torch.zeros(R, device=DEV) for _ in range(n)]
+    kernels.fasterquant_blocks_batched(Ws, Us, p, Ls)
+    for i in range(n):
+        W = base[i].clone()
+        L = torch.zeros(R, device=DEV)
+        kernels.fasterquant_blocks(W, Us[i], p, L)
+        assert torch.equal(Ws[i], W), i
+        assert torch.equal(Ls[i], L), i
+        del W
