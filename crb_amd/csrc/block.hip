@@ -42,7 +42,7 @@ constexpr int NT = 2 * NQ;   // order statistics needed (lo, hi per percentile)
 constexpr int NCMAX = 128;   // widest block
 constexpr int UPMAX = 64;    // largest supported up_lim
 #ifndef CRBQ_Q_RPW
-#define CRBQ_Q_RPW 16
+#define CRBQ_Q_RPW 32
 #endif
 constexpr int Q_RPW = CRBQ_Q_RPW;   // rows per workgroup in the quantile passes
 #ifndef CRBQ_CS_MAXWG
