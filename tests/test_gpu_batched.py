@@ -139,3 +139,39 @@ def test_batched_full_size_layers(name, n, R, C, nfac, method, iters):
         assert torch.equal(Ws[i], W), i
         assert torch.equal(Ls[i], L), i
         del W
+
+
+def test_batched_magnitude_metric_and_partial_traces():
+    """Magnitude salient metric (utils/structure.py:11-12) through the
+    batched loop, with block traces requested for some sublayers only (a
+    NULL entry in the host array): bitwise the single-call results, and the
+    traced sublayers' traces equal to their single-call traces."""
+    import ctypes
+    from crb_amd import _lib, kernels
+    print("batched magnitude metric, partial traces", flush=True)
+    p = _lib.params("crb", metric="magnitude")
+    n, R, C = 3, 512, 384
+    Us = [_factor(C, 51), _factor(C, 52), _factor(C, 51)]
+    base = _weights(n, R, C, C, 53)
+    ref = _one_by_one(base, C, Us, p)
+    lib = _lib.ready(torch.device(DEV))
+    nblk = (C + 127) // 128
+    Ws = [base[i].clone() for i in range(n)]
+    Ls = [torch.zeros(R, device=DEV) for _ in range(n)]
+    trs = [torch.zeros(nblk * _lib.TRACE_BYTES, dtype=torch.uint8, device=DEV), None,
+           torch.zeros(nblk * _lib.TRACE_BYTES, dtype=torch.uint8, device=DEV)]
+    ws = torch.empty(lib.crbq_fasterquant_batched_workspace_size(n, R, C, ctypes.byref(p)),
+                     dtype=torch.uint8, device=DEV)
+    arr = ctypes.c_void_p * n
+    _lib.check(lib.crbq_fasterquant_batched(
+        n, arr(*[w.data_ptr() for w in Ws]), R, C, C, arr(*[u.data_ptr() for u in Us]), C,
+        ctypes.byref(p), arr(*[l.data_ptr() for l in Ls]), None, 0,
+        arr(*[t.data_ptr() if t is not None else None for t in trs]), ws.data_ptr(), ws.numel(),
+        torch.cuda.current_stream().cuda_stream), "crbq_fasterquant_batched")
+    torch.cuda.synchronize()
+    for i in range(n):
+        W, L, _, t = ref[i]
+        assert torch.equal(Ws[i], W), i
+        assert torch.equal(Ls[i], L), i
+        if trs[i] is not None:
+            assert kernels.decode_traces(trs[i], nblk) == t, i
