@@ -237,17 +237,45 @@ constexpr int GV_MAXVEC = 16;
 
 // Two weights (elements 2p, 2p+1 of a lane's 8) from the block's table L:
 // v_perm_b32 picks the 16-bit entries of codes (c_a, c_b) among the four
-// non-salient entries and among the four salient ones; selb (from the two
-// salient bits) takes each half from the salient or the non-salient pick.
-__device__ __forceinline__ uint32_t decode_pair(uint32_t cw, int p, uint4 L, uint32_t sb) {
+// non-salient entries and among the four salient ones; selb (sal_sel of the
+// pair's two salient bits) takes each half from the salient or the
+// non-salient pick.
+__device__ __forceinline__ uint32_t decode_pair(uint32_t cw, int p, uint4 L, uint32_t selb) {
   const uint32_t n = (cw >> (4 * p)) & 0xfu;
   const uint32_t t = (n & 3u) | ((n & 0xcu) << 14);
   const uint32_t sel = t * 0x202u + 0x01000100u;
   const uint32_t wn = __builtin_amdgcn_perm(L.y, L.x, sel);
   const uint32_t ws = __builtin_amdgcn_perm(L.w, L.z, sel);
-  const uint32_t s2 = (sb >> (2 * p)) & 3u;
-  const uint32_t selb = 0x03020100u + (s2 & 1u) * 0x0404u + (s2 >> 1) * 0x04040000u;
   return __builtin_amdgcn_perm(ws, wn, selb);
+}
+
+// The final selector of pair q (columns 2q, 2q + 1) of a lane's 32 columns
+// from their salient bits sb: bytes 0-1 from the salient pick (perm source
+// bytes 4-7) if column 2q is salient, bytes 2-3 likewise for 2q + 1.
+__device__ __forceinline__ uint32_t sal_sel(uint32_t sb, int q) {
+  const uint32_t s2 = (sb >> (2 * q)) & 3u;
+  return 0x03020100u + (s2 & 1u) * 0x0404u + (s2 >> 1) * 0x04040000u;
+}
+
+// The 16 lanes of a DPP row (lanes 16 i .. 16 i + 15) decode the same 32
+// columns (one row of W each), so their selectors are the same: lane r of
+// the row builds pair r's (sal_sel(sb, r)) and the others read it with a
+// row broadcast (DPP row_newbcast), one move instead of the bit arithmetic.
+template <int Q>
+__device__ __forceinline__ uint32_t row_bcast_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + Q, 0xf, 0xf, true);
+}
+__device__ __forceinline__ uint32_t pair_sel(uint32_t mine, int q) {   // q constant when unrolled
+  switch (q) {
+    case 0: return row_bcast_u32<0>(mine);   case 1: return row_bcast_u32<1>(mine);
+    case 2: return row_bcast_u32<2>(mine);   case 3: return row_bcast_u32<3>(mine);
+    case 4: return row_bcast_u32<4>(mine);   case 5: return row_bcast_u32<5>(mine);
+    case 6: return row_bcast_u32<6>(mine);   case 7: return row_bcast_u32<7>(mine);
+    case 8: return row_bcast_u32<8>(mine);   case 9: return row_bcast_u32<9>(mine);
+    case 10: return row_bcast_u32<10>(mine); case 11: return row_bcast_u32<11>(mine);
+    case 12: return row_bcast_u32<12>(mine); case 13: return row_bcast_u32<13>(mine);
+    case 14: return row_bcast_u32<14>(mine); default: return row_bcast_u32<15>(mine);
+  }
 }
 
 template <typename T8>
@@ -300,15 +328,15 @@ __device__ __forceinline__ void gv_block(const uint8_t* crow, const uint4* lrow,
                          h[6] | (h[7] << 16));
     }
   }
+  const uint32_t mine = sal_sel(sb, (int)(threadIdx.x & 15));
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const uint32_t cws = (k < 2 ? cw.x : cw.y) >> (16 * (k & 1));
-    const uint32_t sbs = sb >> (8 * k);
     uint4 a;
-    a.x = decode_pair(cws, 0, L, sbs);
-    a.y = decode_pair(cws, 1, L, sbs);
-    a.z = decode_pair(cws, 2, L, sbs);
-    a.w = decode_pair(cws, 3, L, sbs);
+    a.x = decode_pair(cws, 0, L, pair_sel(mine, 4 * k));
+    a.y = decode_pair(cws, 1, L, pair_sel(mine, 4 * k + 1));
+    a.z = decode_pair(cws, 2, L, pair_sel(mine, 4 * k + 2));
+    a.w = decode_pair(cws, 3, L, pair_sel(mine, 4 * k + 3));
     acc = mfma_gv<T8>(__builtin_bit_cast(T8, a), __builtin_bit_cast(T8, xs[k]), acc);
   }
 }
@@ -420,15 +448,15 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_packed(
     const uint32_t sb = *(const uint32_t*)(sal + (int64_t)b * 16 + kq * 4);
     const uint4 L = row_ok ? lrow[b] : make_uint4(0u, 0u, 0u, 0u);
     T8 a[4];
+    const uint32_t mine = sal_sel(sb, lane & 15);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const uint32_t cws = (k < 2 ? cw.x : cw.y) >> (16 * (k & 1));
-      const uint32_t sbs = sb >> (8 * k);
       uint4 q;
-      q.x = decode_pair(cws, 0, L, sbs);
-      q.y = decode_pair(cws, 1, L, sbs);
-      q.z = decode_pair(cws, 2, L, sbs);
-      q.w = decode_pair(cws, 3, L, sbs);
+      q.x = decode_pair(cws, 0, L, pair_sel(mine, 4 * k));
+      q.y = decode_pair(cws, 1, L, pair_sel(mine, 4 * k + 1));
+      q.z = decode_pair(cws, 2, L, pair_sel(mine, 4 * k + 2));
+      q.w = decode_pair(cws, 3, L, pair_sel(mine, 4 * k + 3));
       a[k] = __builtin_bit_cast(T8, q);
     }
 #pragma unroll
