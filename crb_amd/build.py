@@ -57,6 +57,53 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+def asan_runtime() -> str | None:
+    """The ROCm toolchain's shared AddressSanitizer runtime (to preload into
+    a process that loads an ASan build), or None."""
+    base = os.path.join(os.path.dirname(os.path.dirname(os.path.realpath(HIPCC))), "llvm", "lib",
+                        "clang")
+    if not os.path.isdir(base):
+        base = "/opt/rocm/llvm/lib/clang"
+    if not os.path.isdir(base):
+        return None
+    for ver in sorted(os.listdir(base), reverse=True):
+        p = os.path.join(base, ver, "lib", "linux", "libclang_rt.asan-x86_64.so")
+        if os.path.exists(p):
+            return p
+    return None
+
+
+def build_host_asan(out_dir: str) -> str:
+    """The same library with its host code built with AddressSanitizer
+    (-Xarch_host: the gfx950 code is unchanged), for checks of the C ABI's
+    host side (argument validation, workspace carving, pointer arrays).  It
+    links the shared ASan runtime, which the loading process must preload
+    (asan_runtime()).  Not the product library: written to out_dir."""
+    objdir = os.path.join(out_dir, "obj")
+    os.makedirs(objdir, exist_ok=True)
+    flags = [f for f in FLAGS if f != "-O3"] + [
+        "-O1", "-g", "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-shared-libasan",
+        "-Xarch_host", "-fno-omit-frame-pointer"]
+
+    def one(src: str) -> str:
+        obj = os.path.join(objdir, src.replace(".hip", ".o"))
+        r = subprocess.run([HIPCC, *flags, "-c", os.path.join(CSRC, src), "-o", obj],
+                           capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
+        objs = list(ex.map(one, SOURCES))
+    lib = os.path.join(out_dir, "libcrbq_asan.so")
+    link = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC"]
+    link += ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-shared-libasan"]
+    r = subprocess.run([*link, *objs, "-o", lib], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    return lib
+
+
 if __name__ == "__main__":
     build(verbose=True)
     sys.exit(0)
