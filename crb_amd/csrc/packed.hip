@@ -235,14 +235,22 @@ __global__ __launch_bounds__(256) void k_apply_ex(const int64_t* __restrict__ ex
 
 constexpr int GV_MAXVEC = 16;
 
+// The codes of pair p (elements 2p, 2p+1 of a lane's 8) are bits 4p..4p+1
+// and 4p+2..4p+3 of the 16-bit code word cw.  code_spread adds a copy of cw
+// 14 bits higher, so that pair p's two codes sit at bits 4p..4p+1 and
+// 4p+16..4p+17 for every p in 0..3, and one shift and one mask take them to
+// bits 0-1 and 16-17 (bits 16-31 of the argument are dropped).
+__device__ __forceinline__ uint32_t code_spread(uint32_t cw) {
+  return (cw & 0xffffu) | (cw << 14);
+}
+
 // Two weights (elements 2p, 2p+1 of a lane's 8) from the block's table L:
 // v_perm_b32 picks the 16-bit entries of codes (c_a, c_b) among the four
 // non-salient entries and among the four salient ones; selb (sal_sel of the
 // pair's two salient bits) takes each half from the salient or the
-// non-salient pick.
-__device__ __forceinline__ uint32_t decode_pair(uint32_t cw, int p, uint4 L, uint32_t selb) {
-  const uint32_t n = (cw >> (4 * p)) & 0xfu;
-  const uint32_t t = (n & 3u) | ((n & 0xcu) << 14);
+// non-salient pick.  d is code_spread of the code word.
+__device__ __forceinline__ uint32_t decode_pair(uint32_t d, int p, uint4 L, uint32_t selb) {
+  const uint32_t t = (d >> (4 * p)) & 0x00030003u;     // c_a | c_b << 16
   const uint32_t sel = t * 0x202u + 0x01000100u;
   const uint32_t wn = __builtin_amdgcn_perm(L.y, L.x, sel);
   const uint32_t ws = __builtin_amdgcn_perm(L.w, L.z, sel);
@@ -331,7 +339,7 @@ __device__ __forceinline__ void gv_block(const uint8_t* crow, const uint4* lrow,
   const uint32_t mine = sal_sel(sb, (int)(threadIdx.x & 15));
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const uint32_t cws = (k < 2 ? cw.x : cw.y) >> (16 * (k & 1));
+    const uint32_t cws = code_spread((k < 2 ? cw.x : cw.y) >> (16 * (k & 1)));
     uint4 a;
     a.x = decode_pair(cws, 0, L, pair_sel(mine, 4 * k));
     a.y = decode_pair(cws, 1, L, pair_sel(mine, 4 * k + 1));
@@ -387,8 +395,8 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_packed(
 // 8-column MFMA slices) and multiplies them with every 16-token group of
 // the X tile, which the whole workgroup stages in LDS (rows padded to 136
 // halves so a 16-lane group's 16-byte reads of 16 tokens fall on disjoint
-// banks).  The X tile of the next block is loaded into registers while the
-// current one is used.  When row and token tiles alone would leave CUs idle
+// banks).  The X tile, codes, salient bits and table of the next block are
+// loaded into registers while the current one is used.  When row and token tiles alone would leave CUs idle
 // the block range is split over gridDim.z workgroups, each writing an fp32
 // partial [T][R] slice that k_gemm_packed_sum adds in split order.
 constexpr int GM_WAVES = 8;
@@ -436,22 +444,40 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_packed(
   f4_t acc[GM_TT / 16];
 #pragma unroll
   for (int g = 0; g < GM_TT / 16; ++g) acc[g] = f4_t{0.f, 0.f, 0.f, 0.f};
+  // A block's codes, salient bits and table are loaded with its X tile, one
+  // block ahead, so that the decode never waits on them.  Rows past R read
+  // row 0 (crow, lrow): an MFMA output row depends only on its own weight
+  // row, and those rows are not stored.
   uint4 u[XPT];
-  if (b_beg < b_end) load_x(b_beg, u);
+  uint2 cwn = make_uint2(0u, 0u);
+  uint32_t sbn = 0u;
+  uint4 Ln = make_uint4(0u, 0u, 0u, 0u);
+  auto load_codes = [&](int b) {
+    cwn = *(const uint2*)(crow + b * 32 + kq * 8);
+    sbn = *(const uint32_t*)(sal + (int64_t)b * 16 + kq * 4);
+    Ln = lrow[b];
+  };
+  if (b_beg < b_end) {
+    load_codes(b_beg);
+    load_x(b_beg, u);
+  }
   for (int b = b_beg; b < b_end; ++b) {
     const int buf = (b - b_beg) & 1;
 #pragma unroll
     for (int k = 0; k < XPT; ++k) *(uint4*)&Xs[buf][xt][xc + 8 * k] = u[k];
     __syncthreads();
-    if (b + 1 < b_end) load_x(b + 1, u);
-    const uint2 cw = row_ok ? *(const uint2*)(crow + b * 32 + kq * 8) : make_uint2(0u, 0u);
-    const uint32_t sb = *(const uint32_t*)(sal + (int64_t)b * 16 + kq * 4);
-    const uint4 L = row_ok ? lrow[b] : make_uint4(0u, 0u, 0u, 0u);
+    const uint2 cw = cwn;
+    const uint32_t sb = sbn;
+    const uint4 L = Ln;
+    if (b + 1 < b_end) {
+      load_codes(b + 1);
+      load_x(b + 1, u);
+    }
     T8 a[4];
     const uint32_t mine = sal_sel(sb, lane & 15);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const uint32_t cws = (k < 2 ? cw.x : cw.y) >> (16 * (k & 1));
+      const uint32_t cws = code_spread((k < 2 ? cw.x : cw.y) >> (16 * (k & 1)));
       uint4 q;
       q.x = decode_pair(cws, 0, L, pair_sel(mine, 4 * k));
       q.y = decode_pair(cws, 1, L, pair_sel(mine, 4 * k + 1));
