@@ -694,7 +694,15 @@ def main():
                     help="only the fc2 input's Hessian product through the library and "
                          "through hipBLASLt (torch.mm) on the same channel-major data, for "
                          "counter runs comparing the two kernels")
+    ap.add_argument("--packed-only", action="store_true",
+                    help="only the packed GEMV / GEMM timing (the 'packed_gemv' object), for "
+                         "counter runs of those kernels")
     args = ap.parse_args()
+    if args.packed_only:
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        print(json.dumps({"packed_gemv": packed_gemv(dev)}))
+        return
     if args.syrk_compare:
         dev = torch.device("cuda:0")
         torch.cuda.set_device(dev)
