@@ -395,8 +395,9 @@ __global__ __launch_bounds__(64 * GV_WAVES) void k_gemv_packed(
 // 8-column MFMA slices) and multiplies them with every 16-token group of
 // the X tile, which the whole workgroup stages in LDS (rows padded to 136
 // halves so a 16-lane group's 16-byte reads of 16 tokens fall on disjoint
-// banks).  The X tile, codes, salient bits and table of the next block are
-// loaded into registers while the current one is used.  When row and token tiles alone would leave CUs idle
+// banks).  The X tile of the next block (with 64-token tiles also its codes,
+// salient bits and table) is loaded into registers while the current one is
+// used.  When row and token tiles alone would leave CUs idle
 // the block range is split over gridDim.z workgroups, each writing an fp32
 // partial [T][R] slice that k_gemm_packed_sum adds in split order.
 constexpr int GM_WAVES = 8;
@@ -444,10 +445,13 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_packed(
   f4_t acc[GM_TT / 16];
 #pragma unroll
   for (int g = 0; g < GM_TT / 16; ++g) acc[g] = f4_t{0.f, 0.f, 0.f, 0.f};
-  // A block's codes, salient bits and table are loaded with its X tile, one
-  // block ahead, so that the decode never waits on them.  Rows past R read
-  // row 0 (crow, lrow): an MFMA output row depends only on its own weight
-  // row, and those rows are not stored.
+  // With 64-token tiles a block's codes, salient bits and table are loaded
+  // with its X tile, one block ahead, so that the decode never waits on
+  // them (rows past R read row 0 through crow and lrow: an MFMA output row
+  // depends only on its own weight row, and those rows are not stored);
+  // 128-token tiles spread each decode over 8 token groups and load them
+  // after the barrier.
+  constexpr bool codes_ahead = GM_TT == 64;
   uint4 u[XPT];
   uint2 cwn = make_uint2(0u, 0u);
   uint32_t sbn = 0u;
@@ -458,7 +462,7 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_packed(
     Ln = lrow[b];
   };
   if (b_beg < b_end) {
-    load_codes(b_beg);
+    if constexpr (codes_ahead) load_codes(b_beg);
     load_x(b_beg, u);
   }
   for (int b = b_beg; b < b_end; ++b) {
@@ -466,12 +470,22 @@ __global__ __launch_bounds__(64 * GM_WAVES) void k_gemm_packed(
 #pragma unroll
     for (int k = 0; k < XPT; ++k) *(uint4*)&Xs[buf][xt][xc + 8 * k] = u[k];
     __syncthreads();
-    const uint2 cw = cwn;
-    const uint32_t sb = sbn;
-    const uint4 L = Ln;
-    if (b + 1 < b_end) {
-      load_codes(b + 1);
-      load_x(b + 1, u);
+    uint2 cw;
+    uint32_t sb;
+    uint4 L;
+    if constexpr (codes_ahead) {
+      cw = cwn;
+      sb = sbn;
+      L = Ln;
+      if (b + 1 < b_end) {
+        load_codes(b + 1);
+        load_x(b + 1, u);
+      }
+    } else {
+      if (b + 1 < b_end) load_x(b + 1, u);
+      cw = row_ok ? *(const uint2*)(crow + b * 32 + kq * 8) : make_uint2(0u, 0u);
+      sb = *(const uint32_t*)(sal + (int64_t)b * 16 + kq * 4);
+      L = row_ok ? lrow[b] : make_uint4(0u, 0u, 0u, 0u);
     }
     T8 a[4];
     const uint32_t mine = sal_sel(sb, lane & 15);
