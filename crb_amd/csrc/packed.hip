@@ -540,15 +540,16 @@ __global__ __launch_bounds__(256) void k_gemm_packed_sum(const float* __restrict
   y[(int64_t)t * ldy + r] = v;
 }
 
-// Split of the block range: about 512 workgroups (two per CU of an
-// MI355X; a function of the shapes only, so the workspace size is known
-// without a device), at least 8 blocks per split.
+// Split of the block range: as many splits as keep the workgroups within
+// 512 (two per CU of an MI355X, one round: a few workgroups past it would
+// run as a second round), at least 8 blocks per split; a function of the
+// shapes only, so the workspace size is known without a device.
 constexpr int GM_TARGET_WG = 512;
 static inline int gemm_packed_splits(int64_t R, int64_t C, int64_t T, int* bps) {
   const int64_t nblk = (C + PB - 1) / PB;
   const int64_t tt = gemm_packed_tt(T);
   const int64_t tiles = ((R + GM_ROWS - 1) / GM_ROWS) * ((T + tt - 1) / tt);
-  int64_t ns = (GM_TARGET_WG + tiles - 1) / tiles;
+  int64_t ns = GM_TARGET_WG / tiles;
   ns = std::max<int64_t>(1, std::min<int64_t>(ns, nblk / 8));
   const int64_t per = (nblk + ns - 1) / ns;
   *bps = (int)per;

@@ -323,11 +323,12 @@ int crbq_gemv_packed(const uint8_t* codes, int64_t ldc, const void* lut,
  * count; meant for prefill batches above the GEMV's 16), X in the weights'
  * dtype (ldx multiple of 8, 16-byte aligned), fp32 Y [ntok][ldy], the
  * exceptions added as in the GEMV.  Each decoded weight fragment is reused
- * for 64 tokens (128 above 64).  When the shapes give fewer than about 512
- * row x token tiles the column blocks are split over workgroups whose fp32
- * partials go to the workspace and are summed in split order
- * (deterministic); crbq_gemm_packed_workspace_size(R, C, ntok) bytes (0
- * when there is no split) depend on the shapes only. */
+ * for 64 tokens (128 above 64).  When the shapes give 256 or fewer row x
+ * token tiles (128 rows each) the column blocks are split over workgroups
+ * (floor(512 / tiles) splits of at least 8 blocks) whose fp32 partials go to
+ * the workspace and are summed in split order (deterministic);
+ * crbq_gemm_packed_workspace_size(R, C, ntok) bytes (0 when there is no
+ * split) depend on the shapes only. */
 size_t crbq_gemm_packed_workspace_size(int64_t R, int64_t C, int64_t ntok);
 int crbq_gemm_packed(const uint8_t* codes, int64_t ldc, const void* lut,
                      const uint8_t* sal, const int64_t* ex_idx, const float* ex_delta,

@@ -143,9 +143,9 @@ def test_gemm_against_float64(R, C, T, dtype):
     scale = x64.abs() @ W64.abs().t()
     err = (y.double().cpu() - ref).abs()
     assert (err <= 1e-5 * scale + 1e-30).all(), float((err / scale.clamp_min(1e-30)).max())
-    # the header's rule: split when ~512 workgroups need it and >= 8 blocks per split
+    # the header's rule: floor(512 / tiles) splits of >= 8 blocks each
     tiles = -(-R // 128) * -(-T // (128 if T > 64 else 64))
-    split = min(-(-512 // tiles), -(-C // 128) // 8) > 1
+    split = min(512 // tiles, -(-C // 128) // 8) > 1
     lib = _lib.load()
     assert (lib.crbq_gemm_packed_workspace_size(R, C, T) > 0) == split
 
